@@ -1,0 +1,140 @@
+/*
+ * nimbus_sampler.h — C ABI of the MI355X (gfx950) token sampler.
+ *
+ * Drop-in boundary for nimbus-infer-rs `src/sampler.rs`: every entry point
+ * below replaces one item of the reference's `nimbus_infer_rs::sampler`
+ * module (exported at src/lib.rs:20) and cites it.  The reference has no FFI
+ * of its own; the Rust binding a maintainer would add (`extern "C"` block +
+ * build.rs running hipcc) is shown in INTEGRATION.md.
+ *
+ * Conventions
+ *   - Plain C types, caller-owned device buffers, no torch/HIP types in the
+ *     signatures (streams travel as `void*` = hipStream_t).
+ *   - Return 0 on success, a negative NIS_E* on an argument error (checked
+ *     on the host before any launch), a positive hipError_t on a runtime
+ *     error.  No C++ exception crosses the ABI.
+ *   - One context = one device + one stream; a context is not thread-safe.
+ *   - Batched calls are asynchronous on the context stream; nis_sync() or
+ *     the caller's own stream synchronisation orders them.
+ */
+#ifndef NIMBUS_SAMPLER_H
+#define NIMBUS_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NIS_ABI_VERSION 1
+
+/* Status codes (negative: argument errors detected before launch). */
+#define NIS_OK 0
+#define NIS_EINVAL (-1)   /* null pointer, B<=0, V<=0, ld<V, reserved != 0 */
+#define NIS_ERANGE (-2)   /* V or B beyond the supported maximum */
+#define NIS_EALIGN (-3)   /* logits pointer not 4-byte aligned */
+#define NIS_ENODEV (-4)   /* no HIP device / bad device ordinal */
+
+/* Largest supported vocabulary (the penalty bitmap lives in LDS). */
+#define NIS_MAX_V (1 << 20)
+#define NIS_MAX_B (1 << 24)
+
+/* Sampling knobs of SamplingParams (sampler.rs:7-15), same f32 types:
+ * temperature (sampler.rs:9; greedy iff <= 0, sampler.rs:32-34), top_k
+ * (sampler.rs:10, usize, 0 disables), top_p (sampler.rs:11, >= 1 disables),
+ * repetition_penalty (sampler.rs:12, 1.0 disables).  `seed`,
+ * `max_new_tokens` and `stop_tokens` belong to the caller's decode loop
+ * (engine.rs:266,271,285) and do not cross this boundary. */
+typedef struct nis_params {
+    float temperature;
+    float top_p;
+    float repetition_penalty;
+    uint32_t reserved; /* must be 0 */
+    uint64_t top_k;
+} nis_params;
+
+/* Which branch of sample() (sampler.rs:163-217) produced a row's token. */
+#define NIS_PATH_GREEDY 1        /* temperature <= 0, sampler.rs:172-181 */
+#define NIS_PATH_NONFINITE_MAX 2 /* filtered max not finite, sampler.rs:192-200 */
+#define NIS_PATH_BAD_TOTAL 3     /* NaN / non-positive total, sampler.rs:206-208 */
+#define NIS_PATH_DRAW 4          /* inverse-CDF draw, sampler.rs:209-214 */
+#define NIS_PATH_FALLTHROUGH 5   /* walk overshoot returns V-1, sampler.rs:216 */
+
+/* Optional per-row diagnostics (pass NULL to skip). */
+typedef struct nis_row_stats {
+    double max_w;   /* max of the filtered, temperature-scaled logits */
+    double z_kept;  /* sum of exp(w - max_w) over kept tokens (`total`, sampler.rs:201-205) */
+    double z_all;   /* same sum before top-p (top-p `sum`, sampler.rs:143); 0 if top-p inactive */
+    double u;       /* next_f64() drawn (sampler.rs:209); -1 when the RNG was not advanced */
+    double prob;    /* exp(w_token - max_w) / z_kept for a drawn token, else 0 */
+    uint64_t kept;  /* tokens surviving top-k / top-p */
+    uint32_t path;  /* NIS_PATH_* */
+    uint32_t token;
+    uint32_t kernel;/* 1 = register-resident fast path, 2 = general path */
+    uint32_t _pad;
+} nis_row_stats;
+
+typedef struct nis_ctx nis_ctx;
+
+/* Create a context on `device` with its own default-priority stream. */
+int nis_ctx_create(int device, nis_ctx** out);
+/* Destroy a context (synchronises its stream first). */
+int nis_ctx_destroy(nis_ctx* ctx);
+/* Launch on a caller stream (hipStream_t as void*, NULL = legacy default
+ * stream) instead of the context's own; the caller keeps ownership. */
+int nis_ctx_set_stream(nis_ctx* ctx, void* stream);
+void* nis_ctx_get_stream(const nis_ctx* ctx);
+/* Message of the last error recorded on `ctx` ("" if none). */
+const char* nis_last_error(const nis_ctx* ctx);
+/* Static text for a status code. */
+const char* nis_status_string(int status);
+
+/* Rng::new (sampler.rs:46-56): SplitMix64-seeded xoshiro256++ state. */
+void nis_rng_seed(uint64_t seed, uint64_t state_out[4]);
+/* Rng::next_u64 (sampler.rs:58-72) on a host-held state. */
+uint64_t nis_rng_next_u64(uint64_t state[4]);
+/* Rng::next_f64 (sampler.rs:75-77) on a host-held state. */
+double nis_rng_next_f64(uint64_t state[4]);
+/* Rng::new for B rows on the device: d_states[4*b..4*b+3] = Rng::new(d_seeds[b]). */
+int nis_rng_seed_batch(nis_ctx* ctx, const uint64_t* d_seeds, int32_t B, uint64_t* d_states);
+
+/* Batched sample() (sampler.rs:163-217) over row-major fp32 logits
+ * [B, ld] in device memory, ld >= V.  Row b uses and advances the
+ * xoshiro256++ state d_rng_state[4*b..4*b+3] exactly as the reference
+ * advances `rng` (one next_u64 iff the row reaches sampler.rs:209).
+ * Repetition penalty (sampler.rs:83-101) reads the CSR list
+ * d_gen_ids[d_gen_offsets[b] .. d_gen_offsets[b+1]) (both may be NULL when
+ * params->repetition_penalty == 1).  Writes d_tokens[b] and, if non-NULL,
+ * d_stats[b].  Asynchronous on the context stream. */
+int nis_sample_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     const nis_params* params, uint64_t* d_rng_state,
+                     const uint32_t* d_gen_ids, const int64_t* d_gen_offsets,
+                     uint32_t* d_tokens, nis_row_stats* d_stats);
+
+/* Batched greedy: first index of the row maximum (sampler.rs:172-181);
+ * same as nis_sample_batch with temperature 0 and no penalty. */
+int nis_argmax_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     uint32_t* d_tokens);
+
+/* apply_repetition_penalty (sampler.rs:83-101) on a device f64 row:
+ * d_logits[id] /= penalty if > 0 else *= penalty, once per distinct id < V. */
+int nis_apply_repetition_penalty(nis_ctx* ctx, double* d_logits, int64_t V,
+                                 const uint32_t* d_generated, int64_t n_generated,
+                                 float penalty);
+
+/* Single-row drop-in for sample(logits, params, generated, rng)
+ * (sampler.rs:163-168): host logits and history are staged to the device
+ * through a context-owned workspace, the HIP sampler runs, and the token and
+ * advanced RNG state come back.  Synchronous. */
+int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_params* params,
+                   const uint32_t* h_generated, int64_t n_generated, uint64_t state_inout[4],
+                   uint32_t* token_out);
+
+/* Wait for all work queued on the context stream. */
+int nis_sync(nis_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NIMBUS_SAMPLER_H */

@@ -1,0 +1,282 @@
+// capi.hip — implementation of the C ABI in include/nimbus_sampler.h.
+//
+// Host-side argument checking happens before any launch; device work is
+// asynchronous on the context stream.  There is no CPU fallback: every
+// sampling entry point launches the gfx950 kernels or returns an error.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "kernels.h"
+#include "nimbus_sampler.h"
+#include "rng.h"
+
+struct nis_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // staging for nis_sample_one
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+namespace {
+
+// Make `dev` current for the duration of a call and restore the caller's.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t status = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        status = hipGetDevice(&prev);
+        if (status == hipSuccess && prev != dev) status = hipSetDevice(dev);
+        else if (status == hipSuccess) prev = -1;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+int fail(nis_ctx* ctx, int code, const char* msg) {
+    if (ctx) ctx->err = msg;
+    return code;
+}
+
+int hip_fail(nis_ctx* ctx, hipError_t e, const char* where) {
+    if (ctx) {
+        ctx->err = where;
+        ctx->err += ": ";
+        ctx->err += hipGetErrorString(e);
+    }
+    return (int)e;
+}
+
+int check_batch_args(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     const nis_params* p, const uint64_t* d_rng, const uint32_t* d_gen_ids,
+                     const int64_t* d_gen_off, const uint32_t* d_tokens) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_logits || !p || !d_tokens) return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (B <= 0) return fail(ctx, NIS_EINVAL, "B must be positive");
+    if (V <= 0) return fail(ctx, NIS_EINVAL, "V must be positive");
+    if (ld < V) return fail(ctx, NIS_EINVAL, "ld must be >= V");
+    if (V > NIS_MAX_V) return fail(ctx, NIS_ERANGE, "V exceeds NIS_MAX_V");
+    if (B > NIS_MAX_B) return fail(ctx, NIS_ERANGE, "B exceeds NIS_MAX_B");
+    if (p->reserved != 0) return fail(ctx, NIS_EINVAL, "nis_params.reserved must be 0");
+    if (((uintptr_t)d_logits & 3u) != 0) return fail(ctx, NIS_EALIGN, "logits not 4-byte aligned");
+    if (!(p->temperature <= 0.0f) && !d_rng)
+        return fail(ctx, NIS_EINVAL, "rng state required unless temperature <= 0");
+    if ((d_gen_ids == nullptr) != (d_gen_off == nullptr))
+        return fail(ctx, NIS_EINVAL, "gen_ids and gen_offsets must both be set or both NULL");
+    return NIS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* nis_status_string(int status) {
+    switch (status) {
+        case NIS_OK: return "ok";
+        case NIS_EINVAL: return "invalid argument";
+        case NIS_ERANGE: return "size out of range";
+        case NIS_EALIGN: return "misaligned pointer";
+        case NIS_ENODEV: return "no such HIP device";
+        default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+    }
+}
+
+int nis_ctx_create(int device, nis_ctx** out) {
+    if (!out) return NIS_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return NIS_ENODEV;
+    nis_ctx* ctx = new (std::nothrow) nis_ctx();
+    if (!ctx) return (int)hipErrorOutOfMemory;
+    ctx->device = device;
+    DeviceGuard g(device);
+    if (g.status != hipSuccess) {
+        delete ctx;
+        return (int)g.status;
+    }
+    hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return (int)e;
+    }
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return NIS_OK;
+}
+
+int nis_ctx_destroy(nis_ctx* ctx) {
+    if (!ctx) return NIS_EINVAL;
+    DeviceGuard g(ctx->device);
+    int rc = NIS_OK;
+    if (ctx->own_stream) {
+        hipError_t e = hipStreamSynchronize(ctx->own_stream);
+        if (e != hipSuccess) rc = (int)e;
+        (void)hipStreamDestroy(ctx->own_stream);
+    }
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    delete ctx;
+    return rc;
+}
+
+int nis_ctx_set_stream(nis_ctx* ctx, void* stream) {
+    if (!ctx) return NIS_EINVAL;
+    ctx->stream = (hipStream_t)stream;
+    return NIS_OK;
+}
+
+void* nis_ctx_get_stream(const nis_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+const char* nis_last_error(const nis_ctx* ctx) { return ctx ? ctx->err.c_str() : ""; }
+
+void nis_rng_seed(uint64_t seed, uint64_t state_out[4]) {
+    if (state_out) nis::rng_seed(seed, state_out);
+}
+
+uint64_t nis_rng_next_u64(uint64_t state[4]) { return state ? nis::rng_next_u64(state) : 0; }
+
+double nis_rng_next_f64(uint64_t state[4]) { return state ? nis::rng_next_f64(state) : 0.0; }
+
+int nis_rng_seed_batch(nis_ctx* ctx, const uint64_t* d_seeds, int32_t B, uint64_t* d_states) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_seeds || !d_states) return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (B <= 0 || B > NIS_MAX_B) return fail(ctx, B <= 0 ? NIS_EINVAL : NIS_ERANGE, "bad B");
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+    const int threads = 256;
+    hipLaunchKernelGGL(nis::rng_seed_kernel, dim3((B + threads - 1) / threads), dim3(threads), 0,
+                       ctx->stream, d_seeds, B, d_states);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "rng_seed_kernel launch");
+}
+
+int nis_sample_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     const nis_params* params, uint64_t* d_rng_state, const uint32_t* d_gen_ids,
+                     const int64_t* d_gen_offsets, uint32_t* d_tokens, nis_row_stats* d_stats) {
+    int rc = check_batch_args(ctx, d_logits, ld, B, V, params, d_rng_state, d_gen_ids,
+                              d_gen_offsets, d_tokens);
+    if (rc != NIS_OK) return rc;
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+    nis::RowArgs a;
+    a.logits = d_logits;
+    a.ld = ld;
+    a.V = V;
+    a.temperature = params->temperature;
+    a.top_p = params->top_p;
+    a.penalty = params->repetition_penalty;
+    a.top_k = params->top_k;
+    a.rng = d_rng_state;
+    a.gen_ids = d_gen_ids;
+    a.gen_off = d_gen_offsets;
+    a.tokens = d_tokens;
+    a.stats = d_stats;
+    hipLaunchKernelGGL(nis::sample_rows_general_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
+                       ctx->stream, a);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "sample kernel launch");
+}
+
+int nis_argmax_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     uint32_t* d_tokens) {
+    nis_params p;
+    p.temperature = 0.0f;
+    p.top_p = 1.0f;
+    p.repetition_penalty = 1.0f;
+    p.reserved = 0;
+    p.top_k = 0;
+    return nis_sample_batch(ctx, d_logits, ld, B, V, &p, nullptr, nullptr, nullptr, d_tokens,
+                            nullptr);
+}
+
+int nis_apply_repetition_penalty(nis_ctx* ctx, double* d_logits, int64_t V,
+                                 const uint32_t* d_generated, int64_t n_generated,
+                                 float penalty) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_logits || (n_generated > 0 && !d_generated))
+        return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (V <= 0 || n_generated < 0) return fail(ctx, NIS_EINVAL, "bad size");
+    if (V > NIS_MAX_V) return fail(ctx, NIS_ERANGE, "V exceeds NIS_MAX_V");
+    if (penalty == 1.0f || n_generated == 0) return NIS_OK;  // sampler.rs:84-86
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+    hipLaunchKernelGGL(nis::repetition_penalty_kernel, dim3(1), dim3(nis::kBlock), 0, ctx->stream,
+                       d_logits, V, d_generated, n_generated, (double)penalty);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "penalty kernel launch");
+}
+
+int nis_sync(nis_ctx* ctx) {
+    if (!ctx) return NIS_EINVAL;
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "hipStreamSynchronize");
+}
+
+int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_params* params,
+                   const uint32_t* h_generated, int64_t n_generated, uint64_t state_inout[4],
+                   uint32_t* token_out) {
+    if (!ctx) return NIS_EINVAL;
+    if (!h_logits || !params || !state_inout || !token_out || (n_generated > 0 && !h_generated))
+        return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (V <= 0 || n_generated < 0) return fail(ctx, NIS_EINVAL, "bad size");
+    if (V > NIS_MAX_V) return fail(ctx, NIS_ERANGE, "V exceeds NIS_MAX_V");
+    if (params->reserved != 0) return fail(ctx, NIS_EINVAL, "nis_params.reserved must be 0");
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+
+    const bool use_gen = params->repetition_penalty != 1.0f && n_generated > 0;
+    auto align = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t off_state = 0;
+    const size_t off_tok = align(off_state + 32);
+    const size_t off_goff = align(off_tok + 4);
+    const size_t off_gen = align(off_goff + 16);
+    const size_t off_logits = align(off_gen + (use_gen ? (size_t)n_generated * 4 : 0));
+    const size_t need = align(off_logits + (size_t)V * 4);
+    if (need > ctx->ws_bytes) {
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+        hipError_t e = hipMalloc(&ctx->ws, need);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc workspace");
+        ctx->ws_bytes = need;
+    }
+    char* ws = (char*)ctx->ws;
+    uint64_t* d_state = (uint64_t*)(ws + off_state);
+    uint32_t* d_tok = (uint32_t*)(ws + off_tok);
+    int64_t* d_goff = (int64_t*)(ws + off_goff);
+    uint32_t* d_gen = (uint32_t*)(ws + off_gen);
+    float* d_logits = (float*)(ws + off_logits);
+    hipStream_t s = ctx->stream;
+    hipError_t e;
+#define NIS_TRY(call, what)                           \
+    do {                                              \
+        e = (call);                                   \
+        if (e != hipSuccess) return hip_fail(ctx, e, what); \
+    } while (0)
+    NIS_TRY(hipMemcpyAsync(d_logits, h_logits, (size_t)V * 4, hipMemcpyHostToDevice, s), "H2D logits");
+    NIS_TRY(hipMemcpyAsync(d_state, state_inout, 32, hipMemcpyHostToDevice, s), "H2D rng");
+    if (use_gen) {
+        const int64_t offs[2] = {0, n_generated};
+        NIS_TRY(hipMemcpyAsync(d_gen, h_generated, (size_t)n_generated * 4, hipMemcpyHostToDevice, s),
+                "H2D generated");
+        NIS_TRY(hipMemcpyAsync(d_goff, offs, 16, hipMemcpyHostToDevice, s), "H2D offsets");
+        NIS_TRY(hipStreamSynchronize(s), "sync staging");  // `offs` is stack memory
+    }
+    int rc = nis_sample_batch(ctx, d_logits, V, 1, V, params, d_state, use_gen ? d_gen : nullptr,
+                              use_gen ? d_goff : nullptr, d_tok, nullptr);
+    if (rc != NIS_OK) return rc;
+    NIS_TRY(hipMemcpyAsync(token_out, d_tok, 4, hipMemcpyDeviceToHost, s), "D2H token");
+    NIS_TRY(hipMemcpyAsync(state_inout, d_state, 32, hipMemcpyDeviceToHost, s), "D2H rng");
+    NIS_TRY(hipStreamSynchronize(s), "sync");
+#undef NIS_TRY
+    return NIS_OK;
+}
+
+}  // extern "C"

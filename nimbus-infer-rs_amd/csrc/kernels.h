@@ -1,0 +1,52 @@
+// kernels.h — __global__ entry points of the sampler library (gfx950).
+#pragma once
+#include "general_path.h"
+
+namespace nis {
+
+// One workgroup per row.
+__global__ __launch_bounds__(kBlock) void sample_rows_general_kernel(RowArgs a) {
+    __shared__ GeneralShared sh;
+    general_row(a, (int)blockIdx.x, sh);
+}
+
+// Rng::new per row (sampler.rs:46-56).
+__global__ void rng_seed_kernel(const uint64_t* __restrict__ seeds, int32_t B,
+                                uint64_t* __restrict__ states) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    uint64_t s[4];
+    rng_seed(seeds[b], s);
+    states[4 * b + 0] = s[0];
+    states[4 * b + 1] = s[1];
+    states[4 * b + 2] = s[2];
+    states[4 * b + 3] = s[3];
+}
+
+// apply_repetition_penalty (sampler.rs:83-101) on one f64 row: the distinct
+// ids are collected in an LDS bitmap, then each is penalised once.
+__global__ __launch_bounds__(kBlock) void repetition_penalty_kernel(
+    double* __restrict__ logits, int64_t V, const uint32_t* __restrict__ gen, int64_t n_gen,
+    double penalty) {
+    __shared__ uint32_t bitmap[NIS_MAX_V / 32];
+    const int64_t nw = (V + 31) >> 5;
+    for (int64_t i = threadIdx.x; i < nw; i += kBlock) bitmap[i] = 0u;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < n_gen; i += kBlock) {
+        const uint32_t id = gen[i];
+        if ((int64_t)id < V) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+    for (int64_t w = threadIdx.x; w < nw; w += kBlock) {
+        uint32_t bits = bitmap[w];
+        while (bits) {
+            const int b = __ffs(bits) - 1;
+            bits &= bits - 1;
+            const int64_t j = w * 32 + b;
+            const double v = logits[j];
+            logits[j] = (v > 0.0) ? v / penalty : v * penalty;
+        }
+    }
+}
+
+}  // namespace nis

@@ -1,0 +1,279 @@
+"""Python binding of the MI355X sampler C ABI (include/nimbus_sampler.h).
+
+Mirrors the reference's `nimbus_infer_rs::sampler` module (src/sampler.rs):
+`SamplingParams`, `Rng`, `sample()`, plus the batched device entry point
+`Sampler.sample_batch()` over [B, V] fp32 logits already resident in HBM.
+PyTorch is used only for device memory and the current HIP stream.
+
+There is no CPU fallback: if the HIP library is missing or fails to load,
+every entry point raises.
+"""
+import ctypes
+import dataclasses
+import os
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(ROOT_DIR, "lib", "libnimbus_sampler.so")
+
+NIS_OK, NIS_EINVAL, NIS_ERANGE, NIS_EALIGN, NIS_ENODEV = 0, -1, -2, -3, -4
+NIS_MAX_V = 1 << 20
+PATH_GREEDY, PATH_NONFINITE_MAX, PATH_BAD_TOTAL, PATH_DRAW, PATH_FALLTHROUGH = 1, 2, 3, 4, 5
+
+# nis_row_stats
+ROW_STATS_DTYPE = np.dtype([
+    ("max_w", "<f8"), ("z_kept", "<f8"), ("z_all", "<f8"), ("u", "<f8"), ("prob", "<f8"),
+    ("kept", "<u8"), ("path", "<u4"), ("token", "<u4"), ("kernel", "<u4"), ("_pad", "<u4"),
+])
+assert ROW_STATS_DTYPE.itemsize == 64
+
+EXPORTED_SYMBOLS = (
+    "nis_ctx_create", "nis_ctx_destroy", "nis_ctx_set_stream", "nis_ctx_get_stream",
+    "nis_last_error", "nis_status_string", "nis_rng_seed", "nis_rng_next_u64",
+    "nis_rng_next_f64", "nis_rng_seed_batch", "nis_sample_batch", "nis_argmax_batch",
+    "nis_apply_repetition_penalty", "nis_sample_one", "nis_sync",
+)
+
+
+class NisParams(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float),
+                ("repetition_penalty", ctypes.c_float), ("reserved", ctypes.c_uint32),
+                ("top_k", ctypes.c_uint64)]
+
+
+class SamplerError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"nimbus sampler error {status}: {message}")
+        self.status = status
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libnimbus_sampler.so (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise SamplerError(NIS_EINVAL, f"{path} not built (run __graft_entry__.build())")
+    # torch bundles its own libamdhip64.so.7 (same SONAME as /opt/rocm's).
+    # Initialise torch's HIP runtime first so the library binds to that one
+    # copy: device pointers and streams are then shared with torch tensors.
+    try:
+        import torch
+        if torch.cuda.is_available():
+            torch.cuda.init()
+    except ImportError:
+        pass
+    L = ctypes.CDLL(path)
+    vp, u64p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64)
+    L.nis_ctx_create.argtypes = [ctypes.c_int, ctypes.POINTER(vp)]
+    L.nis_ctx_destroy.argtypes = [vp]
+    L.nis_ctx_set_stream.argtypes = [vp, vp]
+    L.nis_ctx_get_stream.argtypes = [vp]
+    L.nis_ctx_get_stream.restype = vp
+    L.nis_last_error.argtypes = [vp]
+    L.nis_last_error.restype = ctypes.c_char_p
+    L.nis_status_string.argtypes = [ctypes.c_int]
+    L.nis_status_string.restype = ctypes.c_char_p
+    L.nis_rng_seed.argtypes = [ctypes.c_uint64, u64p]
+    L.nis_rng_next_u64.argtypes = [u64p]
+    L.nis_rng_next_u64.restype = ctypes.c_uint64
+    L.nis_rng_next_f64.argtypes = [u64p]
+    L.nis_rng_next_f64.restype = ctypes.c_double
+    L.nis_rng_seed_batch.argtypes = [vp, vp, ctypes.c_int32, vp]
+    L.nis_sample_batch.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                                   ctypes.POINTER(NisParams), vp, vp, vp, vp, vp]
+    L.nis_argmax_batch.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64, vp]
+    L.nis_apply_repetition_penalty.argtypes = [vp, vp, ctypes.c_int64, vp, ctypes.c_int64,
+                                               ctypes.c_float]
+    L.nis_sample_one.argtypes = [vp, vp, ctypes.c_int64, ctypes.POINTER(NisParams), vp,
+                                 ctypes.c_int64, u64p, ctypes.POINTER(ctypes.c_uint32)]
+    L.nis_sync.argtypes = [vp]
+    for name in ("nis_ctx_create", "nis_ctx_destroy", "nis_ctx_set_stream", "nis_rng_seed_batch",
+                 "nis_sample_batch", "nis_argmax_batch", "nis_apply_repetition_penalty",
+                 "nis_sample_one", "nis_sync"):
+        getattr(L, name).restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+# ---------------------------------------------------------------------------
+# Reference API mirror (src/sampler.rs)
+
+@dataclasses.dataclass
+class SamplingParams:
+    """SamplingParams (sampler.rs:6-35) with the reference defaults."""
+    max_new_tokens: int = 64
+    temperature: float = 1.0
+    top_k: int = 0
+    top_p: float = 1.0
+    repetition_penalty: float = 1.0
+    seed: Optional[int] = None
+    stop_tokens: List[int] = dataclasses.field(default_factory=list)
+
+    def greedy(self) -> bool:
+        return np.float32(self.temperature) <= 0.0
+
+    def to_c(self) -> NisParams:
+        return NisParams(float(np.float32(self.temperature)), float(np.float32(self.top_p)),
+                         float(np.float32(self.repetition_penalty)), 0, int(self.top_k))
+
+
+class Rng:
+    """Rng (sampler.rs:40-78): xoshiro256++ seeded by SplitMix64, host-held
+    32-byte state that crosses the ABI as four u64 words."""
+
+    def __init__(self, seed: int):
+        self._s = (ctypes.c_uint64 * 4)()
+        load_library().nis_rng_seed(ctypes.c_uint64(int(seed) & (2**64 - 1)), self._s)
+
+    @classmethod
+    def from_state(cls, words: Sequence[int]) -> "Rng":
+        r = cls.__new__(cls)
+        r._s = (ctypes.c_uint64 * 4)(*[int(w) & (2**64 - 1) for w in words])
+        return r
+
+    def state(self) -> List[int]:
+        return [int(v) for v in self._s]
+
+    def next_u64(self) -> int:
+        return int(load_library().nis_rng_next_u64(self._s))
+
+    def next_f64(self) -> float:
+        return float(load_library().nis_rng_next_f64(self._s))
+
+
+def rng_states(seeds: Sequence[int]) -> np.ndarray:
+    """[B,4] uint64 host array of Rng::new(seed) states."""
+    out = np.zeros((len(seeds), 4), dtype=np.uint64)
+    for i, s in enumerate(seeds):
+        out[i] = Rng(int(s)).state()
+    return out
+
+
+def _check(L, ctx, rc):
+    if rc != NIS_OK:
+        msg = L.nis_last_error(ctx) if ctx else None
+        msg = msg.decode() if msg else L.nis_status_string(rc).decode()
+        raise SamplerError(rc, msg)
+
+
+class Sampler:
+    """A sampler context (one device, launches on torch's current stream)."""
+
+    def __init__(self, device: int = 0):
+        L = load_library()
+        self._L = L
+        self._ctx = ctypes.c_void_p()
+        _check(L, None, L.nis_ctx_create(int(device), ctypes.byref(self._ctx)))
+        self.device = device
+
+    def close(self):
+        if self._ctx:
+            self._L.nis_ctx_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._ctx
+
+    def _bind_stream(self):
+        import torch
+        self._L.nis_ctx_set_stream(self._ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+    def sample_batch(self, logits, params: SamplingParams, rng_states, V: Optional[int] = None,
+                     gen_ids=None, gen_offsets=None, tokens=None, stats=None):
+        """Batched sample() on device tensors.
+
+        logits: float32 [B, ld] (row stride ld >= V, unit column stride);
+        rng_states: int64 [B, 4] holding the u64 words, advanced in place;
+        gen_ids: int32 [n] / gen_offsets: int64 [B+1] CSR history (optional);
+        tokens: optional int32 [B] output; stats: optional uint8 [B, 64].
+        Returns the tokens tensor.  Asynchronous on torch's current stream."""
+        import torch
+        assert logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1
+        B = logits.shape[0]
+        V = logits.shape[1] if V is None else V
+        if tokens is None:
+            tokens = torch.empty(B, dtype=torch.int32, device=logits.device)
+        self._bind_stream()
+        p = params.to_c() if isinstance(params, SamplingParams) else params
+        rc = self._L.nis_sample_batch(
+            self._ctx, ctypes.c_void_p(logits.data_ptr()), logits.stride(0), B, V, ctypes.byref(p),
+            ctypes.c_void_p(rng_states.data_ptr()) if rng_states is not None else None,
+            ctypes.c_void_p(gen_ids.data_ptr()) if gen_ids is not None else None,
+            ctypes.c_void_p(gen_offsets.data_ptr()) if gen_offsets is not None else None,
+            ctypes.c_void_p(tokens.data_ptr()),
+            ctypes.c_void_p(stats.data_ptr()) if stats is not None else None)
+        _check(self._L, self._ctx, rc)
+        return tokens
+
+    def argmax_batch(self, logits, V: Optional[int] = None, tokens=None):
+        import torch
+        B = logits.shape[0]
+        V = logits.shape[1] if V is None else V
+        if tokens is None:
+            tokens = torch.empty(B, dtype=torch.int32, device=logits.device)
+        self._bind_stream()
+        rc = self._L.nis_argmax_batch(self._ctx, ctypes.c_void_p(logits.data_ptr()),
+                                      logits.stride(0), B, V, ctypes.c_void_p(tokens.data_ptr()))
+        _check(self._L, self._ctx, rc)
+        return tokens
+
+    def rng_seed_batch(self, seeds, states):
+        self._bind_stream()
+        rc = self._L.nis_rng_seed_batch(self._ctx, ctypes.c_void_p(seeds.data_ptr()),
+                                        seeds.numel(), ctypes.c_void_p(states.data_ptr()))
+        _check(self._L, self._ctx, rc)
+        return states
+
+    def apply_repetition_penalty(self, logits_f64, generated, penalty: float):
+        self._bind_stream()
+        rc = self._L.nis_apply_repetition_penalty(
+            self._ctx, ctypes.c_void_p(logits_f64.data_ptr()), logits_f64.numel(),
+            ctypes.c_void_p(generated.data_ptr()) if generated.numel() else None,
+            generated.numel(), ctypes.c_float(penalty))
+        _check(self._L, self._ctx, rc)
+        return logits_f64
+
+    def sample_one(self, logits, params: SamplingParams, generated: Sequence[int], rng: Rng) -> int:
+        """Host-buffer drop-in of sample(&logits, params, &generated, &mut rng)."""
+        x = np.ascontiguousarray(logits, dtype=np.float32)
+        g = np.ascontiguousarray(generated, dtype=np.uint32)
+        tok = ctypes.c_uint32()
+        p = params.to_c()
+        rc = self._L.nis_sample_one(self._ctx, ctypes.c_void_p(x.ctypes.data), x.size,
+                                    ctypes.byref(p), ctypes.c_void_p(g.ctypes.data) if g.size else None,
+                                    g.size, rng._s, ctypes.byref(tok))
+        _check(self._L, self._ctx, rc)
+        return int(tok.value)
+
+    def sync(self):
+        _check(self._L, self._ctx, self._L.nis_sync(self._ctx))
+
+
+_default_sampler: Optional[Sampler] = None
+
+
+def sample(logits, params: SamplingParams, generated: Sequence[int], rng: Rng) -> int:
+    """sample(logits, params, generated, rng) -> u32 (sampler.rs:163-168), on the GPU."""
+    global _default_sampler
+    if _default_sampler is None:
+        _default_sampler = Sampler(int(os.environ.get("NIMBUS_DEVICE", "0")))
+    return _default_sampler.sample_one(logits, params, generated, rng)
+
+
+def stats_view(stats_u8) -> np.ndarray:
+    """Host structured view of a uint8 [B, 64] stats tensor."""
+    return np.ascontiguousarray(stats_u8.cpu().numpy()).view(ROW_STATS_DTYPE).reshape(-1)
