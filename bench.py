@@ -1,0 +1,208 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X sampler on the headline workload.
+
+Metric: sampled rows/s + HBM GB/s (% of peak) for
+B=256 x V=50257 fp32 logits, T=0.8, top-p=0.9.  A step is one
+nis_sample_batch() launch over one [256, 50257] batch that is already
+resident in HBM.  Eight distinct input batches (412 MB) are rotated so
+reads cannot be served from the 256 MB Infinity Cache.
+
+JSON line fields beyond the driver contract:
+  roofline      dominant kernel: algorithmic bytes per launch
+                B*(4V + 68) (logits once, token, 32 B RNG state in + out)
+                over its mean launch duration: HIP events bracketing the
+                timed hipGraph replays on the launch stream, divided by the
+                number of launches; traffic from the committed rocprofv3
+                --pmc summary when present.
+  cpu_baseline  the CPU oracle (a C restatement of sampler.rs) over the
+                same 256 rows with the threads.rs fork-join, median of 5
+                batches after one warm-up.
+  parity        first timed batch vs the oracle (greedy and sampled).
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nimbus-infer-rs_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "sampled rows/s + HBM GB/s (% peak), B=256 x V=50257 fp32, T=0.8 top-p=0.9"
+KERNEL_NAME = "sample_rows"
+
+
+def read_traffic(workload):
+    """HBM bytes per launch from profiles/*traffic*<workload>*.txt, if measured."""
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
+        return None
+    for fn in sorted(os.listdir(pdir)):
+        if "traffic" in fn and workload in fn and fn.endswith(".txt"):
+            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(os.path.join(pdir, fn)).read(), re.M)
+            if m:
+                return float(m.group(1))
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="headline")
+    ap.add_argument("--buffers", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="oracle worker threads (0: NIMBUS_THREADS, else min(16, cores))")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this sampler build runs on one GPU only (rows are independent; "
+              "row sharding across GPUs is described in DESIGN.md). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import nimbus_sampler as ns
+    from nimbus_sampler import workloads
+
+    w = workloads.WORKLOADS[args.workload]
+    B, V = w.B, w.V
+    dev = torch.device("cuda:0")
+    sampler = ns.Sampler(0)
+    params = ns.SamplingParams(temperature=w.temperature, top_p=w.top_p)
+
+    host0 = w.make(B)
+    bufs = [torch.from_numpy(host0).to(dev)]
+    for i in range(1, args.buffers):
+        # distinct batches of the same distribution: permute rows and roll columns
+        bufs.append(torch.roll(bufs[0][torch.randperm(B, generator=torch.Generator().manual_seed(i))],
+                               shifts=997 * i, dims=1).contiguous())
+    states = torch.from_numpy(ns.rng_states(w.seeds).view(np.int64)).to(dev)
+    tokens = torch.empty(B, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+
+    # parity of one batch against the oracle (state copy so the timed run is unaffected)
+    parity = None
+    try:
+        from oracle import oracle
+    except Exception:
+        oracle = None
+    if oracle is not None:
+        st_copy = states.clone()
+        stats = torch.zeros((B, 64), dtype=torch.uint8, device=dev)
+        sampler.sample_batch(bufs[0], params, st_copy, tokens=tokens, stats=stats)
+        g = sampler.argmax_batch(bufs[0])
+        torch.cuda.synchronize()
+        ref_states = oracle.rng_states(w.seeds)
+        rt, rs, _ = oracle.sample_batch(host0, V, oracle.make_params(w.temperature, w.top_p), ref_states)
+        gt, _, _ = oracle.sample_batch(host0, V, oracle.make_params(0.0), oracle.rng_states(w.seeds))
+        got = tokens.cpu().numpy().astype(np.uint32)
+        boundary = (rs["topp_margin"] <= 1e-6) | (rs["cdf_margin"] <= 1e-6)
+        parity = {
+            "greedy_mismatch": int((g.cpu().numpy().astype(np.uint32) != gt).sum()),
+            "sampled_mismatch_outside_boundary": int(((got != rt) & ~boundary).sum()),
+            "boundary_rows": int(boundary.sum()),
+            "rng_state_match": bool(np.array_equal(st_copy.cpu().numpy().view(np.uint64), ref_states)),
+        }
+
+    for i in range(args.warmup):
+        sampler.sample_batch(bufs[i % len(bufs)], params, states, tokens=tokens)
+    torch.cuda.synchronize()
+
+    # Timed region: hipGraph replays of one launch per rotated buffer, so the
+    # GPU is not waiting on Python between launches.  HIP events bracket the
+    # whole region on the stream the launches run on; the mean launch
+    # duration is their elapsed time over the number of launches.
+    G = len(bufs)
+    K = max(G, (args.steps // G) * G)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(G):
+                sampler.sample_batch(bufs[i], params, states, tokens=tokens)
+    torch.cuda.current_stream().wait_stream(cap)
+    for _ in range(2):  # warm replays
+        graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(K // G):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    mean_ms = e0.elapsed_time(e1) / K
+
+    # eager rate through the Python binding (one ctypes call per batch), for reference
+    torch.cuda.synchronize()
+    te0 = time.perf_counter()
+    for i in range(min(K, 64)):
+        sampler.sample_batch(bufs[i % G], params, states, tokens=tokens)
+    torch.cuda.synchronize()
+    eager_rows_s = B * min(K, 64) / (time.perf_counter() - te0)
+
+    alg_bytes = B * (4 * V + 68)
+    achieved = alg_bytes / (mean_ms * 1e-3) / 1e9
+    traffic = read_traffic(args.workload)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle
+        nthreads = args.cpu_threads or int(os.environ.get("NIMBUS_THREADS", "0") or 0) or \
+            min(16, os.cpu_count() or 1)
+        p = oracle.make_params(w.temperature, w.top_p)
+        times = []
+        for rep in range(6):
+            st = oracle.rng_states(w.seeds)
+            c0 = time.perf_counter()
+            _, _, used = oracle.sample_batch(host0, V, p, st, n_threads=nthreads)
+            times.append(time.perf_counter() - c0)
+        times = sorted(times[1:])
+        med = times[len(times) // 2]
+        cpu = {"value": B / med, "unit": "rows/s", "cores": used, "kind": "port",
+               "sample": f"C restatement of sampler.rs over the same {B}x{V} batch, "
+                         f"threads.rs fork-join on {used} threads, median of 5 batches after 1 warm-up",
+               "gbs": alg_bytes / med / 1e9}
+
+    out = {
+        "metric": METRIC,
+        "value": B * K / wall,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / K,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: N(0,3^2) logits from PCG64 seed 7, 8 rotated batches resident in HBM",
+        "config": {"workload": args.workload, "B": B, "V": V, "temperature": w.temperature,
+                   "top_p": w.top_p, "ld": V, "parallelism": "1 GPU",
+                   "launch": f"hipGraph replay of {G} nis_sample_batch launches",
+                   "eager_rows_per_s": eager_rows_s},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": KERNEL_NAME, "kernel_mean_us": mean_ms * 1e3,
+                     "alg_bytes_per_launch": alg_bytes},
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(out))
+    sampler.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -72,8 +72,17 @@ typedef struct nis_row_stats {
     uint32_t path;  /* NIS_PATH_* */
     uint32_t token;
     uint32_t kernel;/* 1 = register-resident fast path, 2 = general path */
-    uint32_t _pad;
+    uint32_t reject;/* NIS_REJECT_*: why the fast path handed the row on (0 if it did not) */
 } nis_row_stats;
+
+/* nis_row_stats.reject: the fast path declines a row it cannot prove exact
+ * and the general path recomputes it; the result is the same either way. */
+#define NIS_REJECT_NONE 0
+#define NIS_REJECT_SHAPE 1      /* V out of range, per-row penalty, top-k, top-p <= 0 */
+#define NIS_REJECT_NONFINITE 2  /* NaN / inf / empty row or exponent range */
+#define NIS_REJECT_WINDOW 3     /* the estimated cutoff window missed the cutoff */
+#define NIS_REJECT_CAPACITY 4   /* candidate list or cutoff bucket over capacity */
+#define NIS_REJECT_BUCKET 5     /* cutoff bucket membership did not match its histogram */
 
 typedef struct nis_ctx nis_ctx;
 

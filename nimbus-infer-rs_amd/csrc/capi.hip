@@ -177,7 +177,7 @@ int nis_sample_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B,
     a.gen_off = d_gen_offsets;
     a.tokens = d_tokens;
     a.stats = d_stats;
-    hipLaunchKernelGGL(nis::sample_rows_general_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
+    hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
                        ctx->stream, a);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "sample kernel launch");

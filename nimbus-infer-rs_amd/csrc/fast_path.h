@@ -1,0 +1,1212 @@
+// fast_path.h — register-resident sampler for one row per 512-lane
+// workgroup (V <= 53245), the hot path of nis_sample_batch.
+//
+// HBM is touched once: every lane issues its 26 nontemporal 16-byte loads up
+// front (wave-contiguous layout: wave w owns float4 slots
+// [w*26*64, (w+1)*26*64), chunk k / lane l holds slot w*1664 + 64k + l), and
+// the row then lives in VGPRs (104 logits per lane; 8 waves per workgroup
+// leave each wave up to 256 VGPRs).  While the loads stream in, each wave
+// adds the masses e = 2^(x*c - R_w) of its elements to Z (c = log2(e)/T,
+// R_w a reference from the wave's own first chunk, so no workgroup barrier
+// is needed until the stream ends) and keeps the maximum of every float4.
+//
+// The top-p cutoff of src/sampler.rs:118-160 is then found without sorting
+// the row.  The reference keeps sorted position pos iff
+// cum_excl(pos) - q(pos) <= p; that quantity is non-decreasing in pos, so
+// the kept set is a prefix of the sorted order and one threshold suffices:
+//
+// Sparse route (few kept tokens, the common case):
+//   1. a count histogram of a 4096-element sample (1/64-octave bins) gives a
+//      threshold x_lo with an estimated mass below it of at most
+//      (1 - p) * Z / 2; every float4 holding an element >= x_lo is appended to
+//      its wave's list (in index order) and compacted to single candidates;
+//   2. x_lo is proven safe: the largest element below it is removed iff
+//      G(candidates) - e(x_lo) > p * Z;
+//   3. a 1024-bucket histogram of the candidates (count, fixed-point mass,
+//      largest key) locates the bucket holding the cutoff: the lowest bucket
+//      whose largest element is kept; its members are ranked exactly;
+//   4. the inverse-CDF walk (sampler.rs:209-216) runs over the index-ordered
+//      candidate lists.
+// Dense route (most tokens kept, or top-p off): a value window around the
+// cutoff from the same sample, one register pass that adds the mass above
+// the window into per-(wave, chunk, lane) cells and lists the window
+// elements, a fine histogram of the window, an exact pass over the cutoff
+// bucket, and a walk waves -> chunks -> lanes -> elements.
+//
+// Every step that cannot prove its result (non-finite input, reference
+// overflow, a threshold or window that misses the cutoff, list or bucket
+// overflow) hands the row to the general path, which recomputes it from HBM.
+#pragma once
+#include "general_path.h"
+
+namespace nis {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+// global-address-space views, so loads are global_load with an SGPR base
+typedef const __attribute__((address_space(1))) f4v* gf4p;
+typedef const __attribute__((address_space(1))) float* gfp;
+
+constexpr int kNch = 26;                      // float4 chunks per lane
+constexpr int kWaveSlots = kNch * 64;         // float4 slots per wave
+constexpr int kFastMaxV = kBlock * 4 * kNch - 3;
+constexpr int kSampleBins = 2048;             // 32 octaves at 1/64 octave
+constexpr float kSampleRes = 64.0f;
+constexpr int kFineBins = 1024;
+constexpr int kMaxFinal = 64;
+constexpr int kLaneCap = 16;                  // dense route: window entries per lane
+constexpr float kMaxT = 60.0f;                // overflow guard for 2^(x*c - R)
+constexpr double kFix = 1099511627776.0;      // 2^40 fixed-point mass scale
+constexpr uint8_t kKeptBit = 0x80;
+// sparse route
+constexpr int kWaveEnt = 384;                 // listed float4s per wave
+constexpr int kWaveCand = 512;                // candidates per wave
+constexpr double kSpBeta = 0.5;               // sampled mass below x_lo <= beta * (1-p) * Z
+constexpr double kSpGamma = 0.25;             // e(x_lo) <= gamma * (1-p) * Z
+constexpr double kSpEstCap = 2800.0;          // estimated candidates per row
+
+struct DenseShared {
+    float cell[kWaves][kNch][64];    // kept mass of each lane's 4 elements per chunk
+    float lx[kLaneCap][kBlock];      // lane-private window lists: logit
+    uint8_t lp[kLaneCap][kBlock];    //   position 4k+q in the lane, | kKeptBit when kept
+    f4v stx[kNch][64];               // the chosen wave's logits, staged for the final lane
+    uint32_t cj[kMaxFinal];          // members of the cutoff bucket: row index
+    float cx[kMaxFinal];             //   logit
+    uint32_t cloc[kMaxFinal];        //   owner thread * kLaneCap + list slot
+};
+struct SparseShared {
+    f4v ent_x[kWaves][kWaveEnt];         // listed float4s, wave-compacted in index order
+    uint16_t ent_pos[kWaves][kWaveEnt];  //   their chunk * 64 + lane
+    float cx[kWaves][kWaveCand];         // candidates (x >= x_lo) in index order: logit
+    uint32_t ci[kWaves][kWaveCand];      //   row index
+    float ce[kWaves][kWaveCand];         //   mass 2^(x*c - R)
+    double gab[kFineBins];               // candidate mass above each fine bucket
+    float gx[kMaxFinal];                 // members of the cutoff bucket
+    uint32_t gi[kMaxFinal];
+    float ge[kMaxFinal];
+};
+
+struct FastShared {
+    uint32_t scnt[kSampleBins];
+    uint32_t fcnt[kFineBins];
+    unsigned long long fmass[kFineBins];
+    uint32_t fkmax[kFineBins];
+    uint32_t fkmin[kFineBins];
+    union {
+        DenseShared d;
+        SparseShared s;
+    };
+    uint64_t rng[4];                 // the row's RNG state after its one draw
+    uint32_t ncand;
+    uint32_t overflow;
+    uint32_t gcount;
+    uint32_t cut_key;
+    uint32_t cut_idx;
+    float fa[kWaves];
+    float fb[kWaves];
+    float fc[kWaves];
+    double da[kWaves];
+    double db[kWaves];
+    int32_t ia[kWaves];
+    uint32_t ua[kWaves];
+    uint32_t ub[kWaves];
+    double wtot[kWaves];
+    double ctot[kNch];
+    float bf[8];
+    double bd[8];
+    int32_t bi[8];
+};
+
+// Optional per-phase timestamps of each workgroup's wave 0 (profiling
+// builds only; compiled out unless NIS_PHASE_TIMING is defined).
+#ifdef NIS_PHASE_TIMING
+__device__ unsigned long long nis_phase_ts[8192 * 16];
+#define NIS_TS(i)                                                                   \
+    do {                                                                            \
+        if (threadIdx.x == 0) nis_phase_ts[blockIdx.x * 16 + (i)] = wall_clock64(); \
+    } while (0)
+#else
+#define NIS_TS(i) \
+    do {          \
+    } while (0)
+#endif
+
+// Workgroup barrier that orders LDS only, so global loads still in flight
+// are not drained by it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// Orders one wave's LDS writes before its own later LDS reads of other lanes.
+__device__ __forceinline__ void lds_wave_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Mass of sample bin b (t in (-(b+1)/64, -b/64]) at its centre, for the
+// threshold estimates only.
+__device__ __forceinline__ float bin_mass(int b) {
+    return __builtin_amdgcn_exp2f(-((float)b + 0.5f) * (1.0f / kSampleRes));
+}
+
+__device__ __forceinline__ float elem(const f4v& v, int q) {
+    return q == 0 ? v.x : (q == 1 ? v.y : (q == 2 ? v.z : v.w));
+}
+__device__ __forceinline__ uint32_t elemu(const u4v& v, int q) {
+    return q == 0 ? v.x : (q == 1 ? v.y : (q == 2 ? v.z : v.w));
+}
+__device__ __forceinline__ float max4(const f4v& v) {
+    return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+}
+
+// Mass of a logit relative to the reference R, in the one form used
+// everywhere on this path so that equal logits get bit-equal masses.
+__device__ __forceinline__ float mass_of(float x, float c, float R) {
+    return __builtin_amdgcn_exp2f(fmaf(x, c, -R));
+}
+
+// Fine-histogram bucket of an element in [x_lo, x_top] (monotone in x).
+__device__ __forceinline__ int fine_bucket(float x, float x_lo, float inv_w) {
+    return min(max((int)((x - x_lo) * inv_w), 0), kFineBins - 1);
+}
+
+// Value of a float4 slot that is not fully inside the row: the few head /
+// tail elements come from scalar loads, everything outside the row is -inf.
+__device__ __forceinline__ f4v fix_slot(f4v v, int f, int f_lo, int f_hi, int mis, int V, float h0,
+                                        float h1, float h2, float t0, float t1, float t2) {
+    if (f >= f_lo && f <= f_hi) return v;
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int j = 4 * f + q - mis;
+        float y = -INFINITY;
+        if (j >= 0 && j < V) {
+            if (j < 3) y = (j == 0) ? h0 : (j == 1 ? h1 : h2);
+            else y = (j == V - 3) ? t0 : (j == V - 2 ? t1 : t2);
+        }
+        o[q] = y;
+    }
+    return f4v{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ bool fast_eligible(const RowArgs a, int row) {
+    if (a.V < 256 || a.V > kFastMaxV) return false;
+    if (a.penalty != 1.0f && a.gen_ids != nullptr && a.gen_off != nullptr &&
+        a.gen_off[row + 1] > a.gen_off[row])
+        return false;
+    if (a.temperature <= 0.0f) return true;
+    if (a.top_k > 0 && a.top_k < (uint64_t)a.V) return false;
+    if (a.top_p <= 0.0f) return false;
+    return true;
+}
+
+// Returns NIS_REJECT_NONE when the row is done, else (uniformly across the
+// workgroup) why it must be recomputed by the general path; nothing has been
+// written then.
+__device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, FastShared& sh) {
+    const int tid = threadIdx.x, l = lane_id();
+    const int w = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform
+    const int V = (int)a.V;
+    const gfp rowp = (gfp)(a.logits + (int64_t)row * a.ld);
+    const int mis = (int)(((uintptr_t)rowp >> 2) & 3);  // elements before the row in its 16 B block
+    const gf4p base = (gf4p)(rowp - mis);
+    const int f_lo = mis ? 1 : 0;          // first float4 slot lying fully inside the row
+    const int f_hi = (V + mis - 4) >> 2;   // last one
+    const int slot0 = w * kWaveSlots + l;
+    const bool sampling = a.temperature > 0.0f;
+
+    NIS_TS(0);
+    __builtin_amdgcn_sched_barrier(0);
+    f4v xv[kNch];
+#pragma unroll
+    for (int k = 0; k < kNch; ++k) {
+        const int f = slot0 + k * 64;
+        xv[k] = __builtin_nontemporal_load(base + min(max(f, f_lo), f_hi));
+        __builtin_amdgcn_sched_barrier(0);  // keep chunk order = issue order
+    }
+    // the (at most 3 + 3) elements of the partial head / tail slots
+    const float h0 = rowp[0], h1 = rowp[1], h2 = rowp[2];
+    const float t0 = rowp[V - 3], t1 = rowp[V - 2], t2 = rowp[V - 1];
+
+    // LDS set-up while the loads are in flight
+    for (int i = tid; i < kSampleBins; i += kBlock) sh.scnt[i] = 0u;
+    for (int i = tid; i < kFineBins; i += kBlock) {
+        sh.fcnt[i] = 0u;
+        sh.fmass[i] = 0ull;
+        sh.fkmax[i] = 0u;
+        sh.fkmin[i] = 0xFFFFFFFFu;
+    }
+    if (tid == 0) {
+        sh.ncand = 0u;
+        sh.overflow = 0u;
+        sh.gcount = 0u;
+    }
+
+    // slots not fully inside the row get their exact values or -inf; only
+    // the one or two waves holding such slots take the (wave-uniform) branch.
+    // slot0x is an opaque copy of slot0: the per-chunk slot numbers are then
+    // recomputed where needed instead of being kept live from the loads.
+    int slot0x = slot0;
+    asm volatile("" : "+v"(slot0x));
+#define NIS_FIX(k)                                                                          \
+    do {                                                                                    \
+        const int fb0 = w * kWaveSlots + (k) * 64;                                          \
+        if (fb0 < f_lo || fb0 + 63 > f_hi)                                                  \
+            xv[k] = fix_slot(xv[k], slot0x + (k) * 64, f_lo, f_hi, mis, V, h0, h1, h2, t0, t1, t2); \
+    } while (0)
+#define NIS_INDEX(k, q) (4 * (slot0x + 64 * (k)) + (q) - mis)
+
+    // ------------------------------------------------------------------
+    // greedy (sampler.rs:172-181): first index of the maximum; NaN is
+    // skipped by the strict `>`, except that a NaN at index 0 wins.
+    if (!sampling) {
+        float best = -INFINITY;
+        int bidx = INT_MAX;
+#pragma unroll
+        for (int k = 0; k < kNch; ++k) {
+            NIS_FIX(k);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float x = elem(xv[k], q);
+                if (x > best) {
+                    best = x;
+                    bidx = NIS_INDEX(k, q);
+                }
+            }
+        }
+        // wave max, then its lowest index (lanes interleave indices chunk by
+        // chunk, so the lowest lane holding the max need not hold the lowest index)
+        // (DPP max of the negated index; indices < 2^24 are exact in float)
+        const float wb = wmax_f32(best);
+        const float nwi = wmax_f32((best == wb && bidx != INT_MAX) ? -(float)bidx : -INFINITY);
+        const int wi = (nwi > -INFINITY) ? (int)(-nwi) : INT_MAX;
+        if (l == 0) {
+            sh.fa[w] = wb;
+            sh.ia[w] = wi;
+        }
+        lds_barrier();
+        if (tid == 0) {
+            float b = sh.fa[0];
+            int bi = sh.ia[0];
+            for (int i = 1; i < kWaves; ++i)
+                if (sh.fa[i] > b || (sh.fa[i] == b && sh.ia[i] < bi)) {
+                    b = sh.fa[i];
+                    bi = sh.ia[i];
+                }
+            const uint32_t tok = (h0 != h0 || bi == INT_MAX) ? 0u : (uint32_t)bi;
+            write_row_result(a, row, tok, NIS_PATH_GREEDY, 0.0, 0.0, 0.0, -1.0, 0.0, 0, 1);
+        }
+        return NIS_REJECT_NONE;
+    }
+
+    // ------------------------------------------------------------------
+    const double temp = fmax((double)a.temperature, 1e-6);  // sampler.rs:183
+    const float c = (float)(1.4426950408889634 / temp);     // log2(e) / T
+    const float p = a.top_p;
+    const bool topp = p < 1.0f;  // p <= 0 is excluded by fast_eligible
+
+    // wave-local reference from the wave's first chunk (no barrier)
+    NIS_FIX(0);
+    const float m0 = wmax_f32(max4(xv[0]));
+    const float Rw = (m0 > -INFINITY && fabsf(m0 * c) < 1e30f) ? ceilf(m0 * c) : 0.0f;
+
+    // masses and Z, chunk by chunk as the loads land.  cz / Rz are opaque
+    // copies of c / Rw: without them the compiler merges these masses with
+    // identical later ones and keeps all 104 of them live.
+    double z = 0.0;
+    float mx = -INFINITY;
+    float mx4[kNch];
+    float cz = c, Rz = Rw;
+    asm volatile("" : "+v"(cz), "+v"(Rz));
+#pragma unroll
+    for (int k = 0; k < kNch; ++k) {
+        if (k > 0) NIS_FIX(k);
+        const f4v x = xv[k];
+        f4v e;
+        e.x = mass_of(x.x, cz, Rz);
+        e.y = mass_of(x.y, cz, Rz);
+        e.z = mass_of(x.z, cz, Rz);
+        e.w = mass_of(x.w, cz, Rz);
+        z += (double)((e.x + e.y) + (e.z + e.w));
+        mx4[k] = max4(x);
+        mx = fmaxf(mx, mx4[k]);
+    }
+
+    // ---- T1: row max, reference R, Z ---------------------------------------
+    NIS_TS(1);
+    mx = wmax_f32(mx);
+    z = wsum_f64(z);
+    if (l == 0) {
+        sh.fb[w] = mx;
+        sh.da[w] = z;
+        sh.fc[w] = Rw;
+    }
+    lds_barrier();
+    float M = sh.fb[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) M = fmaxf(M, sh.fb[i]);
+    const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
+    double ZR = 0.0;
+    bool range_ok = true;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+        // each wave's masses were taken against its own reference; a wave
+        // whose reference sits far below the row max may have overflowed
+        range_ok = range_ok && (fmaf(M, c, -sh.fc[i]) <= kMaxT);
+        ZR += ldexp(sh.da[i], (int)(sh.fc[i] - R));  // exact power-of-two rescale
+    }
+    const float tM = fmaf(M, c, -R);
+    // NaN / inf input, an empty row, or a reference too far below the max
+    if (!(M > -INFINITY) || !(M < INFINITY) || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok ||
+        !(fabsf(M * c) < 1e30f))
+        return NIS_REJECT_NONFINITE;
+    // R-units -> units of the max element's mass (tM in (-1, 0])
+    const double rho = (double)__builtin_amdgcn_exp2f(-tM);
+    const double pZ = (double)p * ZR * rho;
+    const double pZR = (double)p * ZR;
+    // The row's RNG state: one word per lane 0..3 of wave 0 (a vector load,
+    // so no LDS wait depends on it), consumed just before the walk.
+    uint64_t rsv = 0;
+    if (w == 0 && l < 4)
+        rsv = ((const __attribute__((address_space(1))) uint64_t*)(a.rng + 4 * (int64_t)row))[l];
+    // sampler.rs:209: the row's single RNG advance, into LDS (written back to
+    // memory only when the row completes here)
+#define NIS_RNG_DRAW()                                                                          \
+    if (w == 0) {                                                                               \
+        uint64_t st[4];                                                                         \
+        for (int j = 0; j < 4; ++j)                                                             \
+            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j); \
+        const double u0 = rng_next_f64(st);                                                     \
+        if (l == 0) {                                                                           \
+            sh.bd[1] = u0;                                                                      \
+            sh.rng[0] = st[0];                                                                  \
+            sh.rng[1] = st[1];                                                                  \
+            sh.rng[2] = st[2];                                                                  \
+            sh.rng[3] = st[3];                                                                  \
+        }                                                                                       \
+    }
+
+    uint32_t reject = NIS_REJECT_NONE;  // reason of a failed sparse attempt
+    if (topp) {
+        // count histogram of chunks 0 and 1 (the sample), relative to R
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float x = elem(xv[q >> 2], q & 3);
+            if (x > -INFINITY) {
+                const float t = fmaf(x, c, -R);
+                const int b = (int)fminf(fmaxf(-t * kSampleRes, 0.0f), (float)(kSampleBins - 1));
+                atomicAdd(&sh.scnt[b], 1u);
+            }
+        }
+        lds_barrier();
+        NIS_TS(2);
+
+        // ---- S1: threshold x_lo from the sample (block-wide scan) --------
+        // lane t owns bins 4t .. 4t+3 (bin 0 = top of the row)
+        const int sb0 = 4 * tid;
+        const u4v cn = *reinterpret_cast<const u4v*>(&sh.scnt[sb0]);
+        const float sm0 = (float)cn.x * bin_mass(sb0), sm1 = (float)cn.y * bin_mass(sb0 + 1);
+        const float sm2 = (float)cn.z * bin_mass(sb0 + 2), sm3 = (float)cn.w * bin_mass(sb0 + 3);
+        const float sms = (sm0 + sm1) + (sm2 + sm3);
+        const uint32_t scs = cn.x + cn.y + cn.z + cn.w;
+        const float smi = wscan_f32(sms);
+        const uint32_t sci = wscan_u32(scs);
+        if (l == 63) {
+            sh.fa[w] = smi;
+            sh.ua[w] = sci;
+        }
+        lds_barrier();
+        float smb = 0.0f, S = 0.0f;
+        uint32_t scb = 0, C = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) {
+            const float v = sh.fa[i];
+            const uint32_t u = sh.ua[i];
+            if (i < w) {
+                smb += v;
+                scb += u;
+            }
+            S += v;
+            C += u;
+        }
+        // row elements per sampled element (estimates only: float is enough)
+        const float F = (float)V * __builtin_amdgcn_rcpf((float)max(C, 1u));
+        const float rem = (1.0f - p) * (float)ZR;  // mass top-p removes
+        const float thr = (float)kSpBeta * rem * __builtin_amdgcn_rcpf(F);
+        // the largest excluded element must weigh at most gamma * (1-p) * Z
+        const float cap_m = (float)kSpGamma * rem;
+        const int bceil =
+            (cap_m < 1.0f)
+                ? min(max((int)ceilf(-kSampleRes * __builtin_amdgcn_logf(cap_m)) - 1, 0), kSampleBins - 1)
+                : 0;
+        int first = kSampleBins;
+        uint32_t cfirst = 0;
+        {
+            float run = smb + (smi - sms);
+            uint32_t crun = scb + (sci - scs);
+#define NIS_SBIN(i, m, n)                                                        \
+    {                                                                            \
+        run += (m);                                                              \
+        crun += (n);                                                             \
+        if (first == kSampleBins && sb0 + (i) >= bceil && S - run <= thr) {      \
+            first = sb0 + (i);                                                   \
+            cfirst = crun;                                                       \
+        }                                                                        \
+    }
+            NIS_SBIN(0, sm0, cn.x)
+            NIS_SBIN(1, sm1, cn.y)
+            NIS_SBIN(2, sm2, cn.z)
+            NIS_SBIN(3, sm3, cn.w)
+#undef NIS_SBIN
+        }
+        {
+            const uint64_t qm = __ballot(first < kSampleBins);
+            if (qm) {
+                const int L = __ffsll((long long)qm) - 1;
+                first = (int)bcast_u32((uint32_t)first, L);
+                cfirst = bcast_u32(cfirst, L);
+            }
+            if (l == 0) {
+                sh.ia[w] = qm ? first : kSampleBins;
+                sh.ub[w] = cfirst;
+            }
+        }
+        lds_barrier();
+        int bsel = kSampleBins;
+        uint32_t csel = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) {
+            if (bsel == kSampleBins && sh.ia[i] < kSampleBins) {
+                bsel = sh.ia[i];
+                csel = sh.ub[i];
+            }
+        }
+        NIS_TS(3);
+        reject = NIS_REJECT_CAPACITY;
+        if (bsel < kSampleBins && F * (float)csel <= (float)kSpEstCap) {
+            const float x_lo =
+                fminf(((float)(-(bsel + 1)) / kSampleRes + R) / c, M);  // the max is a candidate
+
+            // ---- S2: list the float4s holding candidates (wave-compacted) --
+            uint32_t nw = 0;
+#pragma unroll
+            for (int k = 0; k < kNch; ++k) {
+                const bool hit = mx4[k] >= x_lo;
+                const uint64_t mk = __ballot(hit);
+                if (nw <= (uint32_t)(kWaveEnt - 64) && hit) {  // nw is wave-uniform
+                    const uint32_t pos = nw + lane_rank(mk);
+                    sh.s.ent_x[w][pos] = xv[k];
+                    sh.s.ent_pos[w][pos] = (uint16_t)(k * 64 + l);
+                }
+                nw += (uint32_t)__popcll(mk);
+            }
+            NIS_TS(4);
+            lds_wave_fence();
+            // ---- compaction to single candidates, in index order -----------
+            const int ns = 4 * (int)min(nw, (uint32_t)(kWaveEnt - 64));
+            const float* entf = reinterpret_cast<const float*>(&sh.s.ent_x[w][0]);
+            uint32_t nc = 0;
+            #pragma unroll 1
+            for (int s0 = 0; s0 < ns; s0 += 64) {
+                const int s = s0 + l;
+                float x = -INFINITY;
+                uint32_t idx = 0;
+                if (s < ns) {
+                    x = entf[s];
+                    idx = (uint32_t)(4 * (w * kWaveSlots + (int)sh.s.ent_pos[w][s >> 2]) + (s & 3) - mis);
+                }
+                const bool cand = x >= x_lo;
+                const uint64_t mk = __ballot(cand);
+                if (nc <= (uint32_t)(kWaveCand - 64) && cand) {  // nc is wave-uniform
+                    const uint32_t pos = nc + lane_rank(mk);
+                    sh.s.cx[w][pos] = x;
+                    sh.s.ci[w][pos] = idx;
+                }
+                nc += (uint32_t)__popcll(mk);
+            }
+            lds_wave_fence();
+            // ---- candidate masses and their fine histogram over [x_lo, M] --
+            const int ncc = (int)min(nc, (uint32_t)(kWaveCand - 64));
+            const float inv_w = (M > x_lo) ? (float)kFineBins / (M - x_lo) : 0.0f;
+            double g = 0.0;
+            #pragma unroll 1
+            for (int j0 = 0; j0 < ncc; j0 += 64) {
+                const int j = j0 + l;
+                if (j < ncc) {
+                    const float x = sh.s.cx[w][j];
+                    const float e = mass_of(x, c, R);
+                    sh.s.ce[w][j] = e;
+                    g += (double)e;
+                    const int b = fine_bucket(x, x_lo, inv_w);
+                    atomicAdd(&sh.fcnt[b], 1u);
+                    atomicAdd(&sh.fmass[b], (unsigned long long)((double)e * kFix));
+                    atomicMax(&sh.fkmax[b], key32(x));
+                }
+            }
+            g = wsum_f64(g);
+            if (l == 0) {
+                sh.db[w] = g;
+                sh.ua[w] = nw;
+                sh.ub[w] = nc;
+            }
+            lds_barrier();
+            NIS_TS(5);
+            double Gc = 0.0;
+            bool ovf = false;
+#pragma unroll
+            for (int i = 0; i < kWaves; ++i) {
+                Gc += sh.db[i];
+                ovf = ovf || sh.ua[i] > (uint32_t)(kWaveEnt - 64) || sh.ub[i] > (uint32_t)(kWaveCand - 64);
+            }
+            if (ovf) {
+                reject = NIS_REJECT_CAPACITY;
+            } else if (!(Gc - (double)mass_of(x_lo, c, R) > pZR)) {
+                // the largest element below x_lo might be kept
+                reject = NIS_REJECT_WINDOW;
+            } else {
+                // ---- S4: the fine bucket holding the cutoff (block-wide) ---
+                // lane t owns buckets 1023-2t (upper) and 1022-2t
+                const int bA = kFineBins - 1 - 2 * tid, bB = bA - 1;
+                const uint32_t cA = sh.fcnt[bA], cB = sh.fcnt[bB];
+                const double mA = (double)sh.fmass[bA] * (1.0 / kFix);
+                const double mB = (double)sh.fmass[bB] * (1.0 / kFix);
+                const double mt = mA + mB;
+                const double inc = wscan_f64(mt);
+                if (l == 63) sh.da[w] = inc;
+                lds_barrier();
+                double gbase = 0.0;
+#pragma unroll
+                for (int i = 0; i < kWaves; ++i)
+                    if (i < w) gbase += sh.da[i];
+                const double GA = gbase + (inc - mt);  // candidate mass above bucket bA
+                const double GB = GA + mA;
+                // sampler.rs:150 for the largest element of the bucket
+                const bool kA = cA != 0 && (GA - (double)mass_of(unkey32(sh.fkmax[bA]), c, R) <= pZR);
+                const bool kB = cB != 0 && (GB - (double)mass_of(unkey32(sh.fkmax[bB]), c, R) <= pZR);
+                sh.s.gab[bA] = GA;
+                sh.s.gab[bB] = GB;
+                const int lowk = wave_min(kB ? bB : (kA ? bA : kFineBins));
+                if (l == 0) sh.ia[w] = lowk;
+                lds_barrier();
+                int bstar = kFineBins;
+#pragma unroll
+                for (int i = 0; i < kWaves; ++i) bstar = min(bstar, sh.ia[i]);
+                NIS_TS(6);
+                const uint32_t nstar = (bstar < kFineBins) ? sh.fcnt[bstar] : 0u;
+                if (bstar >= kFineBins || nstar > (uint32_t)kMaxFinal) {
+                    reject = NIS_REJECT_CAPACITY;
+                } else {
+                    const double gab = sh.s.gab[bstar];
+                    // ---- gather the cutoff bucket's members ------------------
+                    #pragma unroll 1
+                    for (int j0 = 0; j0 < ncc; j0 += 64) {
+                        const int j = j0 + l;
+                        if (j < ncc) {
+                            const float x = sh.s.cx[w][j];
+                            if (fine_bucket(x, x_lo, inv_w) == bstar) {
+                                const uint32_t s = atomicAdd(&sh.gcount, 1u);
+                                if (s < (uint32_t)kMaxFinal) {
+                                    sh.s.gx[s] = x;
+                                    sh.s.gi[s] = sh.s.ci[w][j];
+                                    sh.s.ge[s] = sh.s.ce[w][j];
+                                }
+                            }
+                        }
+                    }
+                    lds_barrier();
+                    NIS_TS(7);
+                    if (sh.gcount != nstar) {
+                        reject = NIS_REJECT_BUCKET;
+                    } else {
+                        // ---- exact rule inside the bucket (wave 0) -----------
+                        if (w == 0) {
+                            const int n = (int)nstar;
+                            const bool valid = l < n;
+                            const float xm = valid ? sh.s.gx[l] : -INFINITY;
+                            const uint32_t km = key32(xm);
+                            const uint32_t im = valid ? sh.s.gi[l] : 0u;
+                            const float em = valid ? sh.s.ge[l] : 0.0f;
+                            // mass of the members ahead of this one in the
+                            // reference's stable descending order
+                            double pre = 0.0;
+                            #pragma unroll 1
+                            for (int j = 0; j < n; ++j) {
+                                const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
+                                const float ej = bcast_f32(em, j);
+                                const bool before = kj > km || (kj == km && ij < im);
+                                pre += before ? (double)ej : 0.0;
+                            }
+                            const bool kept = valid && (gab + pre - (double)em <= pZR);
+                            // the last kept member: smallest key, then largest index
+                            const uint64_t comp =
+                                kept ? (((uint64_t)km << 32) | (uint64_t)(0xFFFFFFFFu - im)) : ~0ull;
+                            const uint64_t cmin = wave_min(comp);
+                            if (l == 0) {
+                                sh.cut_key = (uint32_t)(cmin >> 32);
+                                sh.cut_idx = 0xFFFFFFFFu - (uint32_t)cmin;
+                            }
+                        }
+                        NIS_RNG_DRAW()
+                        lds_barrier();
+                        NIS_TS(8);
+                        // ---- S7: inverse-CDF walk over the candidate lists -------
+                        const uint32_t kc = sh.cut_key, ic = sh.cut_idx;
+                        double kw = 0.0;
+                        uint32_t nk = 0;
+                        #pragma unroll 1
+                        for (int j0 = 0; j0 < ncc; j0 += 64) {
+                            const int j = j0 + l;
+                            if (j < ncc) {
+                                const uint32_t k = key32(sh.s.cx[w][j]);
+                                const uint32_t id = sh.s.ci[w][j];
+                                if (k > kc || (k == kc && id <= ic)) {
+                                    kw += (double)sh.s.ce[w][j];
+                                    ++nk;
+                                }
+                            }
+                        }
+                        kw = wsum_f64(kw);
+                        nk = wsum_u32(nk);
+                        if (l == 0) {
+                            sh.wtot[w] = kw;
+                            sh.ua[w] = nk;
+                        }
+                        lds_barrier();
+                        double zk = 0.0;
+#pragma unroll
+                        for (int i = 0; i < kWaves; ++i) zk += sh.wtot[i];
+                        const double u = sh.bd[1];
+                        const double r = u * zk;
+                        int wsel = -1;
+                        double wbase = 0.0;
+                        {
+                            double acc = 0.0;
+#pragma unroll
+                            for (int i = 0; i < kWaves; ++i) {
+                                const double nx = acc + sh.wtot[i];
+                                if (wsel < 0 && nx >= r && sh.wtot[i] > 0.0) {
+                                    wsel = i;
+                                    wbase = acc;
+                                }
+                                acc = nx;
+                            }
+                            if (wsel < 0) {  // rounding: the last wave with mass
+                                acc = 0.0;
+#pragma unroll
+                                for (int i = 0; i < kWaves; ++i) {
+                                    if (sh.wtot[i] > 0.0) {
+                                        wsel = i;
+                                        wbase = acc;
+                                    }
+                                    acc += sh.wtot[i];
+                                }
+                            }
+                        }
+                        wsel = __builtin_amdgcn_readfirstlane(wsel);
+                        if (w == wsel) {
+                            double run = wbase;
+                            int tok = -1, last = -1;
+                            float xt = 0.0f, xlast = 0.0f;
+                            #pragma unroll 1
+                            for (int j0 = 0; j0 < ncc; j0 += 64) {
+                                const int j = j0 + l;
+                                float x = -INFINITY;
+                                uint32_t id = 0;
+                                float e = 0.0f;
+                                if (j < ncc) {
+                                    x = sh.s.cx[w][j];
+                                    id = sh.s.ci[w][j];
+                                    e = sh.s.ce[w][j];
+                                }
+                                const uint32_t k = key32(x);
+                                const bool kept = (j < ncc) && (k > kc || (k == kc && id <= ic));
+                                const double em = kept ? (double)e : 0.0;
+                                const double inc = wscan_f64(em);
+                                const uint64_t hit = __ballot(kept && run + inc >= r);
+                                if (hit) {
+                                    const int L = __ffsll((long long)hit) - 1;
+                                    tok = (int)bcast_u32(id, L);
+                                    xt = bcast_f32(x, L);
+                                    break;
+                                }
+                                const uint64_t km = __ballot(kept);
+                                if (km) {
+                                    const int L = 63 - __clzll((long long)km);
+                                    last = (int)bcast_u32(id, L);
+                                    xlast = bcast_f32(x, L);
+                                }
+                                run += bcast_f64(inc, 63);
+                            }
+                            bool tkept = true;
+                            if (tok < 0) {  // rounding: the last kept token of this wave
+                                tok = last;
+                                xt = xlast;
+                            }
+                            if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
+                                tok = 0;
+                                tkept = false;
+                            }
+                            if (l == 0) {
+                                uint32_t kept_total = 0;
+#pragma unroll
+                                for (int i = 0; i < kWaves; ++i) kept_total += sh.ua[i];
+                                const double zkM = zk * rho;
+                                const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
+                                write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
+                                                 zkM, ZR * rho, u, prob, (uint64_t)kept_total, 1);
+                            }
+                        }
+                        if (tid == 0) {
+                            uint64_t* sp = a.rng + 4 * (int64_t)row;
+                            sp[0] = sh.rng[0];
+                            sp[1] = sh.rng[1];
+                            sp[2] = sh.rng[2];
+                            sp[3] = sh.rng[3];
+                        }
+                        NIS_TS(9);
+                        return NIS_REJECT_NONE;
+                    }
+                }
+            }
+        }
+        // the sparse route gave up: the dense route starts from clean buckets
+        __syncthreads();
+        for (int i = tid; i < kFineBins; i += kBlock) {
+            sh.fcnt[i] = 0u;
+            sh.fmass[i] = 0ull;
+            sh.fkmax[i] = 0u;
+            sh.fkmin[i] = 0xFFFFFFFFu;
+        }
+        if (tid == 0) {
+            sh.ncand = 0u;
+            sh.overflow = 0u;
+        }
+    }
+
+    // ====================================================================
+    // Dense route
+    // ---- T2: value window bracketing the cutoff, from the sample (wave 0)
+    if (topp && w == 0) {
+        // lane l owns bins [32l, 32l + 32); bin 0 = top of the row
+        uint32_t cnt = 0;
+        float msf = 0.0f;
+#pragma unroll
+        for (int i4 = 0; i4 < 8; ++i4) {
+            const u4v sb = *reinterpret_cast<const u4v*>(&sh.scnt[32 * l + 4 * i4]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t n = elemu(sb, q);
+                cnt += n;
+                msf += (float)n * bin_mass(32 * l + 4 * i4 + q);
+            }
+        }
+        const uint32_t cnt_incl = wscan_u32(cnt);
+        const double ms_incl = wscan_f64((double)msf);
+        const uint32_t n_s = (uint32_t)__builtin_amdgcn_readlane((int)cnt_incl, 63);
+        const double S_s = bcast_f64(ms_incl, 63);
+        // estimated boundary: the sample rank at which the mass left below
+        // (sample mass scaled to the row) drops to (1 - p) * Z
+        const double F = (double)V / (double)max(n_s, 1u);
+        const double removed = (1.0 - (double)p) * ZR;
+        int n_above = 0;
+        if (F * S_s > removed) {
+            const uint64_t bal = __ballot(F * (S_s - ms_incl) <= removed);
+            const int L0 = bal ? (__ffsll((long long)bal) - 1) : 63;
+            int na_l = -1;
+            if (l == L0) {
+                double mprev = ms_incl - (double)msf;
+                int na = (int)(cnt_incl - cnt);
+                bool done = false;
+                #pragma unroll 1
+                for (int i = 0; i < 32; ++i) {
+                    if (!done) {
+                        const uint32_t n = sh.scnt[32 * l + i];
+                        mprev += (double)((float)n * bin_mass(32 * l + i));
+                        na += (int)n;
+                        done = F * (S_s - mprev) <= removed;
+                    }
+                }
+                na_l = na;
+            }
+            n_above = __shfl(na_l, L0);
+        }
+        const int n_below = (int)n_s - n_above;
+        const int W = (int)(6.0 * sqrt((double)min(n_above, n_below))) + 10;
+        const int top_rank = n_above - W;  // sample ranks (from the top) bracketing the cutoff
+        const int bot_rank = n_above + W;
+        const int cexcl = (int)(cnt_incl - cnt);
+        // the bin holding a given sample rank (read back from LDS by its owner lane)
+        int b_top = -1, b_bot = kSampleBins;
+#define NIS_BIN_OF_RANK(rank, out)                                   \
+    {                                                                \
+        const uint64_t bal = __ballot((int)cnt_incl >= (rank));      \
+        const int L = __ffsll((long long)bal) - 1;                   \
+        int b = -1;                                                  \
+        if (l == L) {                                                \
+            int acc = cexcl;                                         \
+            for (int i = 0; i < 32; ++i) {                           \
+                acc += (int)sh.scnt[32 * l + i];                     \
+                if (b < 0 && acc >= (rank)) b = 32 * l + i;          \
+            }                                                        \
+        }                                                            \
+        (out) = __shfl(b, L);                                        \
+    }
+        if (top_rank > 0) NIS_BIN_OF_RANK(top_rank, b_top)
+        if (bot_rank < (int)n_s) NIS_BIN_OF_RANK(bot_rank, b_bot)
+#undef NIS_BIN_OF_RANK
+        {
+            // never leave the window open below: stop at the lowest sample
+            // bin (a cutoff below it is caught by the bottom check)
+            const uint64_t nzb = __ballot(cnt != 0);
+            if (nzb) {
+                const int L = 63 - __clzll((long long)nzb);
+                int lb = -1;
+                if (l == L) {
+                    #pragma unroll 1
+                    for (int i = 0; i < 32; ++i)
+                        if (sh.scnt[32 * l + i] != 0) lb = 32 * l + i;
+                }
+                lb = __shfl(lb, L);
+                if (b_bot > lb) b_bot = lb;
+            }
+        }
+        if (l == 0) {
+            // bin b holds t in (-(b+1)/64, -b/64]; the elements above bin
+            // b_top are kept for sure, the window spans bins b_top..b_bot
+            sh.bf[0] = (b_top < 0) ? INFINITY : ((float)(-b_top) / kSampleRes + R) / c;
+            sh.bf[1] = (b_bot >= kSampleBins) ? -INFINITY
+                                              : ((float)(-(b_bot + 1)) / kSampleRes + R) / c;
+        }
+    }
+    if (topp) lds_barrier();
+    NIS_TS(10);
+    // without top-p every finite element is kept and the window is empty
+    const float x_hi = topp ? sh.bf[0] : -INFINITY;
+    const float x_lo = topp ? sh.bf[1] : INFINITY;
+
+    // ---- P1: per-chunk kept mass above the window, window elements listed
+    double lane_kept = 0.0;  // kept mass of this lane (R-units)
+    int nsure = 0;           // kept elements of this lane above the window
+    int lpos = 0;            // window elements of this lane
+#pragma unroll
+    for (int k = 0; k < kNch; ++k) {
+        float cs = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float x = elem(xv[k], q);
+            const bool sure = x > x_hi;
+            cs += sure ? mass_of(x, c, R) : 0.0f;
+            nsure += sure ? 1 : 0;
+            if (!sure && x >= x_lo) {
+                if (lpos < kLaneCap) {
+                    sh.d.lx[lpos][tid] = x;
+                    sh.d.lp[lpos][tid] = (uint8_t)(4 * k + q);
+                }
+                ++lpos;
+            }
+        }
+        sh.d.cell[w][k][l] = cs;
+        lane_kept += (double)cs;
+    }
+    if (lpos > kLaneCap) sh.overflow = 1u;
+    lds_barrier();
+    NIS_TS(11);
+    if (sh.overflow) return reject != NIS_REJECT_NONE ? reject : NIS_REJECT_CAPACITY;
+    const int nl = lpos;  // <= kLaneCap here
+
+    float xf_lo = INFINITY, xf_hi = -INFINITY;  // value range of the cutoff bucket
+    double g_above_f = 0.0;
+    uint32_t n_final = 0;
+    if (topp) {
+        // ---- fine histogram of the window lists --------------------------
+        const float x_top = fminf(x_hi, M);
+        const float inv_w = (x_top > x_lo) ? (float)kFineBins / (x_top - x_lo) : 0.0f;
+        const double sfix = rho * kFix;
+        #pragma unroll 1
+        for (int i = 0; i < nl; ++i) {
+            const float x = sh.d.lx[i][tid];
+            const int fb = fine_bucket(x, x_lo, inv_w);
+            const uint32_t key = key32(x);
+            atomicAdd(&sh.fcnt[fb], 1u);
+            atomicAdd(&sh.fmass[fb], (unsigned long long)((double)mass_of(x, c, R) * sfix));
+            atomicMax(&sh.fkmax[fb], key);
+            atomicMin(&sh.fkmin[fb], key);
+        }
+        const double g = wsum_f64(lane_kept);
+        if (l == 0) sh.db[w] = g;
+        lds_barrier();
+        double GhiR = sh.db[0];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) GhiR += sh.db[i];
+
+        // ---- T4: the fine bucket holding the cutoff (wave 0) -------------
+        if (w == 0) {
+            // lane l owns buckets 1023-16l .. 1008-16l (descending value),
+            // i.e. the 16 ascending buckets starting at 1008-16l
+            const int b0 = kFineBins - 16 - 16 * l;
+            double mlane = 0.0;
+            int lastne = -1;  // lowest non-empty bucket of this lane
+            #pragma unroll 1
+            for (int i = 0; i < 16; ++i) {
+                mlane += (double)sh.fmass[b0 + i] / kFix;
+                if (lastne < 0 && sh.fcnt[b0 + i] != 0) lastne = b0 + i;
+            }
+            const double incl = wscan_f64(mlane);
+            const double Ghi = GhiR * rho;
+            double G = Ghi + (incl - mlane);
+            int fstar = -1;
+            double gstar = 0.0;
+            bool stop = false;
+            #pragma unroll 1
+            for (int i = 15; i >= 0; --i) {  // descending value
+                if (!stop && sh.fcnt[b0 + i] != 0) {
+                    const double ef = (double)mass_of(unkey32(sh.fkmax[b0 + i]), c, R) * rho;
+                    if (G - ef <= pZ) {
+                        fstar = b0 + i;
+                        gstar = G;
+                        G += (double)sh.fmass[b0 + i] / kFix;
+                    } else {
+                        stop = true;
+                    }
+                }
+            }
+            // D_first is non-decreasing down the buckets, so the qualifying
+            // buckets form a prefix: the cutoff bucket is the lowest of them
+            int best = (fstar >= 0) ? (kFineBins - fstar) : -1;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) best = max(best, __shfl_xor(best, o));
+            int lowest = (lastne >= 0) ? (kFineBins - lastne) : -1;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) lowest = max(lowest, __shfl_xor(lowest, o));
+            const double Gtot = __shfl(incl, 63) + Ghi;
+            const int owner = (best > 0) ? ((best - 1) / 16) : 0;
+            const double gs = __shfl(gstar, owner);
+            if (l == 0) {
+                int ok = 1;
+                // every element above the window must be kept
+                if (x_hi < INFINITY && !(Ghi - (double)mass_of(x_hi, c, R) * rho <= pZ)) ok = 0;
+                if (best < 0) ok = 0;
+                // cutoff in the lowest bucket: the first element below the
+                // window must be removed
+                if (ok && best == lowest && !(Gtot - (double)mass_of(x_lo, c, R) * rho > pZ)) ok = 0;
+                sh.bi[0] = ok;
+                sh.bi[1] = ok ? (kFineBins - best) : 0;
+                sh.bd[0] = gs;
+            }
+        }
+        lds_barrier();
+        NIS_TS(12);
+        if (!sh.bi[0]) return NIS_REJECT_WINDOW;
+        const int fstar = sh.bi[1];
+        n_final = sh.fcnt[fstar];
+        if (n_final > (uint32_t)kMaxFinal) return NIS_REJECT_CAPACITY;
+        xf_hi = unkey32(sh.fkmax[fstar]);
+        xf_lo = unkey32(sh.fkmin[fstar]);
+        g_above_f = sh.bd[0];
+        // flag list entries above the bucket as kept, gather the bucket's members
+        #pragma unroll 1
+        for (int i = 0; i < nl; ++i) {
+            const float x = sh.d.lx[i][tid];
+            if (x > xf_hi) {
+                sh.d.lp[i][tid] |= kKeptBit;
+            } else if (x >= xf_lo) {
+                const uint32_t s = atomicAdd(&sh.ncand, 1u);
+                if (s < (uint32_t)kMaxFinal) {
+                    const int pos = sh.d.lp[i][tid];
+                    sh.d.cj[s] = (uint32_t)(4 * (slot0 + 64 * (pos >> 2)) + (pos & 3) - mis);
+                    sh.d.cx[s] = x;
+                    sh.d.cloc[s] = (uint32_t)(tid * kLaneCap + i);
+                }
+            }
+        }
+        lds_barrier();
+        if (sh.ncand != n_final) return NIS_REJECT_BUCKET;  // bucket membership must match the histogram
+
+        // ---- T6: exact rule on the cutoff bucket (wave 0) -------------------
+        if (w == 0) {
+            const int n = (int)n_final;
+            const bool valid = l < n;
+            const float xm = valid ? sh.d.cx[l] : -INFINITY;
+            const uint32_t km = key32(xm);
+            const uint32_t im = valid ? sh.d.cj[l] : 0u;
+            const double em = valid ? (double)mass_of(xm, c, R) * rho : 0.0;
+            double pre = 0.0;  // mass of the members ahead in the stable descending order
+            #pragma unroll 1
+            for (int j = 0; j < n; ++j) {
+                const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
+                const double ej = bcast_f64(em, j);
+                pre += (kj > km || (kj == km && ij < im)) ? ej : 0.0;
+            }
+            // sampler.rs:150: removed iff cum_excl - q > p; kept otherwise
+            const bool kept = valid && (g_above_f + pre - em <= pZ);
+            if (kept) {
+                const uint32_t loc = sh.d.cloc[l];
+                sh.d.lp[loc % kLaneCap][loc / kLaneCap] |= kKeptBit;
+            }
+        }
+        lds_barrier();
+    }
+    NIS_TS(13);
+
+    // ---- T7: inverse-CDF walk in index order --------------------------------
+    // kept list entries join their lane's cells (the owner updates its own cells)
+    int nkept = nsure;
+    #pragma unroll 1
+    for (int i = 0; i < nl; ++i) {
+        const int pos = sh.d.lp[i][tid];
+        if (pos & kKeptBit) {
+            const int k = (pos & 0x7F) >> 2;
+            const float e = mass_of(sh.d.lx[i][tid], c, R);
+            sh.d.cell[w][k][l] += e;
+            lane_kept += (double)e;
+            ++nkept;
+        }
+    }
+    {
+        const double wt = wsum_f64(lane_kept);
+        const int wk = (int)wsum_u32((uint32_t)nkept);
+        if (l == 0) {
+            sh.wtot[w] = wt;
+            sh.ia[w] = wk;
+        }
+    }
+    NIS_RNG_DRAW()
+    lds_barrier();
+    double zk = 0.0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) zk += sh.wtot[i];
+    const double u = sh.bd[1];
+    const double r = u * zk;
+    int wsel = -1;
+    double wbase = 0.0;
+    {
+        double acc = 0.0;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) {
+            const double nx = acc + sh.wtot[i];
+            if (wsel < 0 && nx >= r && sh.wtot[i] > 0.0) {
+                wsel = i;
+                wbase = acc;
+            }
+            acc = nx;
+        }
+        if (wsel < 0) {  // rounding: the last wave with mass
+            acc = 0.0;
+#pragma unroll
+            for (int i = 0; i < kWaves; ++i) {
+                if (sh.wtot[i] > 0.0) {
+                    wsel = i;
+                    wbase = acc;
+                }
+                acc += sh.wtot[i];
+            }
+        }
+    }
+    wsel = __builtin_amdgcn_readfirstlane(wsel);
+    if (w == wsel) {  // static register indices only (a dynamic one would demote xv to scratch)
+#pragma unroll
+        for (int k = 0; k < kNch; ++k) sh.d.stx[k][l] = xv[k];
+    }
+    // chunk totals of the chosen wave (wave w handles chunks w, w+8, ...)
+    #pragma unroll 1
+    for (int kk = w; kk < kNch; kk += kWaves) {
+        const double cv = wsum_f64((double)sh.d.cell[wsel][kk][l]);
+        if (l == 0) sh.ctot[kk] = cv;
+    }
+    lds_barrier();
+    int ksel = -1;
+    double kbase = wbase;
+    {
+        double cb = wbase;
+        #pragma unroll 1
+        for (int k = 0; k < kNch; ++k) {
+            const double nb = cb + sh.ctot[k];
+            if (ksel < 0 && nb >= r && sh.ctot[k] > 0.0) {
+                ksel = k;
+                kbase = cb;
+            }
+            cb = nb;
+        }
+        if (ksel < 0) {  // rounding: the last chunk with mass
+            cb = wbase;
+            #pragma unroll 1
+            for (int k = 0; k < kNch; ++k) {
+                if (sh.ctot[k] > 0.0) {
+                    ksel = k;
+                    kbase = cb;
+                }
+                cb += sh.ctot[k];
+            }
+        }
+    }
+    ksel = __builtin_amdgcn_readfirstlane(ksel);
+    if (w == wsel) {
+        // lane prefix inside the chosen chunk; the owning lane finishes the walk
+        const double cvl = (double)sh.d.cell[wsel][ksel][l];
+        const double incl = wscan_f64(cvl);
+        const uint64_t hit = __ballot(kbase + incl >= r && cvl > 0.0);
+        const uint64_t nz = __ballot(cvl > 0.0);
+        const int lsel = hit ? (__ffsll((long long)hit) - 1) : (63 - __clzll((long long)nz));
+        if (l == lsel) {
+            // this lane's kept flags for the chunk's 4 elements
+            uint32_t wkept = 0;
+            #pragma unroll 1
+            for (int i = 0; i < nl; ++i) {
+                const int pos = sh.d.lp[i][tid];
+                if ((pos & kKeptBit) && ((pos & 0x7F) >> 2) == ksel) wkept |= 1u << (pos & 3);
+            }
+            const f4v xs = sh.d.stx[ksel][l];
+            double run = kbase + incl - cvl;
+            int tok = -1, last = -1;
+            float xt = 0.0f, xlast = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float x = elem(xs, q);
+                if (x > x_hi || ((wkept >> q) & 1u)) {
+                    run += (double)mass_of(x, c, R);
+                    const int j = 4 * (slot0 + 64 * ksel) + q - mis;
+                    if (tok < 0) {
+                        last = j;
+                        xlast = x;
+                        if (run >= r) {
+                            tok = j;
+                            xt = x;
+                        }
+                    }
+                }
+            }
+            bool tkept = true;
+            if (tok < 0) {  // rounding: the crossing is this lane's last kept token
+                tok = last;
+                xt = xlast;
+            }
+            if (u == 0.0) {  // r == 0 stops the reference's walk at index 0 (sampler.rs:210-213)
+                tok = 0;
+                tkept = false;
+            }
+            int kept_total = 0;
+            #pragma unroll 1
+            for (int i = 0; i < kWaves; ++i) kept_total += sh.ia[i];
+            const double zkM = zk * rho;
+            const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
+            write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp, zkM,
+                             topp ? ZR * rho : 0.0, u, prob, (uint64_t)kept_total, 1);
+        }
+    }
+    if (tid == 0) {
+        uint64_t* sp = a.rng + 4 * (int64_t)row;
+        sp[0] = sh.rng[0];
+        sp[1] = sh.rng[1];
+        sp[2] = sh.rng[2];
+        sp[3] = sh.rng[3];
+    }
+    NIS_TS(14);
+    return NIS_REJECT_NONE;
+#undef NIS_FIX
+#undef NIS_INDEX
+#undef NIS_RNG_DRAW
+}
+
+}  // namespace nis

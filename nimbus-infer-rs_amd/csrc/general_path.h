@@ -50,10 +50,11 @@ struct GeneralShared {
     int64_t bi[4];
 };
 
-__device__ __forceinline__ void write_row_result(const RowArgs& a, int row, uint32_t token,
+__device__ __forceinline__ void write_row_result(const RowArgs a, int row, uint32_t token,
                                                  uint32_t path, double max_w, double z_kept,
                                                  double z_all, double u, double prob,
-                                                 uint64_t kept, uint32_t kernel) {
+                                                 uint64_t kept, uint32_t kernel,
+                                                 uint32_t reject = NIS_REJECT_NONE) {
     a.tokens[row] = token;
     if (a.stats) {
         nis_row_stats s;
@@ -66,7 +67,7 @@ __device__ __forceinline__ void write_row_result(const RowArgs& a, int row, uint
         s.path = path;
         s.token = token;
         s.kernel = kernel;
-        s._pad = 0;
+        s.reject = reject;
         a.stats[row] = s;
     }
 }
@@ -96,7 +97,9 @@ __device__ __forceinline__ bool in_prefix(uint64_t key, int shift, uint64_t pref
     return (shift + 8 >= 64) ? true : ((key >> (shift + 8)) == prefix);
 }
 
-__device__ void general_row(const RowArgs& a, const int row, GeneralShared& sh) {
+// `reject` is recorded in the row's stats: why the fast path declined it.
+__device__ __noinline__ void general_row(const RowArgs a, const int row, GeneralShared& sh,
+                                         const uint32_t reject) {
     const int tid = threadIdx.x;
     const float* __restrict__ x = a.logits + (int64_t)row * a.ld;
     const int64_t V = a.V;
@@ -155,7 +158,7 @@ __device__ void general_row(const RowArgs& a, const int row, GeneralShared& sh) 
     if (a.temperature <= 0.0f) {
         if (tid == 0) {
             const uint32_t tok = (nan0 || ifirst == INT64_MAX) ? 0u : (uint32_t)ifirst;
-            write_row_result(a, row, tok, NIS_PATH_GREEDY, 0.0, 0.0, 0.0, -1.0, 0.0, 0, 2);
+            write_row_result(a, row, tok, NIS_PATH_GREEDY, 0.0, 0.0, 0.0, -1.0, 0.0, 0, 2, reject);
         }
         return;
     }
@@ -187,7 +190,7 @@ __device__ void general_row(const RowArgs& a, const int row, GeneralShared& sh) 
                 tok = 0u;
                 path = NIS_PATH_NONFINITE_MAX;
             }
-            write_row_result(a, row, tok, path, M_w, 0.0, 0.0, -1.0, 0.0, 0, 2);
+            write_row_result(a, row, tok, path, M_w, 0.0, 0.0, -1.0, 0.0, 0, 2, reject);
         }
         return;
     }
@@ -370,7 +373,7 @@ __device__ void general_row(const RowArgs& a, const int row, GeneralShared& sh) 
     if (!(z_kept > 0.0) || !(z_kept < INFINITY)) {  // sampler.rs:206-208
         if (tid == 0)
             write_row_result(a, row, 0u, NIS_PATH_BAD_TOTAL, M_w, z_kept, z_all, -1.0, 0.0,
-                             (uint64_t)kept_total, 2);
+                             (uint64_t)kept_total, 2, reject);
         return;
     }
     if (tid == 0) {  // sampler.rs:209 — the only RNG advance of the call
@@ -420,7 +423,7 @@ __device__ void general_row(const RowArgs& a, const int row, GeneralShared& sh) 
             etok = exp(val(tok) / temp - M_w);
         }
         write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, M_w, z_kept, z_all, u,
-                         ktok ? etok / z_kept : 0.0, (uint64_t)kept_total, 2);
+                         ktok ? etok / z_kept : 0.0, (uint64_t)kept_total, 2, reject);
     }
 }
 

@@ -1,13 +1,30 @@
 // kernels.h — __global__ entry points of the sampler library (gfx950).
 #pragma once
-#include "general_path.h"
+#include "fast_path.h"
 
 namespace nis {
 
-// One workgroup per row.
+// One workgroup per row: the register-resident fast path when the row fits
+// it, the general path otherwise (or when the fast path declines the row).
+__global__ __launch_bounds__(kBlock) void sample_rows_kernel(RowArgs a) {
+    __shared__ union {
+        GeneralShared g;
+        FastShared f;
+    } sh;
+    const int row = (int)blockIdx.x;
+    uint32_t reject = NIS_REJECT_SHAPE;
+    if (fast_eligible(a, row)) {
+        reject = fast_row(a, row, sh.f);
+        if (reject == NIS_REJECT_NONE) return;
+        __syncthreads();
+    }
+    general_row(a, row, sh.g, reject);
+}
+
+// General path only (used by tests to cross-check the two paths).
 __global__ __launch_bounds__(kBlock) void sample_rows_general_kernel(RowArgs a) {
     __shared__ GeneralShared sh;
-    general_row(a, (int)blockIdx.x, sh);
+    general_row(a, (int)blockIdx.x, sh, NIS_REJECT_NONE);
 }
 
 // Rng::new per row (sampler.rs:46-56).

@@ -26,7 +26,7 @@ PATH_GREEDY, PATH_NONFINITE_MAX, PATH_BAD_TOTAL, PATH_DRAW, PATH_FALLTHROUGH = 1
 # nis_row_stats
 ROW_STATS_DTYPE = np.dtype([
     ("max_w", "<f8"), ("z_kept", "<f8"), ("z_all", "<f8"), ("u", "<f8"), ("prob", "<f8"),
-    ("kept", "<u8"), ("path", "<u4"), ("token", "<u4"), ("kernel", "<u4"), ("_pad", "<u4"),
+    ("kept", "<u8"), ("path", "<u4"), ("token", "<u4"), ("kernel", "<u4"), ("reject", "<u4"),
 ])
 assert ROW_STATS_DTYPE.itemsize == 64
 

@@ -54,7 +54,9 @@ def compare(gpu, ref, greedy):
     g_tok, g_st, g_states = gpu
     r_tok, r_st, r_states = ref
     B = len(r_tok)
-    rep = {"rows": B}
+    rej = g_st["reject"][g_st["kernel"] == 2]
+    rep = {"rows": B, "fast_rows": int((g_st["kernel"] == 1).sum()),
+           "rejects": {int(k): int(n) for k, n in zip(*np.unique(rej, return_counts=True))}}
     assert np.array_equal(g_states, r_states), \
         f"rng state mismatch on rows {np.nonzero((g_states != r_states).any(1))[0][:10].tolist()}"
     if greedy:
