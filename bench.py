@@ -79,11 +79,8 @@ def main():
     params = ns.SamplingParams(temperature=w.temperature, top_p=w.top_p)
 
     host0 = w.make(B)
-    bufs = [torch.from_numpy(host0).to(dev)]
-    for i in range(1, args.buffers):
-        # distinct batches of the same distribution: permute rows and roll columns
-        bufs.append(torch.roll(bufs[0][torch.randperm(B, generator=torch.Generator().manual_seed(i))],
-                               shifts=997 * i, dims=1).contiguous())
+    # distinct batches of the same distribution: rows permuted, columns rolled
+    bufs = [torch.from_numpy(workloads.rotation(host0, i)).to(dev) for i in range(args.buffers)]
     states = torch.from_numpy(ns.rng_states(w.seeds).view(np.int64)).to(dev)
     tokens = torch.empty(B, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()

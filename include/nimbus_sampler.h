@@ -72,7 +72,9 @@ typedef struct nis_row_stats {
     uint32_t path;  /* NIS_PATH_* */
     uint32_t token;
     uint32_t kernel;/* 1 = register-resident fast path, 2 = general path */
-    uint32_t reject;/* NIS_REJECT_*: why the fast path handed the row on (0 if it did not) */
+    uint32_t reject;/* NIS_REJECT_*: kernel 2 -> why the fast path handed the row on;
+                       kernel 1 -> why its sparse top-p route declined (the
+                       register-resident dense route then produced it); 0 if not */
 } nis_row_stats;
 
 /* nis_row_stats.reject: the fast path declines a row it cannot prove exact

@@ -59,10 +59,16 @@ constexpr float kMaxT = 60.0f;                // overflow guard for 2^(x*c - R)
 constexpr double kFix = 1099511627776.0;      // 2^40 fixed-point mass scale
 constexpr uint8_t kKeptBit = 0x80;
 // sparse route
-constexpr int kWaveEnt = 384;                 // listed float4s per wave
-constexpr int kWaveCand = 512;                // candidates per wave
-constexpr double kSpBeta = 0.5;               // sampled mass below x_lo <= beta * (1-p) * Z
-constexpr double kSpGamma = 0.25;             // e(x_lo) <= gamma * (1-p) * Z
+constexpr int kWaveEnt = 352;                 // listed float4s per wave
+constexpr int kWaveCand = 448;                // candidates per wave
+// x_lo: the highest sample bin whose estimated mass below, plus kSpKappa
+// standard deviations of that estimate, stays under beta * (1-p) * Z, with
+// e(x_lo) <= gamma * (1-p) * Z and at least kSpMinAbove sampled elements at
+// or above it (so the band just below x_lo is represented in the sample)
+constexpr double kSpBeta = 0.7;
+constexpr float kSpKappa = 3.0f;
+constexpr double kSpGamma = 0.25;
+constexpr uint32_t kSpMinAbove = 16;
 constexpr double kSpEstCap = 2800.0;          // estimated candidates per row
 
 struct DenseShared {
@@ -75,11 +81,13 @@ struct DenseShared {
     uint32_t cloc[kMaxFinal];        //   owner thread * kLaneCap + list slot
 };
 struct SparseShared {
-    f4v ent_x[kWaves][kWaveEnt];         // listed float4s, wave-compacted in index order
-    uint16_t ent_pos[kWaves][kWaveEnt];  //   their chunk * 64 + lane
-    float cx[kWaves][kWaveCand];         // candidates (x >= x_lo) in index order: logit
-    uint32_t ci[kWaves][kWaveCand];      //   row index
-    float ce[kWaves][kWaveCand];         //   mass 2^(x*c - R)
+    // per-wave lists; the 64 slots past each list's capacity take the
+    // writes of lanes with nothing to append (branch-free appends)
+    f4v ent_x[kWaves][kWaveEnt + 64];         // listed float4s, wave-compacted in index order
+    uint16_t ent_pos[kWaves][kWaveEnt + 64];  //   their chunk * 64 + lane
+    float cx[kWaves][kWaveCand + 64];         // candidates (x >= x_lo) in index order: logit
+    uint32_t ci[kWaves][kWaveCand + 64];      //   row index
+    float ce[kWaves][kWaveCand + 64];         //   mass 2^(x*c - R)
     double gab[kFineBins];               // candidate mass above each fine bucket
     float gx[kMaxFinal];                 // members of the cutoff bucket
     uint32_t gi[kMaxFinal];
@@ -407,28 +415,36 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         // lane t owns bins 4t .. 4t+3 (bin 0 = top of the row)
         const int sb0 = 4 * tid;
         const u4v cn = *reinterpret_cast<const u4v*>(&sh.scnt[sb0]);
-        const float sm0 = (float)cn.x * bin_mass(sb0), sm1 = (float)cn.y * bin_mass(sb0 + 1);
-        const float sm2 = (float)cn.z * bin_mass(sb0 + 2), sm3 = (float)cn.w * bin_mass(sb0 + 3);
+        const float bm0 = bin_mass(sb0), bm1 = bin_mass(sb0 + 1);
+        const float bm2 = bin_mass(sb0 + 2), bm3 = bin_mass(sb0 + 3);
+        const float sm0 = (float)cn.x * bm0, sm1 = (float)cn.y * bm1;
+        const float sm2 = (float)cn.z * bm2, sm3 = (float)cn.w * bm3;
+        const float sq0 = sm0 * bm0, sq1 = sm1 * bm1, sq2 = sm2 * bm2, sq3 = sm3 * bm3;
         const float sms = (sm0 + sm1) + (sm2 + sm3);
+        const float sqs = (sq0 + sq1) + (sq2 + sq3);
         const uint32_t scs = cn.x + cn.y + cn.z + cn.w;
         const float smi = wscan_f32(sms);
+        const float sqi = wscan_f32(sqs);
         const uint32_t sci = wscan_u32(scs);
         if (l == 63) {
             sh.fa[w] = smi;
+            sh.fb[w] = sqi;
             sh.ua[w] = sci;
         }
         lds_barrier();
-        float smb = 0.0f, S = 0.0f;
+        float smb = 0.0f, S = 0.0f, sqb = 0.0f, Q = 0.0f;
         uint32_t scb = 0, C = 0;
 #pragma unroll
         for (int i = 0; i < kWaves; ++i) {
-            const float v = sh.fa[i];
+            const float v = sh.fa[i], q = sh.fb[i];
             const uint32_t u = sh.ua[i];
             if (i < w) {
                 smb += v;
+                sqb += q;
                 scb += u;
             }
             S += v;
+            Q += q;
             C += u;
         }
         // row elements per sampled element (estimates only: float is enough)
@@ -444,21 +460,25 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         int first = kSampleBins;
         uint32_t cfirst = 0;
         {
-            float run = smb + (smi - sms);
+            // running sums through this lane's bins (mass, squared mass, count)
+            float run = smb + (smi - sms), qrun = sqb + (sqi - sqs);
             uint32_t crun = scb + (sci - scs);
-#define NIS_SBIN(i, m, n)                                                        \
-    {                                                                            \
-        run += (m);                                                              \
-        crun += (n);                                                             \
-        if (first == kSampleBins && sb0 + (i) >= bceil && S - run <= thr) {      \
-            first = sb0 + (i);                                                   \
-            cfirst = crun;                                                       \
-        }                                                                        \
+#define NIS_SBIN(i, m, q, n)                                                                   \
+    {                                                                                          \
+        run += (m);                                                                            \
+        qrun += (q);                                                                           \
+        crun += (n);                                                                           \
+        const float below = fmaxf(S - run, 0.0f);                                              \
+        const float ucb = below + kSpKappa * __builtin_sqrtf(fmaxf(Q - qrun, 0.0f));          \
+        if (first == kSampleBins && sb0 + (i) >= bceil && crun >= kSpMinAbove && ucb <= thr) { \
+            first = sb0 + (i);                                                                 \
+            cfirst = crun;                                                                     \
+        }                                                                                      \
     }
-            NIS_SBIN(0, sm0, cn.x)
-            NIS_SBIN(1, sm1, cn.y)
-            NIS_SBIN(2, sm2, cn.z)
-            NIS_SBIN(3, sm3, cn.w)
+            NIS_SBIN(0, sm0, sq0, cn.x)
+            NIS_SBIN(1, sm1, sq1, cn.y)
+            NIS_SBIN(2, sm2, sq2, cn.z)
+            NIS_SBIN(3, sm3, sq3, cn.w)
 #undef NIS_SBIN
         }
         {
@@ -495,55 +515,65 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             for (int k = 0; k < kNch; ++k) {
                 const bool hit = mx4[k] >= x_lo;
                 const uint64_t mk = __ballot(hit);
-                if (nw <= (uint32_t)(kWaveEnt - 64) && hit) {  // nw is wave-uniform
-                    const uint32_t pos = nw + lane_rank(mk);
-                    sh.s.ent_x[w][pos] = xv[k];
-                    sh.s.ent_pos[w][pos] = (uint16_t)(k * 64 + l);
-                }
+                const uint32_t pos = nw + lane_rank(mk);
+                const uint32_t slot = (hit && pos < (uint32_t)kWaveEnt) ? pos : (uint32_t)(kWaveEnt + l);
+                sh.s.ent_x[w][slot] = xv[k];
+                sh.s.ent_pos[w][slot] = (uint16_t)(k * 64 + l);
                 nw += (uint32_t)__popcll(mk);
             }
             NIS_TS(4);
             lds_wave_fence();
             // ---- compaction to single candidates, in index order -----------
-            const int ns = 4 * (int)min(nw, (uint32_t)(kWaveEnt - 64));
+            const int ns = 4 * (int)min(nw, (uint32_t)kWaveEnt);
             const float* entf = reinterpret_cast<const float*>(&sh.s.ent_x[w][0]);
             uint32_t nc = 0;
+            // four groups of 64 slots per step, their reads issued together
+            // (slot s < ns + 256 <= 4 * (kWaveEnt + 64) stays inside the list)
             #pragma unroll 1
-            for (int s0 = 0; s0 < ns; s0 += 64) {
-                const int s = s0 + l;
-                float x = -INFINITY;
-                uint32_t idx = 0;
-                if (s < ns) {
-                    x = entf[s];
-                    idx = (uint32_t)(4 * (w * kWaveSlots + (int)sh.s.ent_pos[w][s >> 2]) + (s & 3) - mis);
+            for (int s0 = 0; s0 < ns; s0 += 256) {
+                float xq[4];
+                uint32_t pq[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int s = s0 + 64 * u + l;
+                    xq[u] = entf[s];
+                    pq[u] = sh.s.ent_pos[w][s >> 2];
                 }
-                const bool cand = x >= x_lo;
-                const uint64_t mk = __ballot(cand);
-                if (nc <= (uint32_t)(kWaveCand - 64) && cand) {  // nc is wave-uniform
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int s = s0 + 64 * u + l;
+                    const bool cand = s < ns && xq[u] >= x_lo;
+                    const uint64_t mk = __ballot(cand);
                     const uint32_t pos = nc + lane_rank(mk);
-                    sh.s.cx[w][pos] = x;
-                    sh.s.ci[w][pos] = idx;
+                    const uint32_t slot = (cand && pos < (uint32_t)kWaveCand) ? pos : (uint32_t)(kWaveCand + l);
+                    sh.s.cx[w][slot] = xq[u];
+                    sh.s.ci[w][slot] = (uint32_t)(4 * (w * kWaveSlots + (int)pq[u]) + (s & 3) - mis);
+                    nc += (uint32_t)__popcll(mk);
                 }
-                nc += (uint32_t)__popcll(mk);
             }
             lds_wave_fence();
             // ---- candidate masses and their fine histogram over [x_lo, M] --
-            const int ncc = (int)min(nc, (uint32_t)(kWaveCand - 64));
+            const int ncc = (int)min(nc, (uint32_t)kWaveCand);
             const float inv_w = (M > x_lo) ? (float)kFineBins / (M - x_lo) : 0.0f;
             double g = 0.0;
+            // two groups of 64 per step (indices past the list read its spare slots)
             #pragma unroll 1
-            for (int j0 = 0; j0 < ncc; j0 += 64) {
-                const int j = j0 + l;
-                if (j < ncc) {
-                    const float x = sh.s.cx[w][j];
-                    const float e = mass_of(x, c, R);
-                    sh.s.ce[w][j] = e;
-                    g += (double)e;
-                    const int b = fine_bucket(x, x_lo, inv_w);
-                    atomicAdd(&sh.fcnt[b], 1u);
-                    atomicAdd(&sh.fmass[b], (unsigned long long)((double)e * kFix));
-                    atomicMax(&sh.fkmax[b], key32(x));
-                }
+            for (int j0 = 0; j0 < ncc; j0 += 128) {
+                const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
+                const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
+#define NIS_CAND(j, x)                                                            \
+    if ((j) < ncc) {                                                              \
+        const float e = mass_of((x), c, R);                                       \
+        sh.s.ce[w][(j)] = e;                                                      \
+        g += (double)e;                                                           \
+        const int b = fine_bucket((x), x_lo, inv_w);                              \
+        atomicAdd(&sh.fcnt[b], 1u);                                               \
+        atomicAdd(&sh.fmass[b], (unsigned long long)((double)e * kFix));          \
+        atomicMax(&sh.fkmax[b], key32((x)));                                      \
+    }
+                NIS_CAND(ja, xa)
+                NIS_CAND(jb, xb)
+#undef NIS_CAND
             }
             g = wsum_f64(g);
             if (l == 0) {
@@ -558,7 +588,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
 #pragma unroll
             for (int i = 0; i < kWaves; ++i) {
                 Gc += sh.db[i];
-                ovf = ovf || sh.ua[i] > (uint32_t)(kWaveEnt - 64) || sh.ub[i] > (uint32_t)(kWaveCand - 64);
+                ovf = ovf || sh.ua[i] > (uint32_t)kWaveEnt || sh.ub[i] > (uint32_t)kWaveCand;
             }
             if (ovf) {
                 reject = NIS_REJECT_CAPACITY;
@@ -587,7 +617,8 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 const bool kB = cB != 0 && (GB - (double)mass_of(unkey32(sh.fkmax[bB]), c, R) <= pZR);
                 sh.s.gab[bA] = GA;
                 sh.s.gab[bB] = GB;
-                const int lowk = wave_min(kB ? bB : (kA ? bA : kFineBins));
+                const int lowk =
+                    (int)(-wmax_f32(-(float)(kB ? bB : (kA ? bA : kFineBins))));  // DPP wave min
                 if (l == 0) sh.ia[w] = lowk;
                 lds_barrier();
                 int bstar = kFineBins;
@@ -601,19 +632,21 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                     const double gab = sh.s.gab[bstar];
                     // ---- gather the cutoff bucket's members ------------------
                     #pragma unroll 1
-                    for (int j0 = 0; j0 < ncc; j0 += 64) {
-                        const int j = j0 + l;
-                        if (j < ncc) {
-                            const float x = sh.s.cx[w][j];
-                            if (fine_bucket(x, x_lo, inv_w) == bstar) {
-                                const uint32_t s = atomicAdd(&sh.gcount, 1u);
-                                if (s < (uint32_t)kMaxFinal) {
-                                    sh.s.gx[s] = x;
-                                    sh.s.gi[s] = sh.s.ci[w][j];
-                                    sh.s.ge[s] = sh.s.ce[w][j];
-                                }
-                            }
-                        }
+                    for (int j0 = 0; j0 < ncc; j0 += 128) {
+                        const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
+                        const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
+#define NIS_GATHER(j, x)                                                    \
+    if ((j) < ncc && fine_bucket((x), x_lo, inv_w) == bstar) {              \
+        const uint32_t s = atomicAdd(&sh.gcount, 1u);                       \
+        if (s < (uint32_t)kMaxFinal) {                                      \
+            sh.s.gx[s] = (x);                                               \
+            sh.s.gi[s] = sh.s.ci[w][(j)];                                   \
+            sh.s.ge[s] = sh.s.ce[w][(j)];                                   \
+        }                                                                   \
+    }
+                        NIS_GATHER(ja, xa)
+                        NIS_GATHER(jb, xb)
+#undef NIS_GATHER
                     }
                     lds_barrier();
                     NIS_TS(7);
@@ -639,13 +672,13 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                                 pre += before ? (double)ej : 0.0;
                             }
                             const bool kept = valid && (gab + pre - (double)em <= pZR);
-                            // the last kept member: smallest key, then largest index
-                            const uint64_t comp =
-                                kept ? (((uint64_t)km << 32) | (uint64_t)(0xFFFFFFFFu - im)) : ~0ull;
-                            const uint64_t cmin = wave_min(comp);
+                            // the last kept member: smallest value, then largest
+                            // index (DPP maxima; indices < 2^24 are exact in float)
+                            const float xcut = -wmax_f32(kept ? -xm : -INFINITY);
+                            const float icut = wmax_f32((kept && xm == xcut) ? (float)im : -1.0f);
                             if (l == 0) {
-                                sh.cut_key = (uint32_t)(cmin >> 32);
-                                sh.cut_idx = 0xFFFFFFFFu - (uint32_t)cmin;
+                                sh.cut_key = key32(xcut);
+                                sh.cut_idx = (uint32_t)icut;
                             }
                         }
                         NIS_RNG_DRAW()
@@ -656,15 +689,19 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                         double kw = 0.0;
                         uint32_t nk = 0;
                         #pragma unroll 1
-                        for (int j0 = 0; j0 < ncc; j0 += 64) {
-                            const int j = j0 + l;
-                            if (j < ncc) {
-                                const uint32_t k = key32(sh.s.cx[w][j]);
-                                const uint32_t id = sh.s.ci[w][j];
-                                if (k > kc || (k == kc && id <= ic)) {
-                                    kw += (double)sh.s.ce[w][j];
-                                    ++nk;
-                                }
+                        for (int j0 = 0; j0 < ncc; j0 += 128) {
+                            const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
+                            const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
+                            const uint32_t ia = sh.s.ci[w][ja], ib = sh.s.ci[w][jb];
+                            const float ea = sh.s.ce[w][ja], eb = sh.s.ce[w][jb];
+                            const uint32_t ka = key32(xa), kb = key32(xb);
+                            if (ja < ncc && (ka > kc || (ka == kc && ia <= ic))) {
+                                kw += (double)ea;
+                                ++nk;
+                            }
+                            if (jb < ncc && (kb > kc || (kb == kc && ib <= ic))) {
+                                kw += (double)eb;
+                                ++nk;
                             }
                         }
                         kw = wsum_f64(kw);
@@ -1191,8 +1228,9 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             for (int i = 0; i < kWaves; ++i) kept_total += sh.ia[i];
             const double zkM = zk * rho;
             const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
+            // `reject`: why the sparse route declined this row (0 without top-p)
             write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp, zkM,
-                             topp ? ZR * rho : 0.0, u, prob, (uint64_t)kept_total, 1);
+                             topp ? ZR * rho : 0.0, u, prob, (uint64_t)kept_total, 1, reject);
         }
     }
     if (tid == 0) {

@@ -28,6 +28,16 @@ def _normal(seed, B, V, sigma):
     return (g.standard_normal((B, V), dtype=np.float32) * np.float32(sigma)).astype(np.float32)
 
 
+def rotation(x: np.ndarray, i: int) -> np.ndarray:
+    """The i-th of the benchmark's rotated batches: rows permuted (PCG64 seed
+    i) and every row rolled by 997*i columns; rotation 0 is x itself.  Same
+    distribution, distinct rows and addresses."""
+    if i == 0:
+        return x
+    perm = np.random.Generator(np.random.PCG64(i)).permutation(x.shape[0])
+    return np.ascontiguousarray(np.roll(x[perm], 997 * i, axis=1))
+
+
 def headline(B=256, V=50257):
     return _normal(7, B, V, 3.0)
 

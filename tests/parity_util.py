@@ -56,6 +56,7 @@ def compare(gpu, ref, greedy):
     B = len(r_tok)
     rej = g_st["reject"][g_st["kernel"] == 2]
     rep = {"rows": B, "fast_rows": int((g_st["kernel"] == 1).sum()),
+           "sparse_rows": int(((g_st["kernel"] == 1) & (g_st["reject"] == 0)).sum()),
            "rejects": {int(k): int(n) for k, n in zip(*np.unique(rej, return_counts=True))}}
     assert np.array_equal(g_states, r_states), \
         f"rng state mismatch on rows {np.nonzero((g_states != r_states).any(1))[0][:10].tolist()}"

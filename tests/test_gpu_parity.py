@@ -116,6 +116,23 @@ def test_config_sampled(sampler, name):
     # its rows on (the result is identical either way).
     min_fast = {"c1": 1.0, "c2": 0.5, "c3": 0.9, "c5": 0.9, "headline": 1.0}[name]
     assert rep["fast_rows"] >= min_fast * w.B, rep
+    # few kept tokens: every row must stay on the sparse top-p route (the
+    # dense route is correct but slower, and one such row sets the launch time)
+    if name in ("c1", "c3", "headline"):
+        assert rep["sparse_rows"] == w.B, rep
+
+
+def test_headline_rotations_stay_sparse(sampler):
+    """All eight batches bench.py rotates through: parity, and every row on
+    the sparse top-p route."""
+    from nimbus_sampler import workloads
+    w = workloads.WORKLOADS["headline"]
+    x0 = w.make(w.B)
+    for i in range(8):
+        rep = _check(sampler, workloads.rotation(x0, i), w.V,
+                     _params(temperature=w.temperature, top_p=w.top_p), w.seeds,
+                     label=f"headline-rot{i}")
+        assert rep["sparse_rows"] == w.B, rep
 
 
 @pytest.mark.parametrize("name", ["c1", "c3", "headline"])
