@@ -9,6 +9,24 @@
  * Every function follows the reference operation by operation in IEEE f64
  * (no fast-math, no FMA contraction, glibc `exp`), citing the lines of
  * /root/reference/src/sampler.rs it restates.
+ *
+ * How each function is pinned (tests/test_oracle.py):
+ *   oracle_rng_*                  published SplitMix64(0) stream, big-integer
+ *                                 KATs (tests/golden/rng_kats.json), GF(2)
+ *                                 linearity, sampler.rs:230-239
+ *   oracle_apply_repetition_penalty  sampler.rs:251-257, brute force
+ *   oracle_top_k_filter           sampler.rs:241-249, brute force on tiny rows
+ *   oracle_top_p_filter           sampler.rs:259-266 (p = 0), exact-rational
+ *                                 brute force of the keep rule on tiny rows,
+ *                                 prefix / tie-group invariants
+ *   oracle_sample                 sampler.rs:223-228, exact-rational inverse
+ *                                 CDF on 4000 tiny rows, special rows
+ *   oracle_sample_batch           equals sequential oracle_sample
+ * Parity unpinned (no reference build or value fixture exists here): the
+ * bit pattern of `exp` (Rust's f64::exp lowers to the platform libm, glibc
+ * here) and the last-bit rounding of the sequential sorted-order and CDF
+ * sums at exact boundaries; the GPU tests treat rows within 1e-6 of such a
+ * boundary as boundary rows and count them.
  */
 #ifndef NIMBUS_SAMPLER_ORACLE_H
 #define NIMBUS_SAMPLER_ORACLE_H

@@ -106,3 +106,16 @@ def test_sampling_params_defaults_mirror_reference():
     assert ns.SamplingParams(temperature=-1.0).greedy()
     c = ns.SamplingParams(temperature=0.8, top_p=0.9).to_c()
     assert c.temperature == np.float32(0.8) and c.top_p == np.float32(0.9) and c.reserved == 0
+
+
+def test_cpp_header_compiles_as_cpp17(tmp_path):
+    """include/nimbus_sampler.hpp is self-contained C++17 over the C ABI."""
+    import subprocess
+    src = tmp_path / "t.cpp"
+    src.write_text('#include "nimbus_sampler.hpp"\n'
+                   'static_assert(sizeof(nis_params) == 24, "nis_params layout");\n'
+                   'int main() { nimbus::SamplingParams p; return p.greedy() ? 1 : 0; }\n')
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-fsyntax-only",
+                        "-I" + os.path.join(ROOT, "include"), str(src)],
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout
