@@ -50,8 +50,13 @@ typedef const __attribute__((address_space(1))) float* gfp;
 constexpr int kNch = 26;                      // float4 chunks per lane
 constexpr int kWaveSlots = kNch * 64;         // float4 slots per wave
 constexpr int kFastMaxV = kBlock * 4 * kNch - 3;
-constexpr int kSampleBins = 2048;             // 32 octaves at 1/64 octave
-constexpr float kSampleRes = 64.0f;
+constexpr int kSampleBins = 512;              // 32 octaves at 1/16 octave
+constexpr float kSampleRes = 16.0f;
+constexpr int kBinsPerLane = kSampleBins / 64;
+// 2^-(i + 0.5)/16: the centre mass of bin 8l + i relative to bin 8l's top
+constexpr float kBinStep[8] = {0.9785720705986023f, 0.9370838403701782f, 0.8973545432090759f,
+                               0.8593096733093262f, 0.8228777647018433f, 0.7879904508590698f,
+                               0.7545822262763977f, 0.7225903868675232f};
 constexpr int kFineBins = 1024;
 constexpr int kMaxFinal = 64;
 constexpr int kLaneCap = 16;                  // dense route: window entries per lane
@@ -85,6 +90,7 @@ struct SparseShared {
     // writes of lanes with nothing to append (branch-free appends)
     f4v ent_x[kWaves][kWaveEnt + 64];         // listed float4s, wave-compacted in index order
     uint16_t ent_pos[kWaves][kWaveEnt + 64];  //   their chunk * 64 + lane
+    uint16_t cb[kWaves][kWaveCand + 64];      // candidates' fine bucket
     float cx[kWaves][kWaveCand + 64];         // candidates (x >= x_lo) in index order: logit
     uint32_t ci[kWaves][kWaveCand + 64];      //   row index
     float ce[kWaves][kWaveCand + 64];         //   mass 2^(x*c - R)
@@ -94,17 +100,24 @@ struct SparseShared {
     float ge[kMaxFinal];
 };
 
+// Branches cost about as much as ten VALU instructions here, so the tail
+// avoids exec-mask branches: lanes with nothing to store write their own
+// slot of `junk`, and masked-off histogram updates go to a dummy bin past
+// the end of each histogram.
 struct FastShared {
-    uint32_t scnt[kSampleBins];
-    uint32_t fcnt[kFineBins];
-    unsigned long long fmass[kFineBins];
-    uint32_t fkmax[kFineBins];
-    uint32_t fkmin[kFineBins];
+    uint32_t scnt[kSampleBins + 64];        // [kSampleBins + lane]: dummy bins
+    uint32_t fcnt[kFineBins + 64];          // [kFineBins + lane]: dummy buckets
+    unsigned long long fmass[kFineBins + 64];
+    uint32_t fkmax[kFineBins + 64];
+    uint32_t fkmin[kFineBins + 64];
+    double junk[kBlock];                    // per-lane spare store slot
     union {
         DenseShared d;
         SparseShared s;
     };
     uint64_t rng[4];                 // the row's RNG state after its one draw
+    unsigned long long wfix[kWaves];  // kept cutoff-bucket mass per wave (2^-40 fixed point)
+    uint32_t wcnt[kWaves];           // kept cutoff-bucket members per wave
     uint32_t ncand;
     uint32_t overflow;
     uint32_t gcount;
@@ -238,19 +251,29 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const float h0 = rowp[0], h1 = rowp[1], h2 = rowp[2];
     const float t0 = rowp[V - 3], t1 = rowp[V - 2], t2 = rowp[V - 1];
 
+    // LDS store by the lanes where `cond` holds; the other lanes write their
+    // own spare slot, so no exec-mask branch is needed
+#define NIS_PUT(cond, ref, val)                                                             \
+    do {                                                                                    \
+        auto* nis_dst_ = (cond) ? &(ref) : reinterpret_cast<decltype(&(ref))>(&sh.junk[tid]); \
+        *nis_dst_ = (val);                                                                  \
+    } while (0)
+
     // LDS set-up while the loads are in flight
-    for (int i = tid; i < kSampleBins; i += kBlock) sh.scnt[i] = 0u;
-    for (int i = tid; i < kFineBins; i += kBlock) {
-        sh.fcnt[i] = 0u;
-        sh.fmass[i] = 0ull;
-        sh.fkmax[i] = 0u;
-        sh.fkmin[i] = 0xFFFFFFFFu;
+    static_assert(kSampleBins == kBlock, "one sample bin per lane to clear");
+    sh.scnt[tid] = 0u;
+#pragma unroll
+    for (int j = 0; j < kFineBins / kBlock; ++j) {
+        sh.fcnt[tid + j * kBlock] = 0u;
+        sh.fmass[tid + j * kBlock] = 0ull;
+        sh.fkmax[tid + j * kBlock] = 0u;
+        sh.fkmin[tid + j * kBlock] = 0xFFFFFFFFu;
     }
-    if (tid == 0) {
-        sh.ncand = 0u;
-        sh.overflow = 0u;
-        sh.gcount = 0u;
-    }
+    NIS_PUT(tid == 0, sh.ncand, 0u);
+    NIS_PUT(tid == 0, sh.overflow, 0u);
+    NIS_PUT(tid == 0, sh.gcount, 0u);
+    NIS_PUT(tid < kWaves, sh.wfix[min(tid, kWaves - 1)], 0ull);
+    NIS_PUT(tid < kWaves, sh.wcnt[min(tid, kWaves - 1)], 0u);
 
     // slots not fully inside the row get their exact values or -inf; only
     // the one or two waves holding such slots take the (wave-uniform) branch.
@@ -265,6 +288,9 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             xv[k] = fix_slot(xv[k], slot0x + (k) * 64, f_lo, f_hi, mis, V, h0, h1, h2, t0, t1, t2); \
     } while (0)
 #define NIS_INDEX(k, q) (4 * (slot0x + 64 * (k)) + (q) - mis)
+    // does this wave hold any slot not fully inside the row?  Only such
+    // waves run the per-chunk checks (each one is a branch).
+    const bool edge_wave = (w * kWaveSlots < f_lo) || (w * kWaveSlots + kWaveSlots - 1 > f_hi);
 
     // ------------------------------------------------------------------
     // greedy (sampler.rs:172-181): first index of the maximum; NaN is
@@ -272,28 +298,31 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     if (!sampling) {
         float best = -INFINITY;
         int bidx = INT_MAX;
-#pragma unroll
-        for (int k = 0; k < kNch; ++k) {
-            NIS_FIX(k);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float x = elem(xv[k], q);
-                if (x > best) {
-                    best = x;
-                    bidx = NIS_INDEX(k, q);
-                }
-            }
+#define NIS_GREEDY(FIX)                                      \
+    _Pragma("unroll") for (int k = 0; k < kNch; ++k) {      \
+        if (FIX) NIS_FIX(k);                                 \
+        _Pragma("unroll") for (int q = 0; q < 4; ++q) {     \
+            const float x = elem(xv[k], q);                  \
+            if (x > best) {                                  \
+                best = x;                                    \
+                bidx = NIS_INDEX(k, q);                      \
+            }                                                \
+        }                                                    \
+    }
+        if (edge_wave) {
+            NIS_GREEDY(true)
+        } else {
+            NIS_GREEDY(false)
         }
+#undef NIS_GREEDY
         // wave max, then its lowest index (lanes interleave indices chunk by
         // chunk, so the lowest lane holding the max need not hold the lowest index)
         // (DPP max of the negated index; indices < 2^24 are exact in float)
         const float wb = wmax_f32(best);
         const float nwi = wmax_f32((best == wb && bidx != INT_MAX) ? -(float)bidx : -INFINITY);
         const int wi = (nwi > -INFINITY) ? (int)(-nwi) : INT_MAX;
-        if (l == 0) {
-            sh.fa[w] = wb;
-            sh.ia[w] = wi;
-        }
+        NIS_PUT(l == 0, sh.fa[w], wb);
+        NIS_PUT(l == 0, sh.ia[w], wi);
         lds_barrier();
         if (tid == 0) {
             float b = sh.fa[0];
@@ -316,7 +345,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const bool topp = p < 1.0f;  // p <= 0 is excluded by fast_eligible
 
     // wave-local reference from the wave's first chunk (no barrier)
-    NIS_FIX(0);
+    if (edge_wave) NIS_FIX(0);
     const float m0 = wmax_f32(max4(xv[0]));
     const float Rw = (m0 > -INFINITY && fabsf(m0 * c) < 1e30f) ? ceilf(m0 * c) : 0.0f;
 
@@ -328,29 +357,33 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     float mx4[kNch];
     float cz = c, Rz = Rw;
     asm volatile("" : "+v"(cz), "+v"(Rz));
-#pragma unroll
-    for (int k = 0; k < kNch; ++k) {
-        if (k > 0) NIS_FIX(k);
-        const f4v x = xv[k];
-        f4v e;
-        e.x = mass_of(x.x, cz, Rz);
-        e.y = mass_of(x.y, cz, Rz);
-        e.z = mass_of(x.z, cz, Rz);
-        e.w = mass_of(x.w, cz, Rz);
-        z += (double)((e.x + e.y) + (e.z + e.w));
-        mx4[k] = max4(x);
-        mx = fmaxf(mx, mx4[k]);
+#define NIS_STREAM(FIX)                                      \
+    _Pragma("unroll") for (int k = 0; k < kNch; ++k) {      \
+        if (FIX && k > 0) NIS_FIX(k);                        \
+        const f4v x = xv[k];                                 \
+        f4v e;                                               \
+        e.x = mass_of(x.x, cz, Rz);                          \
+        e.y = mass_of(x.y, cz, Rz);                          \
+        e.z = mass_of(x.z, cz, Rz);                          \
+        e.w = mass_of(x.w, cz, Rz);                          \
+        z += (double)((e.x + e.y) + (e.z + e.w));            \
+        mx4[k] = max4(x);                                    \
+        mx = fmaxf(mx, mx4[k]);                              \
     }
+    if (edge_wave) {
+        NIS_STREAM(true)
+    } else {
+        NIS_STREAM(false)
+    }
+#undef NIS_STREAM
 
     // ---- T1: row max, reference R, Z ---------------------------------------
     NIS_TS(1);
     mx = wmax_f32(mx);
     z = wsum_f64(z);
-    if (l == 0) {
-        sh.fb[w] = mx;
-        sh.da[w] = z;
-        sh.fc[w] = Rw;
-    }
+    NIS_PUT(l == 0, sh.fb[w], mx);
+    NIS_PUT(l == 0, sh.da[w], z);
+    NIS_PUT(l == 0, sh.fc[w], Rw);
     lds_barrier();
     float M = sh.fb[0];
 #pragma unroll
@@ -376,77 +409,62 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const double pZR = (double)p * ZR;
     // The row's RNG state: one word per lane 0..3 of wave 0 (a vector load,
     // so no LDS wait depends on it), consumed just before the walk.
-    uint64_t rsv = 0;
-    if (w == 0 && l < 4)
-        rsv = ((const __attribute__((address_space(1))) uint64_t*)(a.rng + 4 * (int64_t)row))[l];
+    const uint64_t rsv =
+        ((const __attribute__((address_space(1))) uint64_t*)(a.rng + 4 * (int64_t)row))[l & 3];
     // sampler.rs:209: the row's single RNG advance, into LDS (written back to
     // memory only when the row completes here)
 #define NIS_RNG_DRAW()                                                                          \
     if (w == 0) {                                                                               \
         uint64_t st[4];                                                                         \
-        for (int j = 0; j < 4; ++j)                                                             \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j)                                           \
             st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j); \
         const double u0 = rng_next_f64(st);                                                     \
-        if (l == 0) {                                                                           \
-            sh.bd[1] = u0;                                                                      \
-            sh.rng[0] = st[0];                                                                  \
-            sh.rng[1] = st[1];                                                                  \
-            sh.rng[2] = st[2];                                                                  \
-            sh.rng[3] = st[3];                                                                  \
-        }                                                                                       \
+        NIS_PUT(l == 0, sh.bd[1], u0);                                                          \
+        NIS_PUT(l == 1, sh.rng[0], st[0]);                                                      \
+        NIS_PUT(l == 2, sh.rng[1], st[1]);                                                      \
+        NIS_PUT(l == 3, sh.rng[2], st[2]);                                                      \
+        NIS_PUT(l == 4, sh.rng[3], st[3]);                                                      \
     }
 
     uint32_t reject = NIS_REJECT_NONE;  // reason of a failed sparse attempt
     if (topp) {
-        // count histogram of chunks 0 and 1 (the sample), relative to R
+        // count histogram of chunks 0 and 1 (the sample), 1/16-octave bins below R
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const float x = elem(xv[q >> 2], q & 3);
-            if (x > -INFINITY) {
-                const float t = fmaf(x, c, -R);
-                const int b = (int)fminf(fmaxf(-t * kSampleRes, 0.0f), (float)(kSampleBins - 1));
-                atomicAdd(&sh.scnt[b], 1u);
-            }
+            const float t = fmaf(x, c, -R);
+            const int b = (x > -INFINITY)
+                              ? (int)fminf(fmaxf(-t * kSampleRes, 0.0f), (float)(kSampleBins - 1))
+                              : kSampleBins + l;  // -inf (outside the row or masked): dummy bin
+            atomicAdd(&sh.scnt[b], 1u);
         }
         lds_barrier();
         NIS_TS(2);
 
-        // ---- S1: threshold x_lo from the sample (block-wide scan) --------
-        // lane t owns bins 4t .. 4t+3 (bin 0 = top of the row)
-        const int sb0 = 4 * tid;
-        const u4v cn = *reinterpret_cast<const u4v*>(&sh.scnt[sb0]);
-        const float bm0 = bin_mass(sb0), bm1 = bin_mass(sb0 + 1);
-        const float bm2 = bin_mass(sb0 + 2), bm3 = bin_mass(sb0 + 3);
-        const float sm0 = (float)cn.x * bm0, sm1 = (float)cn.y * bm1;
-        const float sm2 = (float)cn.z * bm2, sm3 = (float)cn.w * bm3;
-        const float sq0 = sm0 * bm0, sq1 = sm1 * bm1, sq2 = sm2 * bm2, sq3 = sm3 * bm3;
-        const float sms = (sm0 + sm1) + (sm2 + sm3);
-        const float sqs = (sq0 + sq1) + (sq2 + sq3);
-        const uint32_t scs = cn.x + cn.y + cn.z + cn.w;
-        const float smi = wscan_f32(sms);
-        const float sqi = wscan_f32(sqs);
-        const uint32_t sci = wscan_u32(scs);
-        if (l == 63) {
-            sh.fa[w] = smi;
-            sh.fb[w] = sqi;
-            sh.ua[w] = sci;
-        }
-        lds_barrier();
-        float smb = 0.0f, S = 0.0f, sqb = 0.0f, Q = 0.0f;
-        uint32_t scb = 0, C = 0;
+        // ---- S1: threshold x_lo.  Every wave evaluates the whole histogram
+        // itself (same inputs, same operations, so the same result) instead
+        // of sharing partial scans through two more barriers.
+        // Lane l owns bins 8l .. 8l+7; bin b holds t in (-(b+1)/16, -b/16].
+        const u4v c0 = *reinterpret_cast<const u4v*>(&sh.scnt[kBinsPerLane * l]);
+        const u4v c1 = *reinterpret_cast<const u4v*>(&sh.scnt[kBinsPerLane * l + 4]);
+        const uint32_t cnt[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float lane_bm = __builtin_amdgcn_exp2f(-(float)(kBinsPerLane * l) / kSampleRes);
+        float bm[8], bmass[8], bsq[8];
+        float ms = 0.0f, qs = 0.0f;
+        uint32_t cs = 0;
 #pragma unroll
-        for (int i = 0; i < kWaves; ++i) {
-            const float v = sh.fa[i], q = sh.fb[i];
-            const uint32_t u = sh.ua[i];
-            if (i < w) {
-                smb += v;
-                sqb += q;
-                scb += u;
-            }
-            S += v;
-            Q += q;
-            C += u;
+        for (int i = 0; i < 8; ++i) {
+            bm[i] = lane_bm * kBinStep[i];  // 2^-(b + 0.5)/16, the bin's centre mass
+            bmass[i] = (float)cnt[i] * bm[i];
+            bsq[i] = bmass[i] * bm[i];
+            ms += bmass[i];
+            qs += bsq[i];
+            cs += cnt[i];
         }
+        const float mI = wscan_f32(ms), qI = wscan_f32(qs);
+        const uint32_t cI = wscan_u32(cs);
+        const float S = bcast_f32(mI, 63), Q = bcast_f32(qI, 63);
+        const uint32_t C = bcast_u32(cI, 63);
         // row elements per sampled element (estimates only: float is enough)
         const float F = (float)V * __builtin_amdgcn_rcpf((float)max(C, 1u));
         const float rem = (1.0f - p) * (float)ZR;  // mass top-p removes
@@ -461,48 +479,26 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         uint32_t cfirst = 0;
         {
             // running sums through this lane's bins (mass, squared mass, count)
-            float run = smb + (smi - sms), qrun = sqb + (sqi - sqs);
-            uint32_t crun = scb + (sci - scs);
-#define NIS_SBIN(i, m, q, n)                                                                   \
-    {                                                                                          \
-        run += (m);                                                                            \
-        qrun += (q);                                                                           \
-        crun += (n);                                                                           \
-        const float below = fmaxf(S - run, 0.0f);                                              \
-        const float ucb = below + kSpKappa * __builtin_sqrtf(fmaxf(Q - qrun, 0.0f));          \
-        if (first == kSampleBins && sb0 + (i) >= bceil && crun >= kSpMinAbove && ucb <= thr) { \
-            first = sb0 + (i);                                                                 \
-            cfirst = crun;                                                                     \
-        }                                                                                      \
-    }
-            NIS_SBIN(0, sm0, sq0, cn.x)
-            NIS_SBIN(1, sm1, sq1, cn.y)
-            NIS_SBIN(2, sm2, sq2, cn.z)
-            NIS_SBIN(3, sm3, sq3, cn.w)
-#undef NIS_SBIN
-        }
-        {
-            const uint64_t qm = __ballot(first < kSampleBins);
-            if (qm) {
-                const int L = __ffsll((long long)qm) - 1;
-                first = (int)bcast_u32((uint32_t)first, L);
-                cfirst = bcast_u32(cfirst, L);
-            }
-            if (l == 0) {
-                sh.ia[w] = qm ? first : kSampleBins;
-                sh.ub[w] = cfirst;
-            }
-        }
-        lds_barrier();
-        int bsel = kSampleBins;
-        uint32_t csel = 0;
+            float run = mI - ms, qrun = qI - qs;
+            uint32_t crun = cI - cs;
 #pragma unroll
-        for (int i = 0; i < kWaves; ++i) {
-            if (bsel == kSampleBins && sh.ia[i] < kSampleBins) {
-                bsel = sh.ia[i];
-                csel = sh.ub[i];
+            for (int i = 0; i < 8; ++i) {
+                run += bmass[i];
+                qrun += bsq[i];
+                crun += cnt[i];
+                const float ucb = fmaxf(S - run, 0.0f) +
+                                  kSpKappa * __builtin_amdgcn_sqrtf(fmaxf(Q - qrun, 0.0f));
+                const int b = kBinsPerLane * l + i;
+                const bool okb = b >= bceil && crun >= kSpMinAbove && ucb <= thr;
+                const bool take = okb && first == kSampleBins;
+                first = take ? b : first;
+                cfirst = take ? crun : cfirst;
             }
         }
+        const uint64_t qm = __ballot(first < kSampleBins);
+        const int qL = qm ? (__ffsll((long long)qm) - 1) : 0;
+        const int bsel = qm ? (int)bcast_u32((uint32_t)first, qL) : kSampleBins;
+        const uint32_t csel = bcast_u32(cfirst, qL);
         NIS_TS(3);
         reject = NIS_REJECT_CAPACITY;
         if (bsel < kSampleBins && F * (float)csel <= (float)kSpEstCap) {
@@ -562,25 +558,26 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
                 const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
 #define NIS_CAND(j, x)                                                            \
-    if ((j) < ncc) {                                                              \
-        const float e = mass_of((x), c, R);                                       \
+    {                                                                             \
+        const bool ok = (j) < ncc;                                                \
+        const float xs = ok ? (x) : x_lo;                                         \
+        const float e = ok ? mass_of(xs, c, R) : 0.0f;                            \
+        const int b = ok ? fine_bucket(xs, x_lo, inv_w) : kFineBins + l;          \
         sh.s.ce[w][(j)] = e;                                                      \
+        sh.s.cb[w][(j)] = (uint16_t)b;                                            \
         g += (double)e;                                                           \
-        const int b = fine_bucket((x), x_lo, inv_w);                              \
         atomicAdd(&sh.fcnt[b], 1u);                                               \
         atomicAdd(&sh.fmass[b], (unsigned long long)((double)e * kFix));          \
-        atomicMax(&sh.fkmax[b], key32((x)));                                      \
+        atomicMax(&sh.fkmax[b], key32(xs));                                       \
     }
                 NIS_CAND(ja, xa)
                 NIS_CAND(jb, xb)
 #undef NIS_CAND
             }
             g = wsum_f64(g);
-            if (l == 0) {
-                sh.db[w] = g;
-                sh.ua[w] = nw;
-                sh.ub[w] = nc;
-            }
+            NIS_PUT(l == 0, sh.db[w], g);
+            NIS_PUT(l == 0, sh.ua[w], nw);
+            NIS_PUT(l == 0, sh.ub[w], nc);
             lds_barrier();
             NIS_TS(5);
             double Gc = 0.0;
@@ -604,12 +601,11 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 const double mB = (double)sh.fmass[bB] * (1.0 / kFix);
                 const double mt = mA + mB;
                 const double inc = wscan_f64(mt);
-                if (l == 63) sh.da[w] = inc;
+                NIS_PUT(l == 63, sh.da[w], inc);
                 lds_barrier();
                 double gbase = 0.0;
 #pragma unroll
-                for (int i = 0; i < kWaves; ++i)
-                    if (i < w) gbase += sh.da[i];
+                for (int i = 0; i < kWaves; ++i) gbase += (i < w) ? sh.da[i] : 0.0;
                 const double GA = gbase + (inc - mt);  // candidate mass above bucket bA
                 const double GB = GA + mA;
                 // sampler.rs:150 for the largest element of the bucket
@@ -619,7 +615,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 sh.s.gab[bB] = GB;
                 const int lowk =
                     (int)(-wmax_f32(-(float)(kB ? bB : (kA ? bA : kFineBins))));  // DPP wave min
-                if (l == 0) sh.ia[w] = lowk;
+                NIS_PUT(l == 0, sh.ia[w], lowk);
                 lds_barrier();
                 int bstar = kFineBins;
 #pragma unroll
@@ -630,30 +626,44 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                     reject = NIS_REJECT_CAPACITY;
                 } else {
                     const double gab = sh.s.gab[bstar];
-                    // ---- gather the cutoff bucket's members ------------------
+                    // ---- gather the cutoff bucket's members; sum the mass and
+                    // count of the candidates above it (all kept) per wave ------
+                    double sw = 0.0;
+                    uint32_t sn = 0;
                     #pragma unroll 1
                     for (int j0 = 0; j0 < ncc; j0 += 128) {
                         const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
-                        const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
-#define NIS_GATHER(j, x)                                                    \
-    if ((j) < ncc && fine_bucket((x), x_lo, inv_w) == bstar) {              \
-        const uint32_t s = atomicAdd(&sh.gcount, 1u);                       \
-        if (s < (uint32_t)kMaxFinal) {                                      \
-            sh.s.gx[s] = (x);                                               \
-            sh.s.gi[s] = sh.s.ci[w][(j)];                                   \
-            sh.s.ge[s] = sh.s.ce[w][(j)];                                   \
-        }                                                                   \
+                        const int ba = sh.s.cb[w][ja], bb = sh.s.cb[w][jb];
+                        const float ea = sh.s.ce[w][ja], eb = sh.s.ce[w][jb];
+                        const bool sa = ja < ncc && ba > bstar, sb = jb < ncc && bb > bstar;
+                        sw += (sa ? (double)ea : 0.0) + (sb ? (double)eb : 0.0);
+                        sn += (sa ? 1u : 0u) + (sb ? 1u : 0u);
+#define NIS_GATHER(j, b, e)                                                              \
+    {                                                                                    \
+        const bool mem = (j) < ncc && (b) == bstar;                                      \
+        const uint32_t s =                                                               \
+            atomicAdd(mem ? &sh.gcount : reinterpret_cast<uint32_t*>(&sh.junk[tid]), 1u); \
+        const bool put = mem && s < (uint32_t)kMaxFinal;                                 \
+        const uint32_t sc = min(s, (uint32_t)kMaxFinal - 1);                             \
+        NIS_PUT(put, sh.s.gx[sc], sh.s.cx[w][(j)]);                                      \
+        NIS_PUT(put, sh.s.gi[sc], sh.s.ci[w][(j)]);                                      \
+        NIS_PUT(put, sh.s.ge[sc], (e));                                                  \
     }
-                        NIS_GATHER(ja, xa)
-                        NIS_GATHER(jb, xb)
+                        NIS_GATHER(ja, ba, ea)
+                        NIS_GATHER(jb, bb, eb)
 #undef NIS_GATHER
                     }
+                    sw = wsum_f64(sw);
+                    sn = wsum_u32(sn);
+                    NIS_PUT(l == 0, sh.wtot[w], sw);
+                    NIS_PUT(l == 0, sh.ua[w], sn);
                     lds_barrier();
                     NIS_TS(7);
                     if (sh.gcount != nstar) {
                         reject = NIS_REJECT_BUCKET;
                     } else {
-                        // ---- exact rule inside the bucket (wave 0) -----------
+                        // ---- wave 0: exact rule inside the bucket, the draw, and
+                        // the wave that holds the crossing -----------------------
                         if (w == 0) {
                             const int n = (int)nstar;
                             const bool valid = l < n;
@@ -665,98 +675,84 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                             // reference's stable descending order
                             double pre = 0.0;
                             #pragma unroll 1
-                            for (int j = 0; j < n; ++j) {
-                                const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
-                                const float ej = bcast_f32(em, j);
-                                const bool before = kj > km || (kj == km && ij < im);
-                                pre += before ? (double)ej : 0.0;
+                            for (int j0 = 0; j0 < n; j0 += 4) {
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) {
+                                    const int j = min(j0 + u, 63);
+                                    const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
+                                    const float ej = bcast_f32(em, j);
+                                    const bool before =
+                                        (j0 + u < n) && (kj > km || (kj == km && ij < im));
+                                    pre += before ? (double)ej : 0.0;
+                                }
                             }
                             const bool kept = valid && (gab + pre - (double)em <= pZR);
                             // the last kept member: smallest value, then largest
                             // index (DPP maxima; indices < 2^24 are exact in float)
                             const float xcut = -wmax_f32(kept ? -xm : -INFINITY);
                             const float icut = wmax_f32((kept && xm == xcut) ? (float)im : -1.0f);
-                            if (l == 0) {
-                                sh.cut_key = key32(xcut);
-                                sh.cut_idx = (uint32_t)icut;
-                            }
+                            // kept members join the total of the wave that owns
+                            // them (fixed-point LDS atomics: order-independent)
+                            const int mw = min((int)((im + (uint32_t)mis) / (uint32_t)(4 * kWaveSlots)),
+                                               kWaves - 1);
+                            const int slotw = kept ? mw : kWaves;  // kWaves: a lane's spare slot
+                            atomicAdd(slotw < kWaves ? &sh.wfix[slotw]
+                                                     : reinterpret_cast<unsigned long long*>(&sh.junk[tid]),
+                                      (unsigned long long)((double)em * kFix));
+                            atomicAdd(slotw < kWaves ? &sh.wcnt[slotw]
+                                                     : reinterpret_cast<uint32_t*>(&sh.junk[tid]),
+                                      1u);
+                            lds_wave_fence();
+                            // per-wave kept mass (lanes 0..7), its prefix, the draw
+                            const int li = min(l, kWaves - 1);
+                            const double T =
+                                (l < kWaves) ? sh.wtot[li] + (double)sh.wfix[li] * (1.0 / kFix) : 0.0;
+                            const uint32_t TN = (l < kWaves) ? sh.ua[li] + sh.wcnt[li] : 0u;
+                            const double Tincl = wscan_f64(T);
+                            const double zk = bcast_f64(Tincl, 63);
+                            const uint32_t kept_total = wsum_u32(TN);
+                            uint64_t st[4];
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) |
+                                        bcast_u32((uint32_t)rsv, j);
+                            const double u = rng_next_f64(st);  // sampler.rs:209
+                            const double r = u * zk;
+                            // the first wave whose running total reaches r (and
+                            // has mass); rounding: the last wave with mass
+                            const uint64_t hw = __ballot(l < kWaves && T > 0.0 && Tincl >= r);
+                            const uint64_t nzw = __ballot(l < kWaves && T > 0.0);
+                            const int wsel = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)nzw));
+                            const double wbase = bcast_f64(Tincl - T, wsel);
+                            NIS_PUT(l == 0, sh.cut_key, key32(xcut));
+                            NIS_PUT(l == 0, sh.cut_idx, (uint32_t)icut);
+                            NIS_PUT(l == 0, sh.bi[0], wsel);
+                            NIS_PUT(l == 0, sh.bi[1], (int32_t)kept_total);
+                            NIS_PUT(l == 0, sh.bd[1], u);
+                            NIS_PUT(l == 0, sh.bd[2], wbase);
+                            NIS_PUT(l == 0, sh.bd[3], zk);
+                            NIS_PUT(l == 0, sh.bd[4], r);
+                            NIS_PUT(l == 1, sh.rng[0], st[0]);
+                            NIS_PUT(l == 2, sh.rng[1], st[1]);
+                            NIS_PUT(l == 3, sh.rng[2], st[2]);
+                            NIS_PUT(l == 4, sh.rng[3], st[3]);
                         }
-                        NIS_RNG_DRAW()
                         lds_barrier();
                         NIS_TS(8);
-                        // ---- S7: inverse-CDF walk over the candidate lists -------
-                        const uint32_t kc = sh.cut_key, ic = sh.cut_idx;
-                        double kw = 0.0;
-                        uint32_t nk = 0;
-                        #pragma unroll 1
-                        for (int j0 = 0; j0 < ncc; j0 += 128) {
-                            const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
-                            const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
-                            const uint32_t ia = sh.s.ci[w][ja], ib = sh.s.ci[w][jb];
-                            const float ea = sh.s.ce[w][ja], eb = sh.s.ce[w][jb];
-                            const uint32_t ka = key32(xa), kb = key32(xb);
-                            if (ja < ncc && (ka > kc || (ka == kc && ia <= ic))) {
-                                kw += (double)ea;
-                                ++nk;
-                            }
-                            if (jb < ncc && (kb > kc || (kb == kc && ib <= ic))) {
-                                kw += (double)eb;
-                                ++nk;
-                            }
-                        }
-                        kw = wsum_f64(kw);
-                        nk = wsum_u32(nk);
-                        if (l == 0) {
-                            sh.wtot[w] = kw;
-                            sh.ua[w] = nk;
-                        }
-                        lds_barrier();
-                        double zk = 0.0;
-#pragma unroll
-                        for (int i = 0; i < kWaves; ++i) zk += sh.wtot[i];
-                        const double u = sh.bd[1];
-                        const double r = u * zk;
-                        int wsel = -1;
-                        double wbase = 0.0;
-                        {
-                            double acc = 0.0;
-#pragma unroll
-                            for (int i = 0; i < kWaves; ++i) {
-                                const double nx = acc + sh.wtot[i];
-                                if (wsel < 0 && nx >= r && sh.wtot[i] > 0.0) {
-                                    wsel = i;
-                                    wbase = acc;
-                                }
-                                acc = nx;
-                            }
-                            if (wsel < 0) {  // rounding: the last wave with mass
-                                acc = 0.0;
-#pragma unroll
-                                for (int i = 0; i < kWaves; ++i) {
-                                    if (sh.wtot[i] > 0.0) {
-                                        wsel = i;
-                                        wbase = acc;
-                                    }
-                                    acc += sh.wtot[i];
-                                }
-                            }
-                        }
-                        wsel = __builtin_amdgcn_readfirstlane(wsel);
+                        // ---- S7: inverse-CDF walk over the chosen wave's list ----
+                        const int wsel = __builtin_amdgcn_readfirstlane(sh.bi[0]);
                         if (w == wsel) {
-                            double run = wbase;
+                            const uint32_t kc = sh.cut_key, ic = sh.cut_idx;
+                            const double u = sh.bd[1], zk = sh.bd[3], r = sh.bd[4];
+                            double run = sh.bd[2];
                             int tok = -1, last = -1;
                             float xt = 0.0f, xlast = 0.0f;
                             #pragma unroll 1
                             for (int j0 = 0; j0 < ncc; j0 += 64) {
-                                const int j = j0 + l;
-                                float x = -INFINITY;
-                                uint32_t id = 0;
-                                float e = 0.0f;
-                                if (j < ncc) {
-                                    x = sh.s.cx[w][j];
-                                    id = sh.s.ci[w][j];
-                                    e = sh.s.ce[w][j];
-                                }
+                                const int j = j0 + l;  // < ncc + 64 <= kWaveCand + 64: inside the list
+                                const float x = sh.s.cx[w][j];
+                                const uint32_t id = sh.s.ci[w][j];
+                                const float e = sh.s.ce[w][j];
                                 const uint32_t k = key32(x);
                                 const bool kept = (j < ncc) && (k > kc || (k == kc && id <= ic));
                                 const double em = kept ? (double)e : 0.0;
@@ -769,11 +765,9 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                                     break;
                                 }
                                 const uint64_t km = __ballot(kept);
-                                if (km) {
-                                    const int L = 63 - __clzll((long long)km);
-                                    last = (int)bcast_u32(id, L);
-                                    xlast = bcast_f32(x, L);
-                                }
+                                const int Lk = km ? (63 - __clzll((long long)km)) : 0;
+                                last = km ? (int)bcast_u32(id, Lk) : last;
+                                xlast = km ? bcast_f32(x, Lk) : xlast;
                                 run += bcast_f64(inc, 63);
                             }
                             bool tkept = true;
@@ -786,13 +780,10 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                                 tkept = false;
                             }
                             if (l == 0) {
-                                uint32_t kept_total = 0;
-#pragma unroll
-                                for (int i = 0; i < kWaves; ++i) kept_total += sh.ua[i];
                                 const double zkM = zk * rho;
                                 const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
                                 write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
-                                                 zkM, ZR * rho, u, prob, (uint64_t)kept_total, 1);
+                                                 zkM, ZR * rho, u, prob, (uint64_t)sh.bi[1], 1);
                             }
                         }
                         if (tid == 0) {
@@ -826,17 +817,17 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     // Dense route
     // ---- T2: value window bracketing the cutoff, from the sample (wave 0)
     if (topp && w == 0) {
-        // lane l owns bins [32l, 32l + 32); bin 0 = top of the row
+        // lane l owns bins [8l, 8l + 8); bin 0 = top of the row
         uint32_t cnt = 0;
         float msf = 0.0f;
 #pragma unroll
-        for (int i4 = 0; i4 < 8; ++i4) {
-            const u4v sb = *reinterpret_cast<const u4v*>(&sh.scnt[32 * l + 4 * i4]);
+        for (int i4 = 0; i4 < kBinsPerLane / 4; ++i4) {
+            const u4v sb = *reinterpret_cast<const u4v*>(&sh.scnt[kBinsPerLane * l + 4 * i4]);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t n = elemu(sb, q);
                 cnt += n;
-                msf += (float)n * bin_mass(32 * l + 4 * i4 + q);
+                msf += (float)n * bin_mass(kBinsPerLane * l + 4 * i4 + q);
             }
         }
         const uint32_t cnt_incl = wscan_u32(cnt);
@@ -857,10 +848,10 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 int na = (int)(cnt_incl - cnt);
                 bool done = false;
                 #pragma unroll 1
-                for (int i = 0; i < 32; ++i) {
+                for (int i = 0; i < kBinsPerLane; ++i) {
                     if (!done) {
-                        const uint32_t n = sh.scnt[32 * l + i];
-                        mprev += (double)((float)n * bin_mass(32 * l + i));
+                        const uint32_t n = sh.scnt[kBinsPerLane * l + i];
+                        mprev += (double)((float)n * bin_mass(kBinsPerLane * l + i));
                         na += (int)n;
                         done = F * (S_s - mprev) <= removed;
                     }
@@ -883,9 +874,9 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         int b = -1;                                                  \
         if (l == L) {                                                \
             int acc = cexcl;                                         \
-            for (int i = 0; i < 32; ++i) {                           \
-                acc += (int)sh.scnt[32 * l + i];                     \
-                if (b < 0 && acc >= (rank)) b = 32 * l + i;          \
+            for (int i = 0; i < kBinsPerLane; ++i) {                           \
+                acc += (int)sh.scnt[kBinsPerLane * l + i];                     \
+                if (b < 0 && acc >= (rank)) b = kBinsPerLane * l + i;          \
             }                                                        \
         }                                                            \
         (out) = __shfl(b, L);                                        \
@@ -902,8 +893,8 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 int lb = -1;
                 if (l == L) {
                     #pragma unroll 1
-                    for (int i = 0; i < 32; ++i)
-                        if (sh.scnt[32 * l + i] != 0) lb = 32 * l + i;
+                    for (int i = 0; i < kBinsPerLane; ++i)
+                        if (sh.scnt[kBinsPerLane * l + i] != 0) lb = kBinsPerLane * l + i;
                 }
                 lb = __shfl(lb, L);
                 if (b_bot > lb) b_bot = lb;
