@@ -86,18 +86,32 @@ struct DenseShared {
     uint32_t cloc[kMaxFinal];        //   owner thread * kLaneCap + list slot
 };
 struct SparseShared {
-    // per-wave lists; the 64 slots past each list's capacity take the
-    // writes of lanes with nothing to append (branch-free appends)
-    f4v ent_x[kWaves][kWaveEnt + 64];         // listed float4s, wave-compacted in index order
-    uint16_t ent_pos[kWaves][kWaveEnt + 64];  //   their chunk * 64 + lane
+    // per-wave lists (64 slots of slack past each capacity: reads of whole
+    // 64-lane groups past a list's end stay inside it)
+    union {
+        struct {
+            f4v ent_x[kWaves][kWaveEnt + 64];         // listed float4s, wave-compacted in index order
+            uint16_t ent_pos[kWaves][kWaveEnt + 64];  //   their chunk * 64 + lane
+        } l;
+        struct {  // members of the cutoff bucket, per wave (the listing is dead by then)
+            float gx[kWaves][kMaxFinal];
+            uint32_t gi[kWaves][kMaxFinal];
+            float ge[kWaves][kMaxFinal];
+        } g;
+    } u;
     uint16_t cb[kWaves][kWaveCand + 64];      // candidates' fine bucket
     float cx[kWaves][kWaveCand + 64];         // candidates (x >= x_lo) in index order: logit
     uint32_t ci[kWaves][kWaveCand + 64];      //   row index
     float ce[kWaves][kWaveCand + 64];         //   mass 2^(x*c - R)
     double gab[kFineBins];               // candidate mass above each fine bucket
-    float gx[kMaxFinal];                 // members of the cutoff bucket
-    uint32_t gi[kMaxFinal];
-    float ge[kMaxFinal];
+};
+
+// One 16-byte record per wave, written by the wave's lane 0 and read whole
+// by every lane after a barrier (one LDS round trip for all eight).
+struct alignas(16) WaveRec {
+    double d;
+    uint32_t a;
+    uint32_t b;
 };
 
 // Branches cost about as much as ten VALU instructions here, so the tail
@@ -115,12 +129,14 @@ struct FastShared {
         DenseShared d;
         SparseShared s;
     };
+    WaveRec t1[kWaves];              // stream end: {Z_w, max_w, R_w}
+    WaveRec wc[kWaves];              // candidates: {mass, listed float4s, candidates}
+    WaveRec wg[kWaves];              // gather: {sure mass, sure count, bucket members}
     uint64_t rng[4];                 // the row's RNG state after its one draw
     unsigned long long wfix[kWaves];  // kept cutoff-bucket mass per wave (2^-40 fixed point)
     uint32_t wcnt[kWaves];           // kept cutoff-bucket members per wave
     uint32_t ncand;
     uint32_t overflow;
-    uint32_t gcount;
     uint32_t cut_key;
     uint32_t cut_idx;
     float fa[kWaves];
@@ -186,6 +202,81 @@ __device__ __forceinline__ float max4(const f4v& v) {
 // everywhere on this path so that equal logits get bit-equal masses.
 __device__ __forceinline__ float mass_of(float x, float c, float R) {
     return __builtin_amdgcn_exp2f(fmaf(x, c, -R));
+}
+
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// LDS stores by the lanes of `mask` only (`mask` must be a subset of the
+// active lanes, e.g. a ballot).  exec is narrowed around the stores, so the
+// other lanes move no data through the LDS and no branch is taken.  Within
+// a wave LDS operations complete in order, and the release fences of the
+// barriers wait for them like for any other LDS store.
+__device__ __forceinline__ void lds_put_x4_u16(uint64_t mask, uint32_t a, f4v v, uint32_t b,
+                                               uint32_t h) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_write_b128 %2, %3\n\t"
+        "ds_write_b16 %4, %5\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(v), "v"(b), "v"(h)
+        : "memory");
+}
+__device__ __forceinline__ void lds_put_u32x3(uint64_t mask, uint32_t a, uint32_t va, uint32_t b,
+                                              uint32_t vb, uint32_t c, uint32_t vc) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_write_b32 %2, %3\n\t"
+        "ds_write_b32 %4, %5\n\t"
+        "ds_write_b32 %6, %7\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(va), "v"(b), "v"(vb), "v"(c), "v"(vc)
+        : "memory");
+}
+// a WaveRec by the wave's lane 0
+__device__ __forceinline__ void lds_put_rec(uint32_t a, double d, uint32_t x, uint32_t y) {
+    const uint64_t db = (uint64_t)__double_as_longlong(d);
+    const u4v v = {(uint32_t)db, (uint32_t)(db >> 32), x, y};
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, 1\n\t"
+        "ds_write_b128 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "v"(a), "v"(v)
+        : "memory");
+}
+__device__ __forceinline__ void read_recs(const WaveRec* r, double* d, uint32_t* x, uint32_t* y) {
+    u4v v[kWaves];
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) v[i] = *reinterpret_cast<const u4v*>(&r[i]);
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+        d[i] = __longlong_as_double((long long)(((uint64_t)v[i].y << 32) | v[i].x));
+        x[i] = v[i].z;
+        y[i] = v[i].w;
+    }
+}
+__device__ __forceinline__ void lds_put_u32x2(uint64_t mask, uint32_t a, uint32_t va, uint32_t b,
+                                              uint32_t vb) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_write_b32 %2, %3\n\t"
+        "ds_write_b32 %4, %5\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(va), "v"(b), "v"(vb)
+        : "memory");
 }
 
 // Fine-histogram bucket of an element in [x_lo, x_top] (monotone in x).
@@ -271,7 +362,6 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     }
     NIS_PUT(tid == 0, sh.ncand, 0u);
     NIS_PUT(tid == 0, sh.overflow, 0u);
-    NIS_PUT(tid == 0, sh.gcount, 0u);
     NIS_PUT(tid < kWaves, sh.wfix[min(tid, kWaves - 1)], 0ull);
     NIS_PUT(tid < kWaves, sh.wcnt[min(tid, kWaves - 1)], 0u);
 
@@ -381,13 +471,14 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     NIS_TS(1);
     mx = wmax_f32(mx);
     z = wsum_f64(z);
-    NIS_PUT(l == 0, sh.fb[w], mx);
-    NIS_PUT(l == 0, sh.da[w], z);
-    NIS_PUT(l == 0, sh.fc[w], Rw);
+    lds_put_rec(lds_addr(&sh.t1[w]), z, __float_as_uint(mx), __float_as_uint(Rw));
     lds_barrier();
-    float M = sh.fb[0];
+    double zw[kWaves];
+    uint32_t mxw[kWaves], rww[kWaves];
+    read_recs(sh.t1, zw, mxw, rww);
+    float M = __uint_as_float(mxw[0]);
 #pragma unroll
-    for (int i = 1; i < kWaves; ++i) M = fmaxf(M, sh.fb[i]);
+    for (int i = 1; i < kWaves; ++i) M = fmaxf(M, __uint_as_float(mxw[i]));
     const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
     double ZR = 0.0;
     bool range_ok = true;
@@ -395,8 +486,9 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     for (int i = 0; i < kWaves; ++i) {
         // each wave's masses were taken against its own reference; a wave
         // whose reference sits far below the row max may have overflowed
-        range_ok = range_ok && (fmaf(M, c, -sh.fc[i]) <= kMaxT);
-        ZR += ldexp(sh.da[i], (int)(sh.fc[i] - R));  // exact power-of-two rescale
+        const float rw = __uint_as_float(rww[i]);
+        range_ok = range_ok & (fmaf(M, c, -rw) <= kMaxT);
+        ZR += ldexp(zw[i], (int)(rw - R));  // exact power-of-two rescale
     }
     const float tM = fmaf(M, c, -R);
     // NaN / inf input, an empty row, or a reference too far below the max
@@ -506,23 +598,26 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 fminf(((float)(-(bsel + 1)) / kSampleRes + R) / c, M);  // the max is a candidate
 
             // ---- S2: list the float4s holding candidates (wave-compacted) --
+            // (only the hit lanes store; past the capacity they all write the
+            // last slot, and the overflow is caught below)
             uint32_t nw = 0;
+            const uint32_t ent_x0 = lds_addr(&sh.s.u.l.ent_x[w][0]);
+            const uint32_t ent_p0 = lds_addr(&sh.s.u.l.ent_pos[w][0]);
 #pragma unroll
             for (int k = 0; k < kNch; ++k) {
-                const bool hit = mx4[k] >= x_lo;
-                const uint64_t mk = __ballot(hit);
-                const uint32_t pos = nw + lane_rank(mk);
-                const uint32_t slot = (hit && pos < (uint32_t)kWaveEnt) ? pos : (uint32_t)(kWaveEnt + l);
-                sh.s.ent_x[w][slot] = xv[k];
-                sh.s.ent_pos[w][slot] = (uint16_t)(k * 64 + l);
+                const uint64_t mk = __ballot(mx4[k] >= x_lo);
+                const uint32_t slot = min(nw + lane_rank(mk), (uint32_t)kWaveEnt - 1);
+                lds_put_x4_u16(mk, ent_x0 + 16 * slot, xv[k], ent_p0 + 2 * slot, (uint32_t)(k * 64 + l));
                 nw += (uint32_t)__popcll(mk);
             }
             NIS_TS(4);
             lds_wave_fence();
             // ---- compaction to single candidates, in index order -----------
             const int ns = 4 * (int)min(nw, (uint32_t)kWaveEnt);
-            const float* entf = reinterpret_cast<const float*>(&sh.s.ent_x[w][0]);
+            const float* entf = reinterpret_cast<const float*>(&sh.s.u.l.ent_x[w][0]);
             uint32_t nc = 0;
+            const uint32_t cx0 = lds_addr(&sh.s.cx[w][0]);
+            const uint32_t ci0 = lds_addr(&sh.s.ci[w][0]);
             // four groups of 64 slots per step, their reads issued together
             // (slot s < ns + 256 <= 4 * (kWaveEnt + 64) stays inside the list)
             #pragma unroll 1
@@ -533,17 +628,15 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 for (int u = 0; u < 4; ++u) {
                     const int s = s0 + 64 * u + l;
                     xq[u] = entf[s];
-                    pq[u] = sh.s.ent_pos[w][s >> 2];
+                    pq[u] = sh.s.u.l.ent_pos[w][s >> 2];
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int s = s0 + 64 * u + l;
-                    const bool cand = s < ns && xq[u] >= x_lo;
-                    const uint64_t mk = __ballot(cand);
-                    const uint32_t pos = nc + lane_rank(mk);
-                    const uint32_t slot = (cand && pos < (uint32_t)kWaveCand) ? pos : (uint32_t)(kWaveCand + l);
-                    sh.s.cx[w][slot] = xq[u];
-                    sh.s.ci[w][slot] = (uint32_t)(4 * (w * kWaveSlots + (int)pq[u]) + (s & 3) - mis);
+                    const uint64_t mk = __ballot(s < ns && xq[u] >= x_lo);
+                    const uint32_t slot = min(nc + lane_rank(mk), (uint32_t)kWaveCand - 1);
+                    lds_put_u32x2(mk, cx0 + 4 * slot, __float_as_uint(xq[u]), ci0 + 4 * slot,
+                                  (uint32_t)(4 * (w * kWaveSlots + (int)pq[u]) + (s & 3) - mis));
                     nc += (uint32_t)__popcll(mk);
                 }
             }
@@ -575,18 +668,21 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
 #undef NIS_CAND
             }
             g = wsum_f64(g);
-            NIS_PUT(l == 0, sh.db[w], g);
-            NIS_PUT(l == 0, sh.ua[w], nw);
-            NIS_PUT(l == 0, sh.ub[w], nc);
+            lds_put_rec(lds_addr(&sh.wc[w]), g, nw, nc);
             lds_barrier();
             NIS_TS(5);
+            double gw[kWaves];
+            uint32_t nww[kWaves], ncw[kWaves];
+            read_recs(sh.wc, gw, nww, ncw);
             double Gc = 0.0;
-            bool ovf = false;
+            uint32_t nwmax = 0, ncmax = 0;
 #pragma unroll
             for (int i = 0; i < kWaves; ++i) {
-                Gc += sh.db[i];
-                ovf = ovf || sh.ua[i] > (uint32_t)kWaveEnt || sh.ub[i] > (uint32_t)kWaveCand;
+                Gc += gw[i];
+                nwmax = max(nwmax, nww[i]);
+                ncmax = max(ncmax, ncw[i]);
             }
+            const bool ovf = (nwmax > (uint32_t)kWaveEnt) | (ncmax > (uint32_t)kWaveCand);
             if (ovf) {
                 reject = NIS_REJECT_CAPACITY;
             } else if (!(Gc - (double)mass_of(x_lo, c, R) > pZR)) {
@@ -599,6 +695,10 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 const uint32_t cA = sh.fcnt[bA], cB = sh.fcnt[bB];
                 const double mA = (double)sh.fmass[bA] * (1.0 / kFix);
                 const double mB = (double)sh.fmass[bB] * (1.0 / kFix);
+                // mass of each bucket's largest element (an empty bucket's
+                // key 0 gives NaN, and its test below is false anyway)
+                const float eA = mass_of(unkey32(sh.fkmax[bA]), c, R);
+                const float eB = mass_of(unkey32(sh.fkmax[bB]), c, R);
                 const double mt = mA + mB;
                 const double inc = wscan_f64(mt);
                 NIS_PUT(l == 63, sh.da[w], inc);
@@ -609,8 +709,8 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 const double GA = gbase + (inc - mt);  // candidate mass above bucket bA
                 const double GB = GA + mA;
                 // sampler.rs:150 for the largest element of the bucket
-                const bool kA = cA != 0 && (GA - (double)mass_of(unkey32(sh.fkmax[bA]), c, R) <= pZR);
-                const bool kB = cB != 0 && (GB - (double)mass_of(unkey32(sh.fkmax[bB]), c, R) <= pZR);
+                const bool kA = (cA != 0) & (GA - (double)eA <= pZR);
+                const bool kB = (cB != 0) & (GB - (double)eB <= pZR);
                 sh.s.gab[bA] = GA;
                 sh.s.gab[bB] = GB;
                 const int lowk =
@@ -628,38 +728,48 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                     const double gab = sh.s.gab[bstar];
                     // ---- gather the cutoff bucket's members; sum the mass and
                     // count of the candidates above it (all kept) per wave ------
+                    // (members go to the wave's own list: no slot allocation
+                    // across waves, so no atomic round trip)
                     double sw = 0.0;
-                    uint32_t sn = 0;
+                    uint32_t sn = 0, nm = 0;
+                    const uint32_t gx0 = lds_addr(&sh.s.u.g.gx[w][0]);
+                    const uint32_t gi0 = lds_addr(&sh.s.u.g.gi[w][0]);
+                    const uint32_t ge0 = lds_addr(&sh.s.u.g.ge[w][0]);
                     #pragma unroll 1
                     for (int j0 = 0; j0 < ncc; j0 += 128) {
                         const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
                         const int ba = sh.s.cb[w][ja], bb = sh.s.cb[w][jb];
                         const float ea = sh.s.ce[w][ja], eb = sh.s.ce[w][jb];
-                        const bool sa = ja < ncc && ba > bstar, sb = jb < ncc && bb > bstar;
+                        const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
+                        const uint32_t ia = sh.s.ci[w][ja], ib = sh.s.ci[w][jb];
+                        const bool va = ja < ncc, vb = jb < ncc;
+                        const bool sa = va & (ba > bstar), sb = vb & (bb > bstar);
                         sw += (sa ? (double)ea : 0.0) + (sb ? (double)eb : 0.0);
                         sn += (sa ? 1u : 0u) + (sb ? 1u : 0u);
-#define NIS_GATHER(j, b, e)                                                              \
-    {                                                                                    \
-        const bool mem = (j) < ncc && (b) == bstar;                                      \
-        const uint32_t s =                                                               \
-            atomicAdd(mem ? &sh.gcount : reinterpret_cast<uint32_t*>(&sh.junk[tid]), 1u); \
-        const bool put = mem && s < (uint32_t)kMaxFinal;                                 \
-        const uint32_t sc = min(s, (uint32_t)kMaxFinal - 1);                             \
-        NIS_PUT(put, sh.s.gx[sc], sh.s.cx[w][(j)]);                                      \
-        NIS_PUT(put, sh.s.gi[sc], sh.s.ci[w][(j)]);                                      \
-        NIS_PUT(put, sh.s.ge[sc], (e));                                                  \
+#define NIS_GATHER(v, b, x, i, e)                                                      \
+    {                                                                                  \
+        const uint64_t mk = __ballot((v) & ((b) == bstar));                            \
+        const uint32_t sc = min(nm + lane_rank(mk), (uint32_t)kMaxFinal - 1);          \
+        lds_put_u32x3(mk, gx0 + 4 * sc, __float_as_uint(x), gi0 + 4 * sc, (i), ge0 + 4 * sc, \
+                      __float_as_uint(e));                                             \
+        nm += (uint32_t)__popcll(mk);                                                  \
     }
-                        NIS_GATHER(ja, ba, ea)
-                        NIS_GATHER(jb, bb, eb)
+                        NIS_GATHER(va, ba, xa, ia, ea)
+                        NIS_GATHER(vb, bb, xb, ib, eb)
 #undef NIS_GATHER
                     }
                     sw = wsum_f64(sw);
                     sn = wsum_u32(sn);
-                    NIS_PUT(l == 0, sh.wtot[w], sw);
-                    NIS_PUT(l == 0, sh.ua[w], sn);
+                    lds_put_rec(lds_addr(&sh.wg[w]), sw, sn, nm);
                     lds_barrier();
                     NIS_TS(7);
-                    if (sh.gcount != nstar) {
+                    double sww[kWaves];
+                    uint32_t snw[kWaves], nmw[kWaves];
+                    read_recs(sh.wg, sww, snw, nmw);
+                    uint32_t nmtot = 0;
+#pragma unroll
+                    for (int i = 0; i < kWaves; ++i) nmtot += nmw[i];
+                    if (nmtot != nstar) {
                         reject = NIS_REJECT_BUCKET;
                     } else {
                         // ---- wave 0: exact rule inside the bucket, the draw, and
@@ -667,10 +777,21 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                         if (w == 0) {
                             const int n = (int)nstar;
                             const bool valid = l < n;
-                            const float xm = valid ? sh.s.gx[l] : -INFINITY;
+                            // member l of the waves' lists taken in wave order
+                            int mwv = 0;
+                            uint32_t mbase = 0, acc = 0;
+#pragma unroll
+                            for (int i = 0; i < kWaves; ++i) {
+                                const bool here = (uint32_t)l >= acc;
+                                mwv = here ? i : mwv;
+                                mbase = here ? acc : mbase;
+                                acc += nmw[i];
+                            }
+                            const int mj = min(l - (int)mbase, kMaxFinal - 1);
+                            const float xm = valid ? sh.s.u.g.gx[mwv][mj] : -INFINITY;
                             const uint32_t km = key32(xm);
-                            const uint32_t im = valid ? sh.s.gi[l] : 0u;
-                            const float em = valid ? sh.s.ge[l] : 0.0f;
+                            const uint32_t im = valid ? sh.s.u.g.gi[mwv][mj] : 0u;
+                            const float em = valid ? sh.s.u.g.ge[mwv][mj] : 0.0f;
                             // mass of the members ahead of this one in the
                             // reference's stable descending order
                             double pre = 0.0;
@@ -705,9 +826,16 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                             lds_wave_fence();
                             // per-wave kept mass (lanes 0..7), its prefix, the draw
                             const int li = min(l, kWaves - 1);
+                            double swl = sww[0];
+                            uint32_t snl = snw[0];
+#pragma unroll
+                            for (int i = 1; i < kWaves; ++i) {
+                                swl = (li == i) ? sww[i] : swl;
+                                snl = (li == i) ? snw[i] : snl;
+                            }
                             const double T =
-                                (l < kWaves) ? sh.wtot[li] + (double)sh.wfix[li] * (1.0 / kFix) : 0.0;
-                            const uint32_t TN = (l < kWaves) ? sh.ua[li] + sh.wcnt[li] : 0u;
+                                (l < kWaves) ? swl + (double)sh.wfix[li] * (1.0 / kFix) : 0.0;
+                            const uint32_t TN = (l < kWaves) ? snl + sh.wcnt[li] : 0u;
                             const double Tincl = wscan_f64(T);
                             const double zk = bcast_f64(Tincl, 63);
                             const uint32_t kept_total = wsum_u32(TN);
