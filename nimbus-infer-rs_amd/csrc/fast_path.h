@@ -133,12 +133,8 @@ struct FastShared {
     WaveRec wc[kWaves];              // candidates: {mass, listed float4s, candidates}
     WaveRec wg[kWaves];              // gather: {sure mass, sure count, bucket members}
     uint64_t rng[4];                 // the row's RNG state after its one draw
-    unsigned long long wfix[kWaves];  // kept cutoff-bucket mass per wave (2^-40 fixed point)
-    uint32_t wcnt[kWaves];           // kept cutoff-bucket members per wave
     uint32_t ncand;
     uint32_t overflow;
-    uint32_t cut_key;
-    uint32_t cut_idx;
     float fa[kWaves];
     float fb[kWaves];
     float fc[kWaves];
@@ -362,8 +358,6 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     }
     NIS_PUT(tid == 0, sh.ncand, 0u);
     NIS_PUT(tid == 0, sh.overflow, 0u);
-    NIS_PUT(tid < kWaves, sh.wfix[min(tid, kWaves - 1)], 0ull);
-    NIS_PUT(tid < kWaves, sh.wcnt[min(tid, kWaves - 1)], 0u);
 
     // slots not fully inside the row get their exact values or -inf; only
     // the one or two waves holding such slots take the (wave-uniform) branch.
@@ -772,154 +766,136 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                     if (nmtot != nstar) {
                         reject = NIS_REJECT_BUCKET;
                     } else {
-                        // ---- wave 0: exact rule inside the bucket, the draw, and
-                        // the wave that holds the crossing -----------------------
-                        if (w == 0) {
-                            const int n = (int)nstar;
-                            const bool valid = l < n;
-                            // member l of the waves' lists taken in wave order
-                            int mwv = 0;
-                            uint32_t mbase = 0, acc = 0;
+                        // ---- wave 0 alone from here: the exact rule inside the
+                        // bucket, the draw, and the walk over the list of the wave
+                        // that holds the crossing (all of it in LDS) -------------
+                        if (w != 0) return NIS_REJECT_NONE;
+                        const int n = (int)nstar;
+                        const bool valid = l < n;
+                        // member l of the waves' lists taken in wave order
+                        int mwv = 0;
+                        uint32_t mbase = 0, acc = 0;
 #pragma unroll
-                            for (int i = 0; i < kWaves; ++i) {
-                                const bool here = (uint32_t)l >= acc;
-                                mwv = here ? i : mwv;
-                                mbase = here ? acc : mbase;
-                                acc += nmw[i];
-                            }
-                            const int mj = min(l - (int)mbase, kMaxFinal - 1);
-                            const float xm = valid ? sh.s.u.g.gx[mwv][mj] : -INFINITY;
-                            const uint32_t km = key32(xm);
-                            const uint32_t im = valid ? sh.s.u.g.gi[mwv][mj] : 0u;
-                            const float em = valid ? sh.s.u.g.ge[mwv][mj] : 0.0f;
-                            // mass of the members ahead of this one in the
-                            // reference's stable descending order
-                            double pre = 0.0;
-                            #pragma unroll 1
-                            for (int j0 = 0; j0 < n; j0 += 4) {
-#pragma unroll
-                                for (int u = 0; u < 4; ++u) {
-                                    const int j = min(j0 + u, 63);
-                                    const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
-                                    const float ej = bcast_f32(em, j);
-                                    const bool before =
-                                        (j0 + u < n) && (kj > km || (kj == km && ij < im));
-                                    pre += before ? (double)ej : 0.0;
-                                }
-                            }
-                            const bool kept = valid && (gab + pre - (double)em <= pZR);
-                            // the last kept member: smallest value, then largest
-                            // index (DPP maxima; indices < 2^24 are exact in float)
-                            const float xcut = -wmax_f32(kept ? -xm : -INFINITY);
-                            const float icut = wmax_f32((kept && xm == xcut) ? (float)im : -1.0f);
-                            // kept members join the total of the wave that owns
-                            // them (fixed-point LDS atomics: order-independent)
-                            const int mw = min((int)((im + (uint32_t)mis) / (uint32_t)(4 * kWaveSlots)),
-                                               kWaves - 1);
-                            const int slotw = kept ? mw : kWaves;  // kWaves: a lane's spare slot
-                            atomicAdd(slotw < kWaves ? &sh.wfix[slotw]
-                                                     : reinterpret_cast<unsigned long long*>(&sh.junk[tid]),
-                                      (unsigned long long)((double)em * kFix));
-                            atomicAdd(slotw < kWaves ? &sh.wcnt[slotw]
-                                                     : reinterpret_cast<uint32_t*>(&sh.junk[tid]),
-                                      1u);
-                            lds_wave_fence();
-                            // per-wave kept mass (lanes 0..7), its prefix, the draw
-                            const int li = min(l, kWaves - 1);
-                            double swl = sww[0];
-                            uint32_t snl = snw[0];
-#pragma unroll
-                            for (int i = 1; i < kWaves; ++i) {
-                                swl = (li == i) ? sww[i] : swl;
-                                snl = (li == i) ? snw[i] : snl;
-                            }
-                            const double T =
-                                (l < kWaves) ? swl + (double)sh.wfix[li] * (1.0 / kFix) : 0.0;
-                            const uint32_t TN = (l < kWaves) ? snl + sh.wcnt[li] : 0u;
-                            const double Tincl = wscan_f64(T);
-                            const double zk = bcast_f64(Tincl, 63);
-                            const uint32_t kept_total = wsum_u32(TN);
-                            uint64_t st[4];
-#pragma unroll
-                            for (int j = 0; j < 4; ++j)
-                                st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) |
-                                        bcast_u32((uint32_t)rsv, j);
-                            const double u = rng_next_f64(st);  // sampler.rs:209
-                            const double r = u * zk;
-                            // the first wave whose running total reaches r (and
-                            // has mass); rounding: the last wave with mass
-                            const uint64_t hw = __ballot(l < kWaves && T > 0.0 && Tincl >= r);
-                            const uint64_t nzw = __ballot(l < kWaves && T > 0.0);
-                            const int wsel = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)nzw));
-                            const double wbase = bcast_f64(Tincl - T, wsel);
-                            NIS_PUT(l == 0, sh.cut_key, key32(xcut));
-                            NIS_PUT(l == 0, sh.cut_idx, (uint32_t)icut);
-                            NIS_PUT(l == 0, sh.bi[0], wsel);
-                            NIS_PUT(l == 0, sh.bi[1], (int32_t)kept_total);
-                            NIS_PUT(l == 0, sh.bd[1], u);
-                            NIS_PUT(l == 0, sh.bd[2], wbase);
-                            NIS_PUT(l == 0, sh.bd[3], zk);
-                            NIS_PUT(l == 0, sh.bd[4], r);
-                            NIS_PUT(l == 1, sh.rng[0], st[0]);
-                            NIS_PUT(l == 2, sh.rng[1], st[1]);
-                            NIS_PUT(l == 3, sh.rng[2], st[2]);
-                            NIS_PUT(l == 4, sh.rng[3], st[3]);
+                        for (int i = 0; i < kWaves; ++i) {
+                            const bool here = (uint32_t)l >= acc;
+                            mwv = here ? i : mwv;
+                            mbase = here ? acc : mbase;
+                            acc += nmw[i];
                         }
-                        lds_barrier();
+                        const int mj = min(l - (int)mbase, kMaxFinal - 1);  // in bounds for every lane
+                        const float gxv = sh.s.u.g.gx[mwv][mj];
+                        const uint32_t giv = sh.s.u.g.gi[mwv][mj];
+                        const float gev = sh.s.u.g.ge[mwv][mj];
+                        const float xm = valid ? gxv : -INFINITY;
+                        const uint32_t km = key32(xm);
+                        const uint32_t im = valid ? giv : 0u;
+                        const float em = valid ? gev : 0.0f;
+                        // mass of the members ahead of this one in the
+                        // reference's stable descending order
+                        double pre = 0.0;
+                        #pragma unroll 1
+                        for (int j0 = 0; j0 < n; j0 += 4) {
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                const int j = min(j0 + u, 63);
+                                const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
+                                const float ej = bcast_f32(em, j);
+                                const bool before = (j0 + u < n) & ((kj > km) | ((kj == km) & (ij < im)));
+                                pre += before ? (double)ej : 0.0;
+                            }
+                        }
+                        const bool kept = valid & (gab + pre - (double)em <= pZR);
+                        // the last kept member: smallest value, then largest
+                        // index (DPP maxima; indices < 2^24 are exact in float)
+                        const float xcut = -wmax_f32(kept ? -xm : -INFINITY);
+                        const float icut = wmax_f32((kept & (xm == xcut)) ? (float)im : -1.0f);
+                        const uint32_t kc = key32(xcut), ic = (uint32_t)icut;
+                        // per-wave kept mass (lanes 0..7): the wave's sure mass plus
+                        // its kept members, added in member order
+                        const int mw = min((int)((im + (uint32_t)mis) / (uint32_t)(4 * kWaveSlots)), kWaves - 1);
+                        const int li = min(l, kWaves - 1);
+                        double T = sww[0];
+                        uint32_t TN = snw[0];
+#pragma unroll
+                        for (int i = 1; i < kWaves; ++i) {
+                            T = (li == i) ? sww[i] : T;
+                            TN = (li == i) ? snw[i] : TN;
+                        }
+                        #pragma unroll 1
+                        for (uint64_t km_ = __ballot(kept); km_ != 0; km_ &= km_ - 1) {
+                            const int j = __ffsll((long long)km_) - 1;
+                            const bool mine = (int)bcast_u32((uint32_t)mw, j) == l;
+                            T += mine ? (double)bcast_f32(em, j) : 0.0;
+                            TN += mine ? 1u : 0u;
+                        }
+                        T = (l < kWaves) ? T : 0.0;
+                        TN = (l < kWaves) ? TN : 0u;
+                        const double Tincl = wscan_f64(T);
+                        const double zk = bcast_f64(Tincl, 63);
+                        const uint32_t kept_total = wsum_u32(TN);
+                        uint64_t st[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) |
+                                    bcast_u32((uint32_t)rsv, j);
+                        const double u = rng_next_f64(st);  // sampler.rs:209
+                        const double r = u * zk;
+                        // the first wave whose running total reaches r (and has
+                        // mass); rounding: the last wave with mass
+                        const uint64_t hw = __ballot((l < kWaves) & (T > 0.0) & (Tincl >= r));
+                        const uint64_t nzw = __ballot((l < kWaves) & (T > 0.0));
+                        const int wsel = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)nzw));
+                        double run = bcast_f64(Tincl - T, wsel);
+                        uint32_t nsel = ncw[0];
+#pragma unroll
+                        for (int i = 1; i < kWaves; ++i) nsel = (i == wsel) ? ncw[i] : nsel;
+                        const int ncs = (int)min(nsel, (uint32_t)kWaveCand);
                         NIS_TS(8);
-                        // ---- S7: inverse-CDF walk over the chosen wave's list ----
-                        const int wsel = __builtin_amdgcn_readfirstlane(sh.bi[0]);
-                        if (w == wsel) {
-                            const uint32_t kc = sh.cut_key, ic = sh.cut_idx;
-                            const double u = sh.bd[1], zk = sh.bd[3], r = sh.bd[4];
-                            double run = sh.bd[2];
-                            int tok = -1, last = -1;
-                            float xt = 0.0f, xlast = 0.0f;
-                            #pragma unroll 1
-                            for (int j0 = 0; j0 < ncc; j0 += 64) {
-                                const int j = j0 + l;  // < ncc + 64 <= kWaveCand + 64: inside the list
-                                const float x = sh.s.cx[w][j];
-                                const uint32_t id = sh.s.ci[w][j];
-                                const float e = sh.s.ce[w][j];
-                                const uint32_t k = key32(x);
-                                const bool kept = (j < ncc) && (k > kc || (k == kc && id <= ic));
-                                const double em = kept ? (double)e : 0.0;
-                                const double inc = wscan_f64(em);
-                                const uint64_t hit = __ballot(kept && run + inc >= r);
-                                if (hit) {
-                                    const int L = __ffsll((long long)hit) - 1;
-                                    tok = (int)bcast_u32(id, L);
-                                    xt = bcast_f32(x, L);
-                                    break;
-                                }
-                                const uint64_t km = __ballot(kept);
-                                const int Lk = km ? (63 - __clzll((long long)km)) : 0;
-                                last = km ? (int)bcast_u32(id, Lk) : last;
-                                xlast = km ? bcast_f32(x, Lk) : xlast;
-                                run += bcast_f64(inc, 63);
+                        // ---- S7: inverse-CDF walk over the chosen wave's list ------
+                        int tok = -1, last = -1;
+                        float xt = 0.0f, xlast = 0.0f;
+                        #pragma unroll 1
+                        for (int j0 = 0; j0 < ncs; j0 += 64) {
+                            const int j = j0 + l;  // < ncs + 64 <= kWaveCand + 64: inside the list
+                            const float x = sh.s.cx[wsel][j];
+                            const uint32_t id = sh.s.ci[wsel][j];
+                            const float e = sh.s.ce[wsel][j];
+                            const uint32_t k = key32(x);
+                            const bool kj = (j < ncs) & ((k > kc) | ((k == kc) & (id <= ic)));
+                            const double emj = kj ? (double)e : 0.0;
+                            const double inc = wscan_f64(emj);
+                            const uint64_t hit = __ballot(kj & (run + inc >= r));
+                            if (hit) {
+                                const int L = __ffsll((long long)hit) - 1;
+                                tok = (int)bcast_u32(id, L);
+                                xt = bcast_f32(x, L);
+                                break;
                             }
-                            bool tkept = true;
-                            if (tok < 0) {  // rounding: the last kept token of this wave
-                                tok = last;
-                                xt = xlast;
-                            }
-                            if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
-                                tok = 0;
-                                tkept = false;
-                            }
-                            if (l == 0) {
-                                const double zkM = zk * rho;
-                                const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
-                                write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
-                                                 zkM, ZR * rho, u, prob, (uint64_t)sh.bi[1], 1);
-                            }
+                            const uint64_t kmk = __ballot(kj);
+                            const int Lk = kmk ? (63 - __clzll((long long)kmk)) : 0;
+                            last = kmk ? (int)bcast_u32(id, Lk) : last;
+                            xlast = kmk ? bcast_f32(x, Lk) : xlast;
+                            run += bcast_f64(inc, 63);
                         }
-                        if (tid == 0) {
+                        bool tkept = true;
+                        if (tok < 0) {  // rounding: the last kept token of that wave
+                            tok = last;
+                            xt = xlast;
+                        }
+                        if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
+                            tok = 0;
+                            tkept = false;
+                        }
+                        if (l == 0) {
+                            const double zkM = zk * rho;
+                            const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
+                            write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
+                                             zkM, ZR * rho, u, prob, (uint64_t)kept_total, 1);
                             uint64_t* sp = a.rng + 4 * (int64_t)row;
-                            sp[0] = sh.rng[0];
-                            sp[1] = sh.rng[1];
-                            sp[2] = sh.rng[2];
-                            sp[3] = sh.rng[3];
+                            sp[0] = st[0];
+                            sp[1] = st[1];
+                            sp[2] = st[2];
+                            sp[3] = st[3];
                         }
                         NIS_TS(9);
                         return NIS_REJECT_NONE;
