@@ -53,28 +53,24 @@ constexpr int kFastMaxV = kBlock * 4 * kNch - 3;
 constexpr int kSampleBins = 512;              // 32 octaves at 1/16 octave
 constexpr float kSampleRes = 16.0f;
 constexpr int kBinsPerLane = kSampleBins / 64;
-// 2^-(i + 0.5)/16: the centre mass of bin 8l + i relative to bin 8l's top
-constexpr float kBinStep[8] = {0.9785720705986023f, 0.9370838403701782f, 0.8973545432090759f,
-                               0.8593096733093262f, 0.8228777647018433f, 0.7879904508590698f,
-                               0.7545822262763977f, 0.7225903868675232f};
 constexpr int kFineBins = 1024;
 constexpr int kMaxFinal = 64;
 constexpr int kLaneCap = 16;                  // dense route: window entries per lane
 constexpr float kMaxT = 60.0f;                // overflow guard for 2^(x*c - R)
 constexpr double kFix = 1099511627776.0;      // 2^40 fixed-point mass scale
 constexpr uint8_t kKeptBit = 0x80;
-// sparse route
-constexpr int kWaveEnt = 352;                 // listed float4s per wave
+// sparse route: each wave takes the float4 maxima of its first kTopS chunks
+// as a sample and lists, chunk by chunk as the loads land, the float4s
+// reaching the lower edge of the sample's top histogram bins that hold at
+// most kTopT of it (bins of 1/kTopRes octave of x*c, from kTopHead octaves
+// above the wave's reference down)
+constexpr int kTopS = 8;
+constexpr uint32_t kTopT = 80;
+constexpr int kTopBins = 256;
+constexpr float kTopRes = 8.0f;
+constexpr float kTopHead = 8.0f;
+constexpr int kWaveEnt = 384;                 // listed float4s per wave
 constexpr int kWaveCand = 448;                // candidates per wave
-// x_lo: the highest sample bin whose estimated mass below, plus kSpKappa
-// standard deviations of that estimate, stays under beta * (1-p) * Z, with
-// e(x_lo) <= gamma * (1-p) * Z and at least kSpMinAbove sampled elements at
-// or above it (so the band just below x_lo is represented in the sample)
-constexpr double kSpBeta = 0.7;
-constexpr float kSpKappa = 3.0f;
-constexpr double kSpGamma = 0.25;
-constexpr uint32_t kSpMinAbove = 16;
-constexpr double kSpEstCap = 2800.0;          // estimated candidates per row
 
 struct DenseShared {
     float cell[kWaves][kNch][64];    // kept mass of each lane's 4 elements per chunk
@@ -90,8 +86,8 @@ struct SparseShared {
     // 64-lane groups past a list's end stay inside it)
     union {
         struct {
-            f4v ent_x[kWaves][kWaveEnt + 64];         // listed float4s, wave-compacted in index order
-            uint16_t ent_pos[kWaves][kWaveEnt + 64];  //   their chunk * 64 + lane
+            f4v ent_x[kWaves][kWaveEnt];         // listed float4s, wave-compacted in index order
+            uint16_t ent_pos[kWaves][kWaveEnt];  //   their chunk * 64 + lane
         } l;
         struct {  // members of the cutoff bucket, per wave (the listing is dead by then)
             float gx[kWaves][kMaxFinal];
@@ -130,6 +126,7 @@ struct FastShared {
         SparseShared s;
     };
     WaveRec t1[kWaves];              // stream end: {Z_w, max_w, R_w}
+    WaveRec tc[kWaves];              // listing: {th_w, listed float4s, candidates}
     WaveRec wc[kWaves];              // candidates: {mass, listed float4s, candidates}
     WaveRec wg[kWaves];              // gather: {sure mass, sure count, bucket members}
     uint64_t rng[4];                 // the row's RNG state after its one draw
@@ -358,6 +355,10 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     }
     NIS_PUT(tid == 0, sh.ncand, 0u);
     NIS_PUT(tid == 0, sh.overflow, 0u);
+    // this wave's histogram of float4 maxima (in its own candidate-mass row,
+    // which is written only after the stream)
+    static_assert(kTopBins == 4 * 64 && kTopBins <= kWaveCand + 64, "4 bins per lane, inside a row");
+    *reinterpret_cast<u4v*>(reinterpret_cast<uint32_t*>(&sh.s.ce[w][0]) + 4 * l) = u4v{0u, 0u, 0u, 0u};
 
     // slots not fully inside the row get their exact values or -inf; only
     // the one or two waves holding such slots take the (wave-uniform) branch.
@@ -432,27 +433,70 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     if (edge_wave) NIS_FIX(0);
     const float m0 = wmax_f32(max4(xv[0]));
     const float Rw = (m0 > -INFINITY && fabsf(m0 * c) < 1e30f) ? ceilf(m0 * c) : 0.0f;
+    const float RwH = Rw + kTopHead;
 
     // masses and Z, chunk by chunk as the loads land.  cz / Rz are opaque
     // copies of c / Rw: without them the compiler merges these masses with
     // identical later ones and keeps all 104 of them live.
+    //
+    // Sparse top-p candidates are listed in the same pass (the loads of later
+    // chunks are still in flight meanwhile): a count histogram of the float4
+    // maxima of the first kTopS chunks (fire-and-forget LDS atomics, 1/8-
+    // octave bins from kTopHead octaves above the wave's reference) gives
+    // th_w, the lower edge of its top bins holding at most kTopT of them;
+    // every float4 holding an element >= th_w is then appended to the wave's
+    // list (index order, only the hit lanes store; past the capacity they
+    // all write the last slot and the overflow is caught after the stream).
+    // x_lo = max over the waves of th_w is a threshold at and above which
+    // every element is listed; it is proven safe after the stream
+    // (sampler.rs:150 for the largest element below it).  th_w = +inf when
+    // no bin fits, and without top-p.
     double z = 0.0;
     float mx = -INFINITY;
     float mx4[kNch];
     float cz = c, Rz = Rw;
     asm volatile("" : "+v"(cz), "+v"(Rz));
-#define NIS_STREAM(FIX)                                      \
-    _Pragma("unroll") for (int k = 0; k < kNch; ++k) {      \
-        if (FIX && k > 0) NIS_FIX(k);                        \
-        const f4v x = xv[k];                                 \
-        f4v e;                                               \
-        e.x = mass_of(x.x, cz, Rz);                          \
-        e.y = mass_of(x.y, cz, Rz);                          \
-        e.z = mass_of(x.z, cz, Rz);                          \
-        e.w = mass_of(x.w, cz, Rz);                          \
-        z += (double)((e.x + e.y) + (e.z + e.w));            \
-        mx4[k] = max4(x);                                    \
-        mx = fmaxf(mx, mx4[k]);                              \
+    uint32_t* const whist = reinterpret_cast<uint32_t*>(&sh.s.ce[w][0]);
+    const uint32_t ent_x0 = lds_addr(&sh.s.u.l.ent_x[w][0]);
+    const uint32_t ent_p0 = lds_addr(&sh.s.u.l.ent_pos[w][0]);
+    float thw = INFINITY;
+    uint32_t nw = 0, nc = 0;
+#define NIS_LIST(k)                                                                      \
+    {                                                                                    \
+        const uint64_t mk = __ballot(mx4[k] >= thw);                                     \
+        const uint32_t slot = min(nw + lane_rank(mk), (uint32_t)kWaveEnt - 1);           \
+        lds_put_x4_u16(mk, ent_x0 + 16 * slot, xv[k], ent_p0 + 2 * slot, (uint32_t)((k) * 64 + l)); \
+        nw += (uint32_t)__popcll(mk);                                                    \
+    }
+#define NIS_STREAM(FIX)                                                                 \
+    _Pragma("unroll") for (int k = 0; k < kNch; ++k) {                                 \
+        if (FIX && k > 0) NIS_FIX(k);                                                   \
+        const f4v x = xv[k];                                                            \
+        f4v e;                                                                          \
+        e.x = mass_of(x.x, cz, Rz);                                                     \
+        e.y = mass_of(x.y, cz, Rz);                                                     \
+        e.z = mass_of(x.z, cz, Rz);                                                     \
+        e.w = mass_of(x.w, cz, Rz);                                                     \
+        z += (double)((e.x + e.y) + (e.z + e.w));                                       \
+        mx4[k] = max4(x);                                                               \
+        mx = fmaxf(mx, mx4[k]);                                                         \
+        if (k < kTopS) {                                                                \
+            const float tb = floorf((RwH - mx4[k] * cz) * kTopRes); /* -inf -> +inf */   \
+            atomicAdd(&whist[(uint32_t)fminf(fmaxf(tb, 0.0f), (float)(kTopBins - 1))], 1u); \
+        }                                                                               \
+        if (k == kTopS - 1) {                                                           \
+            lds_wave_fence();                                                           \
+            const u4v hc = *reinterpret_cast<const u4v*>(&whist[4 * l]); /* bins 4l.. */ \
+            const uint32_t hs = hc.x + hc.y + hc.z + hc.w;                              \
+            const uint32_t hi = wscan_u32(hs);                                          \
+            const uint32_t c0 = hi - hs + hc.x, c1 = c0 + hc.y, c2 = c1 + hc.z, c3 = c2 + hc.w; \
+            const uint32_t nok = (uint32_t)(c0 <= kTopT) + (uint32_t)(c1 <= kTopT) +    \
+                                 (uint32_t)(c2 <= kTopT) + (uint32_t)(c3 <= kTopT);     \
+            const int bw = (int)wsum_u32(nok) - 1; /* the last bin whose count fits */  \
+            thw = (!topp || bw < 0) ? INFINITY : (RwH - (float)(bw + 1) * (1.0f / kTopRes)) / c; \
+            _Pragma("unroll") for (int j = 0; j < kTopS; ++j) NIS_LIST(j)               \
+        }                                                                               \
+        if (k >= kTopS) NIS_LIST(k)                                                     \
     }
     if (edge_wave) {
         NIS_STREAM(true)
@@ -460,9 +504,44 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         NIS_STREAM(false)
     }
 #undef NIS_STREAM
+#undef NIS_LIST
+    NIS_TS(1);
+
+    // ---- this wave's candidates: compaction of its list to single elements
+    // >= th_w, in index order (while other waves' loads still land)
+    if (topp) {
+        lds_wave_fence();
+        const int ns = 4 * (int)min(nw, (uint32_t)kWaveEnt);
+        const float* entf = reinterpret_cast<const float*>(&sh.s.u.l.ent_x[w][0]);
+        const uint32_t cx0 = lds_addr(&sh.s.cx[w][0]);
+        const uint32_t ci0 = lds_addr(&sh.s.ci[w][0]);
+        // four groups of 64 slots per step, their reads issued together
+        // (clamped into the list; slots past ns take no part)
+        #pragma unroll 1
+        for (int s0 = 0; s0 < ns; s0 += 256) {
+            float xq[4];
+            uint32_t pq[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int s = min(s0 + 64 * u + l, 4 * kWaveEnt - 1);
+                xq[u] = entf[s];
+                pq[u] = sh.s.u.l.ent_pos[w][s >> 2];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int s = s0 + 64 * u + l;
+                const uint64_t mk = __ballot((s < ns) & (xq[u] >= thw));
+                const uint32_t slot = min(nc + lane_rank(mk), (uint32_t)kWaveCand - 1);
+                lds_put_u32x2(mk, cx0 + 4 * slot, __float_as_uint(xq[u]), ci0 + 4 * slot,
+                              (uint32_t)(4 * (w * kWaveSlots + (int)pq[u]) + (s & 3) - mis));
+                nc += (uint32_t)__popcll(mk);
+            }
+        }
+        lds_put_rec(lds_addr(&sh.tc[w]), (double)thw, nw, nc);
+    }
+    NIS_TS(2);
 
     // ---- T1: row max, reference R, Z ---------------------------------------
-    NIS_TS(1);
     mx = wmax_f32(mx);
     z = wsum_f64(z);
     lds_put_rec(lds_addr(&sh.t1[w]), z, __float_as_uint(mx), __float_as_uint(Rw));
@@ -514,128 +593,23 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
 
     uint32_t reject = NIS_REJECT_NONE;  // reason of a failed sparse attempt
     if (topp) {
-        // count histogram of chunks 0 and 1 (the sample), 1/16-octave bins below R
+        double thv[kWaves];
+        uint32_t nwv[kWaves], ncv[kWaves];
+        read_recs(sh.tc, thv, nwv, ncv);
+        float x_lo = -INFINITY;
+        uint32_t nwmax = 0, ncmax = 0;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float x = elem(xv[q >> 2], q & 3);
-            const float t = fmaf(x, c, -R);
-            const int b = (x > -INFINITY)
-                              ? (int)fminf(fmaxf(-t * kSampleRes, 0.0f), (float)(kSampleBins - 1))
-                              : kSampleBins + l;  // -inf (outside the row or masked): dummy bin
-            atomicAdd(&sh.scnt[b], 1u);
+        for (int i = 0; i < kWaves; ++i) {
+            x_lo = fmaxf(x_lo, (float)thv[i]);
+            nwmax = max(nwmax, nwv[i]);
+            ncmax = max(ncmax, ncv[i]);
         }
-        lds_barrier();
-        NIS_TS(2);
-
-        // ---- S1: threshold x_lo.  Every wave evaluates the whole histogram
-        // itself (same inputs, same operations, so the same result) instead
-        // of sharing partial scans through two more barriers.
-        // Lane l owns bins 8l .. 8l+7; bin b holds t in (-(b+1)/16, -b/16].
-        const u4v c0 = *reinterpret_cast<const u4v*>(&sh.scnt[kBinsPerLane * l]);
-        const u4v c1 = *reinterpret_cast<const u4v*>(&sh.scnt[kBinsPerLane * l + 4]);
-        const uint32_t cnt[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        const float lane_bm = __builtin_amdgcn_exp2f(-(float)(kBinsPerLane * l) / kSampleRes);
-        float bm[8], bmass[8], bsq[8];
-        float ms = 0.0f, qs = 0.0f;
-        uint32_t cs = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            bm[i] = lane_bm * kBinStep[i];  // 2^-(b + 0.5)/16, the bin's centre mass
-            bmass[i] = (float)cnt[i] * bm[i];
-            bsq[i] = bmass[i] * bm[i];
-            ms += bmass[i];
-            qs += bsq[i];
-            cs += cnt[i];
-        }
-        const float mI = wscan_f32(ms), qI = wscan_f32(qs);
-        const uint32_t cI = wscan_u32(cs);
-        const float S = bcast_f32(mI, 63), Q = bcast_f32(qI, 63);
-        const uint32_t C = bcast_u32(cI, 63);
-        // row elements per sampled element (estimates only: float is enough)
-        const float F = (float)V * __builtin_amdgcn_rcpf((float)max(C, 1u));
-        const float rem = (1.0f - p) * (float)ZR;  // mass top-p removes
-        const float thr = (float)kSpBeta * rem * __builtin_amdgcn_rcpf(F);
-        // the largest excluded element must weigh at most gamma * (1-p) * Z
-        const float cap_m = (float)kSpGamma * rem;
-        const int bceil =
-            (cap_m < 1.0f)
-                ? min(max((int)ceilf(-kSampleRes * __builtin_amdgcn_logf(cap_m)) - 1, 0), kSampleBins - 1)
-                : 0;
-        int first = kSampleBins;
-        uint32_t cfirst = 0;
-        {
-            // running sums through this lane's bins (mass, squared mass, count)
-            float run = mI - ms, qrun = qI - qs;
-            uint32_t crun = cI - cs;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                run += bmass[i];
-                qrun += bsq[i];
-                crun += cnt[i];
-                const float ucb = fmaxf(S - run, 0.0f) +
-                                  kSpKappa * __builtin_amdgcn_sqrtf(fmaxf(Q - qrun, 0.0f));
-                const int b = kBinsPerLane * l + i;
-                const bool okb = b >= bceil && crun >= kSpMinAbove && ucb <= thr;
-                const bool take = okb && first == kSampleBins;
-                first = take ? b : first;
-                cfirst = take ? crun : cfirst;
-            }
-        }
-        const uint64_t qm = __ballot(first < kSampleBins);
-        const int qL = qm ? (__ffsll((long long)qm) - 1) : 0;
-        const int bsel = qm ? (int)bcast_u32((uint32_t)first, qL) : kSampleBins;
-        const uint32_t csel = bcast_u32(cfirst, qL);
         NIS_TS(3);
         reject = NIS_REJECT_CAPACITY;
-        if (bsel < kSampleBins && F * (float)csel <= (float)kSpEstCap) {
-            const float x_lo =
-                fminf(((float)(-(bsel + 1)) / kSampleRes + R) / c, M);  // the max is a candidate
-
-            // ---- S2: list the float4s holding candidates (wave-compacted) --
-            // (only the hit lanes store; past the capacity they all write the
-            // last slot, and the overflow is caught below)
-            uint32_t nw = 0;
-            const uint32_t ent_x0 = lds_addr(&sh.s.u.l.ent_x[w][0]);
-            const uint32_t ent_p0 = lds_addr(&sh.s.u.l.ent_pos[w][0]);
-#pragma unroll
-            for (int k = 0; k < kNch; ++k) {
-                const uint64_t mk = __ballot(mx4[k] >= x_lo);
-                const uint32_t slot = min(nw + lane_rank(mk), (uint32_t)kWaveEnt - 1);
-                lds_put_x4_u16(mk, ent_x0 + 16 * slot, xv[k], ent_p0 + 2 * slot, (uint32_t)(k * 64 + l));
-                nw += (uint32_t)__popcll(mk);
-            }
-            NIS_TS(4);
-            lds_wave_fence();
-            // ---- compaction to single candidates, in index order -----------
-            const int ns = 4 * (int)min(nw, (uint32_t)kWaveEnt);
-            const float* entf = reinterpret_cast<const float*>(&sh.s.u.l.ent_x[w][0]);
-            uint32_t nc = 0;
-            const uint32_t cx0 = lds_addr(&sh.s.cx[w][0]);
-            const uint32_t ci0 = lds_addr(&sh.s.ci[w][0]);
-            // four groups of 64 slots per step, their reads issued together
-            // (slot s < ns + 256 <= 4 * (kWaveEnt + 64) stays inside the list)
-            #pragma unroll 1
-            for (int s0 = 0; s0 < ns; s0 += 256) {
-                float xq[4];
-                uint32_t pq[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int s = s0 + 64 * u + l;
-                    xq[u] = entf[s];
-                    pq[u] = sh.s.u.l.ent_pos[w][s >> 2];
-                }
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int s = s0 + 64 * u + l;
-                    const uint64_t mk = __ballot(s < ns && xq[u] >= x_lo);
-                    const uint32_t slot = min(nc + lane_rank(mk), (uint32_t)kWaveCand - 1);
-                    lds_put_u32x2(mk, cx0 + 4 * slot, __float_as_uint(xq[u]), ci0 + 4 * slot,
-                                  (uint32_t)(4 * (w * kWaveSlots + (int)pq[u]) + (s & 3) - mis));
-                    nc += (uint32_t)__popcll(mk);
-                }
-            }
-            lds_wave_fence();
-            // ---- candidate masses and their fine histogram over [x_lo, M] --
+        if ((x_lo < INFINITY) & (nwmax <= (uint32_t)kWaveEnt) & (ncmax <= (uint32_t)kWaveCand)) {
+            // ---- candidate masses and their fine histogram over [x_lo, M]
+            // (a wave's candidates below x_lo, listed against a lower th_w,
+            // take no part: dummy bucket, no mass)
             const int ncc = (int)min(nc, (uint32_t)kWaveCand);
             const float inv_w = (M > x_lo) ? (float)kFineBins / (M - x_lo) : 0.0f;
             double g = 0.0;
@@ -646,7 +620,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
 #define NIS_CAND(j, x)                                                            \
     {                                                                             \
-        const bool ok = (j) < ncc;                                                \
+        const bool ok = ((j) < ncc) & ((x) >= x_lo);                              \
         const float xs = ok ? (x) : x_lo;                                         \
         const float e = ok ? mass_of(xs, c, R) : 0.0f;                            \
         const int b = ok ? fine_bucket(xs, x_lo, inv_w) : kFineBins + l;          \
@@ -661,6 +635,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                 NIS_CAND(jb, xb)
 #undef NIS_CAND
             }
+            NIS_TS(4);
             g = wsum_f64(g);
             lds_put_rec(lds_addr(&sh.wc[w]), g, nw, nc);
             lds_barrier();
@@ -669,17 +644,9 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             uint32_t nww[kWaves], ncw[kWaves];
             read_recs(sh.wc, gw, nww, ncw);
             double Gc = 0.0;
-            uint32_t nwmax = 0, ncmax = 0;
 #pragma unroll
-            for (int i = 0; i < kWaves; ++i) {
-                Gc += gw[i];
-                nwmax = max(nwmax, nww[i]);
-                ncmax = max(ncmax, ncw[i]);
-            }
-            const bool ovf = (nwmax > (uint32_t)kWaveEnt) | (ncmax > (uint32_t)kWaveCand);
-            if (ovf) {
-                reject = NIS_REJECT_CAPACITY;
-            } else if (!(Gc - (double)mass_of(x_lo, c, R) > pZR)) {
+            for (int i = 0; i < kWaves; ++i) Gc += gw[i];
+            if (!(Gc - (double)mass_of(x_lo, c, R) > pZR)) {
                 // the largest element below x_lo might be kept
                 reject = NIS_REJECT_WINDOW;
             } else {
@@ -737,7 +704,9 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                         const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
                         const uint32_t ia = sh.s.ci[w][ja], ib = sh.s.ci[w][jb];
                         const bool va = ja < ncc, vb = jb < ncc;
-                        const bool sa = va & (ba > bstar), sb = vb & (bb > bstar);
+                        // (dummy buckets >= kFineBins: candidates below x_lo)
+                        const bool sa = va & (ba > bstar) & (ba < kFineBins);
+                        const bool sb = vb & (bb > bstar) & (bb < kFineBins);
                         sw += (sa ? (double)ea : 0.0) + (sb ? (double)eb : 0.0);
                         sn += (sa ? 1u : 0u) + (sb ? 1u : 0u);
 #define NIS_GATHER(v, b, x, i, e)                                                      \
@@ -904,6 +873,8 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             }
         }
         // the sparse route gave up: the dense route starts from clean buckets
+        // and a count histogram of chunks 0 and 1 (its sample), 1/16-octave
+        // bins below R
         __syncthreads();
         for (int i = tid; i < kFineBins; i += kBlock) {
             sh.fcnt[i] = 0u;
@@ -915,6 +886,16 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             sh.ncand = 0u;
             sh.overflow = 0u;
         }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float x = elem(xv[q >> 2], q & 3);
+            const float t = fmaf(x, c, -R);
+            const int b = (x > -INFINITY)
+                              ? (int)fminf(fmaxf(-t * kSampleRes, 0.0f), (float)(kSampleBins - 1))
+                              : kSampleBins + l;  // -inf (outside the row or masked): dummy bin
+            atomicAdd(&sh.scnt[b], 1u);
+        }
+        lds_barrier();
     }
 
     // ====================================================================
