@@ -323,6 +323,10 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const bool sampling = a.temperature > 0.0f;
 
     NIS_TS(0);
+    // the (at most 3 + 3) elements of the partial head / tail slots, first:
+    // the waves holding such slots need them before their first chunk
+    const float h0 = rowp[0], h1 = rowp[1], h2 = rowp[2];
+    const float t0 = rowp[V - 3], t1 = rowp[V - 2], t2 = rowp[V - 1];
     __builtin_amdgcn_sched_barrier(0);
     f4v xv[kNch];
 #pragma unroll
@@ -331,9 +335,6 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         xv[k] = __builtin_nontemporal_load(base + min(max(f, f_lo), f_hi));
         __builtin_amdgcn_sched_barrier(0);  // keep chunk order = issue order
     }
-    // the (at most 3 + 3) elements of the partial head / tail slots
-    const float h0 = rowp[0], h1 = rowp[1], h2 = rowp[2];
-    const float t0 = rowp[V - 3], t1 = rowp[V - 2], t2 = rowp[V - 1];
 
     // LDS store by the lanes where `cond` holds; the other lanes write their
     // own spare slot, so no exec-mask branch is needed
@@ -1023,7 +1024,27 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         sh.d.cell[w][k][l] = cs;
         lane_kept += (double)cs;
     }
+    // the window's fine histogram (count, mass, largest and smallest key)
+    if (topp && lpos <= kLaneCap) {
+        const float x_top = fminf(x_hi, M);
+        const float inv_wd = (x_top > x_lo) ? (float)kFineBins / (x_top - x_lo) : 0.0f;
+        const double sfix = rho * kFix;
+        #pragma unroll 1
+        for (int i = 0; i < lpos; ++i) {
+            const float x = sh.d.lx[i][tid];
+            const int fb = fine_bucket(x, x_lo, inv_wd);
+            const uint32_t key = key32(x);
+            atomicAdd(&sh.fcnt[fb], 1u);
+            atomicAdd(&sh.fmass[fb], (unsigned long long)((double)mass_of(x, c, R) * sfix));
+            atomicMax(&sh.fkmax[fb], key);
+            atomicMin(&sh.fkmin[fb], key);
+        }
+    }
     if (lpos > kLaneCap) sh.overflow = 1u;
+    {
+        const double g = wsum_f64(lane_kept);
+        NIS_PUT(l == 0, sh.db[w], g);
+    }
     lds_barrier();
     NIS_TS(11);
     if (sh.overflow) return reject != NIS_REJECT_NONE ? reject : NIS_REJECT_CAPACITY;
@@ -1033,81 +1054,75 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     double g_above_f = 0.0;
     uint32_t n_final = 0;
     if (topp) {
-        // ---- fine histogram of the window lists --------------------------
-        const float x_top = fminf(x_hi, M);
-        const float inv_w = (x_top > x_lo) ? (float)kFineBins / (x_top - x_lo) : 0.0f;
-        const double sfix = rho * kFix;
-        #pragma unroll 1
-        for (int i = 0; i < nl; ++i) {
-            const float x = sh.d.lx[i][tid];
-            const int fb = fine_bucket(x, x_lo, inv_w);
-            const uint32_t key = key32(x);
-            atomicAdd(&sh.fcnt[fb], 1u);
-            atomicAdd(&sh.fmass[fb], (unsigned long long)((double)mass_of(x, c, R) * sfix));
-            atomicMax(&sh.fkmax[fb], key);
-            atomicMin(&sh.fkmin[fb], key);
-        }
-        const double g = wsum_f64(lane_kept);
-        if (l == 0) sh.db[w] = g;
-        lds_barrier();
         double GhiR = sh.db[0];
 #pragma unroll
         for (int i = 1; i < kWaves; ++i) GhiR += sh.db[i];
 
         // ---- T4: the fine bucket holding the cutoff (wave 0) -------------
         if (w == 0) {
-            // lane l owns buckets 1023-16l .. 1008-16l (descending value),
-            // i.e. the 16 ascending buckets starting at 1008-16l
+            // lane l owns buckets 1008-16l .. 1023-16l; index i = 15 is the
+            // top one (descending value runs i = 15 .. 0, then the next lane)
             const int b0 = kFineBins - 16 - 16 * l;
-            double mlane = 0.0;
-            int lastne = -1;  // lowest non-empty bucket of this lane
-            #pragma unroll 1
-            for (int i = 0; i < 16; ++i) {
-                mlane += (double)sh.fmass[b0 + i] / kFix;
-                if (lastne < 0 && sh.fcnt[b0 + i] != 0) lastne = b0 + i;
+            uint32_t cnt[16], kmx[16];
+            unsigned long long fm[16];
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const u4v cv = *reinterpret_cast<const u4v*>(&sh.fcnt[b0 + i]);
+                const u4v kv = *reinterpret_cast<const u4v*>(&sh.fkmax[b0 + i]);
+                cnt[i] = cv.x; cnt[i + 1] = cv.y; cnt[i + 2] = cv.z; cnt[i + 3] = cv.w;
+                kmx[i] = kv.x; kmx[i + 1] = kv.y; kmx[i + 2] = kv.z; kmx[i + 3] = kv.w;
             }
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                const u4v mv = *reinterpret_cast<const u4v*>(&sh.fmass[b0 + i]);
+                fm[i] = ((unsigned long long)mv.y << 32) | mv.x;
+                fm[i + 1] = ((unsigned long long)mv.w << 32) | mv.z;
+            }
+            unsigned long long mlf = 0;  // the lane's mass in fixed point (exact sum)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mlf += fm[i];
+            const double mlane = (double)mlf / kFix;
             const double incl = wscan_f64(mlane);
             const double Ghi = GhiR * rho;
+            // mass above each bucket, walking down the lane's buckets; a
+            // bucket qualifies if its largest element is kept (sampler.rs:150)
             double G = Ghi + (incl - mlane);
-            int fstar = -1;
-            double gstar = 0.0;
+            int lowq = kFineBins;       // lowest qualifying bucket of this lane
+            double gq = 0.0;            // mass above it
+            int lastne = kFineBins;     // lowest non-empty bucket of this lane
             bool stop = false;
-            #pragma unroll 1
-            for (int i = 15; i >= 0; --i) {  // descending value
-                if (!stop && sh.fcnt[b0 + i] != 0) {
-                    const double ef = (double)mass_of(unkey32(sh.fkmax[b0 + i]), c, R) * rho;
-                    if (G - ef <= pZ) {
-                        fstar = b0 + i;
-                        gstar = G;
-                        G += (double)sh.fmass[b0 + i] / kFix;
-                    } else {
-                        stop = true;
-                    }
-                }
-            }
-            // D_first is non-decreasing down the buckets, so the qualifying
-            // buckets form a prefix: the cutoff bucket is the lowest of them
-            int best = (fstar >= 0) ? (kFineBins - fstar) : -1;
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) best = max(best, __shfl_xor(best, o));
-            int lowest = (lastne >= 0) ? (kFineBins - lastne) : -1;
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) lowest = max(lowest, __shfl_xor(lowest, o));
-            const double Gtot = __shfl(incl, 63) + Ghi;
-            const int owner = (best > 0) ? ((best - 1) / 16) : 0;
-            const double gs = __shfl(gstar, owner);
-            if (l == 0) {
-                int ok = 1;
-                // every element above the window must be kept
-                if (x_hi < INFINITY && !(Ghi - (double)mass_of(x_hi, c, R) * rho <= pZ)) ok = 0;
-                if (best < 0) ok = 0;
-                // cutoff in the lowest bucket: the first element below the
-                // window must be removed
-                if (ok && best == lowest && !(Gtot - (double)mass_of(x_lo, c, R) * rho > pZ)) ok = 0;
-                sh.bi[0] = ok;
-                sh.bi[1] = ok ? (kFineBins - best) : 0;
-                sh.bd[0] = gs;
+            for (int i = 15; i >= 0; --i) {
+                const bool ne = cnt[i] != 0;
+                const double ef = (double)mass_of(unkey32(kmx[i]), c, R) * rho;
+                const bool q = ne & !stop & (G - ef <= pZ);
+                stop = stop | (ne & !q);
+                lowq = q ? (b0 + i) : lowq;
+                gq = q ? G : gq;
+                lastne = ne ? (b0 + i) : lastne;
+                G += (double)fm[i] / kFix;
             }
+            // qualifying buckets form a prefix from the top: the cutoff
+            // bucket is the lowest of them (DPP minima of bucket indices;
+            // exact in float)
+            const float lowf = -wmax_f32(-(float)lowq);
+            const int best = (int)lowf;
+            const float nef = -wmax_f32(-(float)lastne);
+            const int lowest = (int)nef;
+            const double Gtot = bcast_f64(incl, 63) + Ghi;
+            const uint64_t own = __ballot(lowq == best);
+            const int owner = own ? (__ffsll((long long)own) - 1) : 0;
+            const double gs = bcast_f64(gq, owner);
+            int ok = 1;
+            // every element above the window must be kept
+            if (x_hi < INFINITY && !(Ghi - (double)mass_of(x_hi, c, R) * rho <= pZ)) ok = 0;
+            if (best >= kFineBins) ok = 0;
+            // cutoff in the lowest bucket: the first element below the
+            // window must be removed
+            if (ok && best == lowest && !(Gtot - (double)mass_of(x_lo, c, R) * rho > pZ)) ok = 0;
+            NIS_PUT(l == 0, sh.bi[0], ok);
+            NIS_PUT(l == 0, sh.bi[1], ok ? best : 0);
+            NIS_PUT(l == 0, sh.bd[0], gs);
         }
         lds_barrier();
         NIS_TS(12);
@@ -1141,19 +1156,22 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         if (w == 0) {
             const int n = (int)n_final;
             const bool valid = l < n;
-            const float xm = valid ? sh.d.cx[l] : -INFINITY;
+            const int lc = min(l, kMaxFinal - 1);
+            const float cxv = sh.d.cx[lc];
+            const uint32_t cjv = sh.d.cj[lc];
+            const float xm = valid ? cxv : -INFINITY;
             const uint32_t km = key32(xm);
-            const uint32_t im = valid ? sh.d.cj[l] : 0u;
+            const uint32_t im = valid ? cjv : 0u;
             const double em = valid ? (double)mass_of(xm, c, R) * rho : 0.0;
             double pre = 0.0;  // mass of the members ahead in the stable descending order
             #pragma unroll 1
             for (int j = 0; j < n; ++j) {
                 const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
                 const double ej = bcast_f64(em, j);
-                pre += (kj > km || (kj == km && ij < im)) ? ej : 0.0;
+                pre += ((kj > km) | ((kj == km) & (ij < im))) ? ej : 0.0;
             }
             // sampler.rs:150: removed iff cum_excl - q > p; kept otherwise
-            const bool kept = valid && (g_above_f + pre - em <= pZ);
+            const bool kept = valid & (g_above_f + pre - em <= pZ);
             if (kept) {
                 const uint32_t loc = sh.d.cloc[l];
                 sh.d.lp[loc % kLaneCap][loc / kLaneCap] |= kKeptBit;
@@ -1187,35 +1205,22 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     }
     NIS_RNG_DRAW()
     lds_barrier();
-    double zk = 0.0;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) zk += sh.wtot[i];
+    // per-wave totals (lanes 0..7), their prefix and the wave holding the
+    // crossing: the first whose running total reaches r (and has mass);
+    // rounding: the last wave with mass
     const double u = sh.bd[1];
-    const double r = u * zk;
-    int wsel = -1;
-    double wbase = 0.0;
+    double zk, r, wbase;
+    int wsel;
     {
-        double acc = 0.0;
-#pragma unroll
-        for (int i = 0; i < kWaves; ++i) {
-            const double nx = acc + sh.wtot[i];
-            if (wsel < 0 && nx >= r && sh.wtot[i] > 0.0) {
-                wsel = i;
-                wbase = acc;
-            }
-            acc = nx;
-        }
-        if (wsel < 0) {  // rounding: the last wave with mass
-            acc = 0.0;
-#pragma unroll
-            for (int i = 0; i < kWaves; ++i) {
-                if (sh.wtot[i] > 0.0) {
-                    wsel = i;
-                    wbase = acc;
-                }
-                acc += sh.wtot[i];
-            }
-        }
+        const int li = min(l, kWaves - 1);
+        const double Tw = (l < kWaves) ? sh.wtot[li] : 0.0;
+        const double Twi = wscan_f64(Tw);
+        zk = bcast_f64(Twi, 63);
+        r = u * zk;
+        const uint64_t hw = __ballot((l < kWaves) & (Tw > 0.0) & (Twi >= r));
+        const uint64_t nzw = __ballot((l < kWaves) & (Tw > 0.0));
+        wsel = hw ? (__ffsll((long long)hw) - 1) : (nzw ? (63 - __clzll((long long)nzw)) : 0);
+        wbase = bcast_f64(Twi - Tw, wsel);
     }
     wsel = __builtin_amdgcn_readfirstlane(wsel);
     if (w == wsel) {  // static register indices only (a dynamic one would demote xv to scratch)
@@ -1226,33 +1231,20 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     #pragma unroll 1
     for (int kk = w; kk < kNch; kk += kWaves) {
         const double cv = wsum_f64((double)sh.d.cell[wsel][kk][l]);
-        if (l == 0) sh.ctot[kk] = cv;
+        NIS_PUT(l == 0, sh.ctot[kk], cv);
     }
     lds_barrier();
-    int ksel = -1;
-    double kbase = wbase;
+    // the chunk holding the crossing (lanes 0..kNch-1), as for the waves
+    int ksel;
+    double kbase;
     {
-        double cb = wbase;
-        #pragma unroll 1
-        for (int k = 0; k < kNch; ++k) {
-            const double nb = cb + sh.ctot[k];
-            if (ksel < 0 && nb >= r && sh.ctot[k] > 0.0) {
-                ksel = k;
-                kbase = cb;
-            }
-            cb = nb;
-        }
-        if (ksel < 0) {  // rounding: the last chunk with mass
-            cb = wbase;
-            #pragma unroll 1
-            for (int k = 0; k < kNch; ++k) {
-                if (sh.ctot[k] > 0.0) {
-                    ksel = k;
-                    kbase = cb;
-                }
-                cb += sh.ctot[k];
-            }
-        }
+        const int lk = min(l, kNch - 1);
+        const double Ck = (l < kNch) ? sh.ctot[lk] : 0.0;
+        const double Cki = wscan_f64(Ck);
+        const uint64_t hk = __ballot((l < kNch) & (Ck > 0.0) & (wbase + Cki >= r));
+        const uint64_t nzk = __ballot((l < kNch) & (Ck > 0.0));
+        ksel = hk ? (__ffsll((long long)hk) - 1) : (nzk ? (63 - __clzll((long long)nzk)) : 0);
+        kbase = wbase + bcast_f64(Cki - Ck, ksel);
     }
     ksel = __builtin_amdgcn_readfirstlane(ksel);
     if (w == wsel) {

@@ -1,9 +1,17 @@
-// general_path.h — the general per-row sampler: one 1024-lane workgroup per
+// general_path.h — the general per-row sampler: one 512-lane workgroup per
 // row, any V <= NIS_MAX_V, repetition penalty, top-k, top-p and every
 // special case of sample() (src/sampler.rs:163-217).  It makes several
-// passes over the row (re-read through L2 / MALL), computes in f64 with the
-// device libm `exp`, and is used for rows the register-resident fast path
-// does not take (penalty, top-k, non-finite input, V above its capacity).
+// passes over the row (the first from HBM, the others mostly from L2 /
+// MALL), each with kGU loads in flight per lane, and is used for the rows
+// the register-resident fast path does not take (penalty, top-k, non-finite
+// input, V above its capacity) or hands on.
+//
+// Masses: without a penalty a row's masses are 2^(x*c - R) in f32 (c =
+// log2(e)/T, R = ceil(M*c)), the same values as the fast path's; with a
+// penalty the f64 value w = v/T gives 2^((w - M/T) * log2 e), evaluated as an
+// f32 exp2 of the leading part times a first-order correction for the rest
+// (relative error ~1e-7).  Sums are f64; histogram masses are 2^-40 fixed
+// point (exact and order-independent).
 //
 // Sort-free top-p (sampler.rs:118-160): the reference keeps sorted position
 // pos iff D(pos) = cum_excl(pos) - q(pos) <= p (normalised).  D is
@@ -13,6 +21,10 @@
 // last bucket whose first (largest-key) element is kept: G - e_first <= p*Z.
 // At the last digit the bucket is one key value K*, i.e. a tie group whose
 // members are kept in ascending index order while G + (j-1)*e* <= p*Z.
+//
+// The inverse-CDF walk (sampler.rs:209-216) runs over chunks of kGChunk
+// consecutive elements: their kept masses, a prefix over the chunks, and one
+// wave's scan of the chunk holding the crossing.
 #pragma once
 #include <math.h>
 
@@ -37,12 +49,18 @@ struct RowArgs {
     nis_row_stats* stats;
 };
 
+constexpr int kGU = 16;                          // loads per lane per block of a pass
+constexpr int kGChunk = 512;                     // walk chunk: 64 lanes x 8 elements
+constexpr int kGMaxChunks = NIS_MAX_V / kGChunk;
+constexpr double kGFix = 1099511627776.0;        // 2^40 fixed-point mass scale
+
 struct GeneralShared {
     uint32_t bitmap[NIS_MAX_V / 32];  // penalised-id set of the row
     uint32_t hcnt[256];
-    double hmass[256];
+    unsigned long long hmass[256];    // 2^-40 fixed point
     unsigned long long hkey[256];
-    double incl[kBlock];              // per-thread inclusive kept-mass prefix
+    double csum[kGMaxChunks];         // kept mass of each walk chunk
+    uint32_t tcnt[kGMaxChunks];       // tie-group members before each walk chunk
     double dscr[kWaves];
     uint64_t uscr[kWaves];
     int64_t iscr[kWaves];
@@ -97,10 +115,87 @@ __device__ __forceinline__ bool in_prefix(uint64_t key, int shift, uint64_t pref
     return (shift + 8 >= 64) ? true : ((key >> (shift + 8)) == prefix);
 }
 
+// Every element j of the row with its raw logit xr (element order within a
+// lane is ascending j).  Whole blocks of kGU loads per lane, the next
+// block's loads issued before the current one is processed (its indices
+// clamped into the row, so the last prefetch stays in bounds), then the
+// partial last block with a bounds test.
+#define NIS_G_EACH(BODY)                                                          \
+    {                                                                             \
+        const int64_t gstep_ = (int64_t)kBlock * kGU;                             \
+        const int64_t gfull_ = (V / gstep_) * gstep_;                             \
+        float xs_[kGU], xn_[kGU];                                                 \
+        if (gfull_ > 0) {                                                         \
+            _Pragma("unroll") for (int u_ = 0; u_ < kGU; ++u_) xs_[u_] =          \
+                x[tid + (int64_t)u_ * kBlock];                                    \
+        }                                                                         \
+        for (int64_t jb_ = tid; jb_ < gfull_; jb_ += gstep_) {                    \
+            _Pragma("unroll") for (int u_ = 0; u_ < kGU; ++u_) xn_[u_] =          \
+                x[min(jb_ + gstep_ + (int64_t)u_ * kBlock, V - 1)];               \
+            _Pragma("unroll") for (int u_ = 0; u_ < kGU; ++u_) {                  \
+                const int64_t j = jb_ + (int64_t)u_ * kBlock;                     \
+                const float xr = xs_[u_];                                         \
+                BODY                                                              \
+            }                                                                     \
+            _Pragma("unroll") for (int u_ = 0; u_ < kGU; ++u_) xs_[u_] = xn_[u_];  \
+        }                                                                         \
+        for (int64_t j = gfull_ + tid; j < V; j += kBlock) {                      \
+            const float xr = x[j];                                                \
+            BODY                                                                  \
+        }                                                                         \
+    }
+
+// Wave 0, top-p radix step: the digit buckets d = 255 .. 0 (descending key)
+// with count, fixed-point mass and largest key; G0 = mass above them.
+// Returns (uniform across the wave) the lowest bucket whose largest element
+// is kept (sampler.rs:150: G(d) - e_first(d) <= pZ; qualifying buckets form
+// a prefix from the top), the mass above it and its count.
+template <typename MassOfKey>
+__device__ __forceinline__ void topp_digit_select(const GeneralShared& sh, double G0, double pZ,
+                                                  MassOfKey mass_of_key, int* sel, double* gsel,
+                                                  uint32_t* nsel) {
+    const int l = lane_id();
+    // lane l owns buckets 4l .. 4l+3 (ascending key)
+    uint32_t cnt[4];
+    unsigned long long fm[4], km[4];
+    unsigned long long ltot = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        cnt[i] = sh.hcnt[4 * l + i];
+        fm[i] = sh.hmass[4 * l + i];
+        km[i] = sh.hkey[4 * l + i];
+        ltot += fm[i];
+    }
+    // mass of the buckets of higher lanes (exact: integer sums below 2^53)
+    const double lt = (double)ltot;
+    const double incl = wscan_f64(lt);
+    const double tot = bcast_f64(incl, 63);
+    double above = tot - incl;  // fixed point
+    int low = 256;
+    double glow = 0.0;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) {
+        const double G = G0 + above / kGFix;
+        const bool q = (cnt[i] != 0) && (G - mass_of_key(km[i]) <= pZ);
+        low = q ? (4 * l + i) : low;
+        glow = q ? G : glow;
+        above += (double)fm[i];
+    }
+    const int best = (int)(-wmax_f32(-(float)low));  // DPP minimum (exact in float)
+    const uint64_t own = __ballot(low == best);
+    const int owner = own ? (__ffsll((long long)own) - 1) : 0;
+    *sel = best;
+    *gsel = bcast_f64(glow, owner);
+    *nsel = (best < 256) ? sh.hcnt[best] : 0u;
+}
+
 // `reject` is recorded in the row's stats: why the fast path declined it.
-__device__ __noinline__ void general_row(const RowArgs a, const int row, GeneralShared& sh,
-                                         const uint32_t reject) {
-    const int tid = threadIdx.x;
+// SIMPLE: a row without a penalty whose masses have a finite f32 reference;
+// the SIMPLE form returns false, having written nothing, for any other row.
+template <bool SIMPLE>
+__device__ __noinline__ bool general_row_t(const RowArgs a, const int row, GeneralShared& sh,
+                                           const uint32_t reject) {
+    const int tid = threadIdx.x, l = lane_id(), w = wave_id();
     const float* __restrict__ x = a.logits + (int64_t)row * a.ld;
     const int64_t V = a.V;
 
@@ -108,7 +203,8 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
     bool pen = false;
     if (a.penalty != 1.0f && a.gen_ids != nullptr && a.gen_off != nullptr) {
         const int64_t g0 = a.gen_off[row], g1 = a.gen_off[row + 1];
-        if (g1 > g0) {
+        if (SIMPLE && g1 > g0) return false;
+        if (!SIMPLE && g1 > g0) {
             pen = true;
             const int64_t nw = (V + 31) >> 5;
             for (int64_t i = tid; i < nw; i += kBlock) sh.bitmap[i] = 0u;
@@ -121,35 +217,34 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
         }
     }
     const double penf = (double)a.penalty;
-    auto val = [&](int64_t j) -> double {
-        double v = (double)x[j];
-        if (pen && ((sh.bitmap[j >> 5] >> (j & 31)) & 1u)) v = (v > 0.0) ? v / penf : v * penf;
+    auto pval = [&](int64_t j, float xr) -> double {
+        double v = (double)xr;
+        if constexpr (!SIMPLE) {
+            if (pen && ((sh.bitmap[j >> 5] >> (j & 31)) & 1u)) v = (v > 0.0) ? v / penf : v * penf;
+        }
         return v;
     };
+    auto val = [&](int64_t j) -> double { return pval(j, x[j]); };
 
     // ---- pass 1: max, first / last index of the max, NaN / +inf ---------
     double vmax = -INFINITY;
     int64_t ifirst = INT64_MAX, ilast = -1;
-    uint64_t flags = 0;  // bit0 NaN, bit1 +inf
-    for (int64_t j = tid; j < V; j += kBlock) {
-        const double v = val(j);
-        if (v != v) {
-            flags |= 1;
-            continue;
-        }
-        if (ifirst == INT64_MAX || v > vmax) {
-            vmax = v;
-            ifirst = j;
-            ilast = j;
-        } else if (v == vmax) {
-            ilast = j;
-        }
-        if (v == INFINITY) flags |= 2;
-    }
+    uint32_t flg = 0;  // bit0 NaN, bit1 +inf
+    NIS_G_EACH({
+        const double v = pval(j, xr);
+        const bool nan = v != v;
+        flg |= nan ? 1u : 0u;
+        flg |= (v == INFINITY) ? 2u : 0u;
+        const bool gt = !nan && (ifirst == INT64_MAX || v > vmax);
+        const bool eq = !nan && !gt && v == vmax;
+        vmax = gt ? v : vmax;
+        ifirst = gt ? j : ifirst;
+        ilast = (gt || eq) ? j : ilast;
+    })
     const double M = block_max(vmax, sh.dscr);
     ifirst = block_min(vmax == M ? ifirst : INT64_MAX, sh.iscr);
     ilast = block_max(vmax == M ? ilast : (int64_t)-1, sh.iscr);
-    flags = block_or(flags, sh.uscr);
+    const uint64_t flags = block_or((uint64_t)flg, sh.uscr);
     const bool any_nan = flags & 1, any_pinf = flags & 2;
     const bool nan0 = (val(0) != val(0));
 
@@ -160,7 +255,7 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
             const uint32_t tok = (nan0 || ifirst == INT64_MAX) ? 0u : (uint32_t)ifirst;
             write_row_result(a, row, tok, NIS_PATH_GREEDY, 0.0, 0.0, 0.0, -1.0, 0.0, 0, 2, reject);
         }
-        return;
+        return true;
     }
 
     const double temp = fmax((double)a.temperature, 1e-6);  // sampler.rs:183
@@ -192,25 +287,49 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
             }
             write_row_result(a, row, tok, path, M_w, 0.0, 0.0, -1.0, 0.0, 0, 2, reject);
         }
-        return;
+        return true;
     }
 
     // Keys: penalised rows use the f64 key of w = v / T; other rows the f32
     // key of the logit (dividing by T > 0 preserves order and ties).
     auto keyof = [&](double v) -> uint64_t {
-        return pen ? key64(v / temp) : ((uint64_t)key32((float)v) << 32);
-    };
-    auto key_w = [&](uint64_t k) -> double {
-        return pen ? unkey64(k) : (double)unkey32((uint32_t)(k >> 32)) / temp;
+        if constexpr (SIMPLE) return (uint64_t)key32((float)v) << 32;
+        else return pen ? key64(v / temp) : ((uint64_t)key32((float)v) << 32);
     };
     const uint64_t kmax = keyof(M);
+
+    // Masses (see the header): f32 2^(x*c - R) when the row has no penalty
+    // and a finite reference; otherwise relative to the max, 2^((w - M_w)
+    // log2 e).  `rho` turns the first form into units of the max element.
+    const float cf = (float)(1.4426950408889634 / temp);
+    const bool mf32 = !pen && fabsf((float)M * cf) < 1e30f;
+    if (SIMPLE && !mf32) return false;  // nothing written yet
+    const float Rf = mf32 ? ceilf((float)M * cf) : 0.0f;
+    const double rho = mf32 ? (double)__builtin_amdgcn_exp2f(-fmaf((float)M, cf, -Rf)) : 1.0;
+    auto mass_w = [&](double wv) -> double {  // wv = value / T (penalised rows)
+        const double t = (wv - M_w) * 1.4426950408889634;
+        const float th = (float)t;
+        return (double)__builtin_amdgcn_exp2f(th) * (1.0 + (t - (double)th) * 0.6931471805599453);
+    };
+    auto massv = [&](double v, float xr) -> double {
+        if constexpr (SIMPLE) return (double)__builtin_amdgcn_exp2f(fmaf(xr, cf, -Rf));
+        else return mf32 ? (double)__builtin_amdgcn_exp2f(fmaf(xr, cf, -Rf)) : mass_w(v / temp);
+    };
+    auto mass_of_key = [&](uint64_t k) -> double {
+        const float xk = unkey32((uint32_t)(k >> 32));
+        if constexpr (SIMPLE) return (double)__builtin_amdgcn_exp2f(fmaf(xk, cf, -Rf));
+        else {
+            if (pen) return mass_w(unkey64(k));
+            return mf32 ? (double)__builtin_amdgcn_exp2f(fmaf(xk, cf, -Rf)) : mass_w((double)xk / temp);
+        }
+    };
 
     // ---- top-k (sampler.rs:103-116): keep keys >= key of the k-th largest
     uint64_t kth = 0;
     const bool topk_on = a.top_k > 0 && a.top_k < (uint64_t)V;
     if (topk_on) {
         uint64_t diff = 0;
-        for (int64_t j = tid; j < V; j += kBlock) diff |= keyof(val(j)) ^ kmax;
+        NIS_G_EACH({ diff |= keyof(pval(j, xr)) ^ kmax; })
         const DigitRange dr = digit_range(block_or(diff, sh.uscr));
         uint64_t prefix = (dr.hi_shift + 8 >= 64) ? 0 : (kmax >> (dr.hi_shift + 8));
         uint64_t remaining = a.top_k;
@@ -219,23 +338,41 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
                 __syncthreads();
                 if (tid < 256) sh.hcnt[tid] = 0;
                 __syncthreads();
-                for (int64_t j = tid; j < V; j += kBlock) {
-                    const uint64_t k = keyof(val(j));
+                NIS_G_EACH({
+                    const uint64_t k = keyof(pval(j, xr));
                     if (in_prefix(k, shift, prefix)) atomicAdd(&sh.hcnt[(k >> shift) & 255], 1u);
-                }
+                })
                 __syncthreads();
-                if (tid == 0) {
-                    uint64_t cum = 0;
-                    int sel = 0;
-                    for (int d = 255; d >= 0; --d) {
-                        if (cum + sh.hcnt[d] >= remaining) {
-                            sel = d;
-                            break;
-                        }
-                        cum += sh.hcnt[d];
+                if (w == 0) {
+                    // the bucket holding the remaining-th largest key: the
+                    // largest d whose count from the top reaches `remaining`
+                    uint32_t cnt[4];
+                    uint32_t lt = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        cnt[i] = sh.hcnt[4 * l + i];
+                        lt += cnt[i];
                     }
-                    sh.bi[0] = sel;
-                    sh.bi[1] = (int64_t)(remaining - cum);
+                    const uint32_t incl = wscan_u32(lt);
+                    const uint32_t tot = bcast_u32(incl, 63);
+                    uint64_t fromtop = tot - incl;  // keys in higher lanes
+                    int selb = -1;
+                    uint64_t cum = 0;
+#pragma unroll
+                    for (int i = 3; i >= 0; --i) {
+                        const bool hit = (fromtop + cnt[i] >= remaining) && selb < 0;
+                        selb = hit ? (4 * l + i) : selb;
+                        cum = hit ? fromtop : cum;
+                        fromtop += cnt[i];
+                    }
+                    const int best = (int)wmax_f32((float)selb);  // highest d (exact in float)
+                    const uint64_t own = __ballot(selb == best && best >= 0);
+                    const int owner = own ? (__ffsll((long long)own) - 1) : 0;
+                    const uint32_t cumb = bcast_u32((uint32_t)cum, owner);
+                    if (l == 0) {
+                        sh.bi[0] = best < 0 ? 0 : best;
+                        sh.bi[1] = (int64_t)(remaining - cumb);
+                    }
                 }
                 __syncthreads();
                 prefix = (prefix << 8) | (uint64_t)sh.bi[0];
@@ -255,13 +392,13 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
     if (topp_on) {
         double zl = 0.0;
         uint64_t diff = 0;
-        for (int64_t j = tid; j < V; j += kBlock) {
-            const double v = val(j);
+        NIS_G_EACH({
+            const double v = pval(j, xr);
             const uint64_t k = keyof(v);
-            if (k < kth) continue;
-            zl += exp(v / temp - M_w);
-            diff |= k ^ kmax;
-        }
+            const bool live = k >= kth;
+            zl += live ? massv(v, xr) : 0.0;
+            diff |= live ? (k ^ kmax) : 0ull;
+        })
         z_all = block_sum(zl, sh.dscr);
         const DigitRange dr = digit_range(block_or(diff, sh.uscr));
         const double pZ = (double)p * z_all;
@@ -272,37 +409,33 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
                 __syncthreads();
                 if (tid < 256) {
                     sh.hcnt[tid] = 0;
-                    sh.hmass[tid] = 0.0;
+                    sh.hmass[tid] = 0ull;
                     sh.hkey[tid] = 0ull;
                 }
                 __syncthreads();
-                for (int64_t j = tid; j < V; j += kBlock) {
-                    const double v = val(j);
+                NIS_G_EACH({
+                    const double v = pval(j, xr);
                     const uint64_t k = keyof(v);
-                    if (k < kth || !in_prefix(k, shift, prefix)) continue;
-                    const int d = (int)((k >> shift) & 255);
-                    atomicAdd(&sh.hcnt[d], 1u);
-                    atomicAdd(&sh.hmass[d], exp(v / temp - M_w));
-                    atomicMax(&sh.hkey[d], (unsigned long long)k);
-                }
-                __syncthreads();
-                if (tid == 0) {
-                    double g = G, g_sel = G;
-                    int sel = -1;
-                    for (int d = 255; d >= 0; --d) {
-                        if (sh.hcnt[d] == 0) continue;
-                        const double ef = exp(key_w(sh.hkey[d]) - M_w);
-                        if (g - ef <= pZ) {
-                            sel = d;
-                            g_sel = g;
-                            g += sh.hmass[d];
-                        } else {
-                            break;
-                        }
+                    if (k >= kth && in_prefix(k, shift, prefix)) {
+                        const int d = (int)((k >> shift) & 255);
+                        atomicAdd(&sh.hcnt[d], 1u);
+                        atomicAdd(&sh.hmass[d], (unsigned long long)(massv(v, xr) * kGFix));
+                        atomicMax(&sh.hkey[d], (unsigned long long)k);
                     }
-                    sh.bi[0] = sel < 0 ? 0 : sel;  // sel >= 0: the first bucket holds a kept element
-                    sh.bi[1] = sel < 0 ? 0 : sh.hcnt[sel];
-                    sh.bd[0] = g_sel;
+                })
+                __syncthreads();
+                if (w == 0) {
+                    int sel;
+                    double gsel;
+                    uint32_t nsel;
+                    topp_digit_select(sh, G, pZ, mass_of_key, &sel, &gsel, &nsel);
+                    if (l == 0) {
+                        // sel < 256: a bucket holds a kept element (the first
+                        // key of the current range always is)
+                        sh.bi[0] = sel < 256 ? sel : 0;
+                        sh.bi[1] = sel < 256 ? (int64_t)nsel : 0;
+                        sh.bd[0] = sel < 256 ? gsel : G;
+                    }
                 }
                 __syncthreads();
                 prefix = (prefix << 8) | (uint64_t)sh.bi[0];
@@ -314,10 +447,10 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
         } else {
             kstar = kmax;
             int64_t cnt = 0;
-            for (int64_t j = tid; j < V; j += kBlock) cnt += (keyof(val(j)) == kmax) ? 1 : 0;
+            NIS_G_EACH({ cnt += (keyof(pval(j, xr)) == kmax) ? 1 : 0; })
             n_tie = block_sum(cnt, sh.iscr);
         }
-        const double es = exp(key_w(kstar) - M_w);
+        const double es = mass_of_key(kstar);
         const double q = (pZ - G) / es;  // >= -1 for the selected key
         if (!(q < (double)n_tie)) n_keep = n_tie;
         else n_keep = min(n_tie, (int64_t)floor(q) + 2);
@@ -329,101 +462,218 @@ __device__ __noinline__ void general_row(const RowArgs a, const int row, General
     const int mode = topp_zero ? 2 : (topp_on ? 1 : 0);
     const bool tie_split = (mode == 1) && (n_keep < n_tie);
 
-    // ---- contiguous index ranges for the in-order walk ------------------
-    const int64_t L = (V + kBlock - 1) / kBlock;
-    const int64_t j0 = min((int64_t)tid * L, V), j1 = min(j0 + L, V);
-
-    int64_t tie_base = 0;
-    if (tie_split) {
-        int64_t c = 0;
-        for (int64_t j = j0; j < j1; ++j) c += (keyof(val(j)) == kstar) ? 1 : 0;
-        int64_t tot;
-        const int64_t inc = block_inclusive_scan(c, sh.iscr, &tot);
-        tie_base = inc - c;
-    }
-    auto kept_at = [&](int64_t j, uint64_t k, int64_t& tie_rank) -> bool {
-        if (mode == 2) return j == ilast;
-        if (k < kth) return false;
-        if (mode == 0) return true;
-        if (k > kstar) return true;
-        if (k < kstar) return false;
-        const bool keep = tie_rank < n_keep;
-        ++tie_rank;
-        return keep;
+    // ---- walk chunks: chunk c = elements [c*kGChunk, (c+1)*kGChunk), wave
+    // c % kWaves, lane l its 8 consecutive elements from c*kGChunk + 8l ----
+    const int64_t nch = (V + kGChunk - 1) / kGChunk;
+    auto load8 = [&](int64_t c, float* xs) {
+        const int64_t j0 = c * kGChunk + 8 * l;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xs[e] = x[min(j0 + e, V - 1)];
     };
-
-    double s = 0.0;
-    int64_t nk = 0;
-    {
-        int64_t tr = tie_base;
-        for (int64_t j = j0; j < j1; ++j) {
-            const double v = val(j);
-            const uint64_t k = keyof(v);
-            if (kept_at(j, k, tr)) {
-                s += exp(v / temp - M_w);
-                ++nk;
+    // tie-group members (key == kstar) before each chunk, when only some of
+    // them are kept (ties are kept in ascending index order)
+    if (tie_split) {
+        for (int64_t cc = w; cc < nch; cc += kWaves) {
+            float xs[8];
+            load8(cc, xs);
+            uint32_t tl = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t j = cc * kGChunk + 8 * l + e;
+                tl += (j < V && keyof(pval(j, xs[e])) == kstar) ? 1u : 0u;
+            }
+            const uint32_t tc = wsum_u32(tl);
+            if (l == 0) sh.tcnt[cc] = tc;
+        }
+        __syncthreads();
+        if (w == 0) {  // exclusive prefix over the chunks, in place
+            uint32_t run = 0;
+            for (int64_t c0 = 0; c0 < nch; c0 += 64) {
+                const int64_t cc = c0 + l;
+                const uint32_t v = (cc < nch) ? sh.tcnt[cc] : 0u;
+                const uint32_t inc = wscan_u32(v);
+                if (cc < nch) sh.tcnt[cc] = run + inc - v;
+                run += bcast_u32(inc, 63);
             }
         }
+        __syncthreads();
     }
-    double z_kept;
-    const double I = block_inclusive_scan(s, sh.dscr, &z_kept);
-    sh.incl[tid] = I;
-    const int64_t kept_total = block_sum(nk, sh.iscr);  // contains a barrier: incl[] visible after it
+    // kept flags and masses of a lane's 8 elements of chunk cc
+    auto chunk_kept = [&](int64_t cc, const float* xs, uint32_t tie_base, double* e8,
+                          uint32_t* kmask) {
+        uint32_t tl = 0;
+        uint32_t ties[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t j = cc * kGChunk + 8 * l + e;
+            const bool in = j < V;
+            const double v = pval(j, xs[e]);
+            const uint64_t k = keyof(v);
+            ties[e] = (in && tie_split && k == kstar) ? 1u : 0u;
+            tl += ties[e];
+        }
+        // tie rank of this lane's first tie member
+        uint32_t tr = tie_split ? (tie_base + wscan_u32(tl) - tl) : 0u;
+        uint32_t km = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t j = cc * kGChunk + 8 * l + e;
+            const bool in = j < V;
+            const double v = pval(j, xs[e]);
+            const uint64_t k = keyof(v);
+            bool kp;
+            if (mode == 2) kp = (j == ilast);
+            else if (k < kth) kp = false;
+            else if (mode == 0) kp = true;
+            else if (k > kstar) kp = true;
+            else if (k < kstar) kp = false;
+            else kp = tie_split ? ((int64_t)tr < n_keep) : true;
+            tr += ties[e];
+            kp = kp && in;
+            km |= kp ? (1u << e) : 0u;
+            e8[e] = kp ? massv(v, xs[e]) : 0.0;
+        }
+        *kmask = km;
+    };
 
-    if (!(z_kept > 0.0) || !(z_kept < INFINITY)) {  // sampler.rs:206-208
-        if (tid == 0)
-            write_row_result(a, row, 0u, NIS_PATH_BAD_TOTAL, M_w, z_kept, z_all, -1.0, 0.0,
-                             (uint64_t)kept_total, 2, reject);
-        return;
+    // ---- kept mass of every chunk ----------------------------------------
+    int64_t nk = 0;
+    float xn8[8];
+    if (w < nch) load8(w, xn8);
+    for (int64_t cc = w; cc < nch; cc += kWaves) {
+        float xs[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xs[e] = xn8[e];
+        load8(min(cc + kWaves, nch - 1), xn8);  // the next chunk, in flight meanwhile
+        double e8[8];
+        uint32_t km;
+        chunk_kept(cc, xs, tie_split ? sh.tcnt[cc] : 0u, e8, &km);
+        double s = 0.0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += e8[e];
+        nk += __popc(km);
+        const double cs = wsum_f64(s);
+        if (l == 0) sh.csum[cc] = cs;
     }
-    if (tid == 0) {  // sampler.rs:209 — the only RNG advance of the call
-        uint64_t st[4];
-        uint64_t* sp = a.rng + 4 * (int64_t)row;
+    const int64_t kept_total = block_sum(nk, sh.iscr);  // contains a barrier: csum[] visible after it
+
+    // ---- wave 0: the total, the draw, the chunk, lane and element of the
+    // crossing (sampler.rs:209-216) -----------------------------------------
+    if (w != 0) return true;
+    const int64_t per = (nch + 63) / 64;  // chunks per lane, in order
+    double ls = 0.0;
+    for (int64_t i = 0; i < per; ++i) {
+        const int64_t cc = (int64_t)l * per + i;
+        ls += (cc < nch) ? sh.csum[cc] : 0.0;
+    }
+    const double lincl = wscan_f64(ls);
+    const double z_kept = bcast_f64(lincl, 63);
+    const double zkM = z_kept * rho, zaM = z_all * rho;
+    if (!(z_kept > 0.0) || !(z_kept < INFINITY)) {  // sampler.rs:206-208
+        if (l == 0)
+            write_row_result(a, row, 0u, NIS_PATH_BAD_TOTAL, M_w, zkM, zaM, -1.0, 0.0,
+                             (uint64_t)kept_total, 2, reject);
+        return true;
+    }
+    uint64_t st[4];  // sampler.rs:209 — the only RNG advance of the call
+    {
+        const uint64_t* sp = a.rng + 4 * (int64_t)row;
         st[0] = sp[0];
         st[1] = sp[1];
         st[2] = sp[2];
         st[3] = sp[3];
-        sh.bd[1] = rng_next_f64(st);
+    }
+    const double u = rng_next_f64(st);
+    if (l == 0) {
+        uint64_t* sp = a.rng + 4 * (int64_t)row;
         sp[0] = st[0];
         sp[1] = st[1];
         sp[2] = st[2];
         sp[3] = st[3];
     }
-    __syncthreads();
-    const double u = sh.bd[1];
     const double r = u * z_kept;
-    // first thread whose inclusive prefix reaches r (exists: r < z_kept)
-    const int64_t tsel = block_min((I >= r) ? (int64_t)tid : (int64_t)INT64_MAX, sh.iscr);
-    if ((int64_t)tid == tsel) {
-        double run = (tid == 0) ? 0.0 : sh.incl[tid - 1];
-        int64_t tr = tie_base;
-        int64_t tok = -1, last_kept = -1;
-        double etok = 0.0;
-        bool ktok = false;
-        for (int64_t j = j0; j < j1; ++j) {
-            const double v = val(j);
-            const uint64_t k = keyof(v);
-            const bool kp = kept_at(j, k, tr);
-            double e = 0.0;
-            if (kp) {
-                e = exp(v / temp - M_w);
-                run += e;
-                last_kept = j;
+    // the lane whose chunks hold the crossing: the first whose running total
+    // reaches r with mass of its own; rounding: the last lane with mass
+    const uint64_t hl = __ballot((lincl >= r) & (ls > 0.0));
+    const uint64_t nzl = __ballot(ls > 0.0);
+    const int L = hl ? (__ffsll((long long)hl) - 1) : (63 - __clzll((long long)nzl));
+    int64_t csel = -1, clast = -1;
+    double cbase = 0.0, clbase = 0.0;
+    {
+        double run = bcast_f64(lincl - ls, L);
+        for (int64_t i = 0; i < per; ++i) {
+            const int64_t cc = (int64_t)L * per + i;
+            const double v = (cc < nch) ? sh.csum[cc] : 0.0;
+            if (v > 0.0 && csel < 0) {
+                clast = cc;
+                clbase = run;
+                if (run + v >= r) {
+                    csel = cc;
+                    cbase = run;
+                }
             }
-            if (run >= r) {  // sampler.rs:211-213: r -= w; if r <= 0 return i
-                tok = j;
-                etok = e;
-                ktok = kp;
-                break;
+            run += v;
+        }
+    }
+    if (csel < 0) {  // rounding: the last chunk with mass
+        csel = clast;
+        cbase = clbase;
+    }
+    // the chunk's 512 elements: lane prefix, then the lane's own elements
+    float xs[8];
+    load8(csel, xs);
+    double e8[8];
+    uint32_t km;
+    chunk_kept(csel, xs, tie_split ? sh.tcnt[csel] : 0u, e8, &km);
+    double lsum = 0.0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lsum += e8[e];
+    const double cincl = wscan_f64(lsum);
+    const uint64_t hit = __ballot((cbase + cincl >= r) & (lsum > 0.0));
+    const uint64_t nz = __ballot(lsum > 0.0);
+    const int LL = hit ? (__ffsll((long long)hit) - 1) : (63 - __clzll((long long)nz));
+    if (l == LL) {
+        double run = cbase + cincl - lsum;
+        int64_t tok = -1, last = -1;
+        double etok = 0.0, elast = 0.0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t j = csel * kGChunk + 8 * l + e;
+            if ((km >> e) & 1u) {
+                run += e8[e];
+                if (tok < 0) {
+                    last = j;
+                    elast = e8[e];
+                    if (run >= r) {  // sampler.rs:211-213: r -= w; if r <= 0 return i
+                        tok = j;
+                        etok = e8[e];
+                    }
+                }
             }
         }
-        if (tok < 0) {  // rounding: the crossing is the range's last kept token
-            tok = last_kept;
-            ktok = true;
-            etok = exp(val(tok) / temp - M_w);
+        bool ktok = true;
+        if (tok < 0) {  // rounding: the crossing is this lane's last kept token
+            tok = last;
+            etok = elast;
         }
-        write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, M_w, z_kept, z_all, u,
+        if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
+            tok = 0;
+            ktok = false;
+        }
+        write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, M_w, zkM, zaM, u,
                          ktok ? etok / z_kept : 0.0, (uint64_t)kept_total, 2, reject);
+    }
+    return true;
+}
+#undef NIS_G_EACH
+
+// The general path: the SIMPLE form (f32 masses, no penalty lookups in the
+// passes) when it applies, else the general one.
+__device__ __forceinline__ void general_row(const RowArgs a, const int row, GeneralShared& sh,
+                                            const uint32_t reject) {
+    if (!general_row_t<true>(a, row, sh, reject)) {
+        __syncthreads();
+        general_row_t<false>(a, row, sh, reject);
     }
 }
 
