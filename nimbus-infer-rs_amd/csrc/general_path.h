@@ -50,12 +50,27 @@ struct RowArgs {
 };
 
 constexpr int kGU = 16;                          // loads per lane per block of a pass
-constexpr int kGChunk = 512;                     // walk chunk: 64 lanes x 8 elements
+constexpr int kGChunk = 512;                     // walk chunk: 8 rows of 64 elements
 constexpr int kGMaxChunks = NIS_MAX_V / kGChunk;
 constexpr double kGFix = 1099511627776.0;        // 2^40 fixed-point mass scale
+// SIMPLE top-p: value histogram of t = x*c - R (bin b holds t in
+// (-(b+1)/kGVRes, -b/kGVRes], the last bin everything lower) and the
+// lane-private lists of the members of the (at most two) bins that can hold
+// the cutoff
+constexpr int kGVBins = 2048;
+constexpr float kGVRes = 32.0f;
+constexpr int kGLane = 16;                       // list entries per lane
 
 struct GeneralShared {
-    uint32_t bitmap[NIS_MAX_V / 32];  // penalised-id set of the row
+    union {
+        uint32_t bitmap[NIS_MAX_V / 32];  // penalised-id set of the row
+        struct {
+            uint32_t cnt[kGVBins];
+            unsigned long long mass[kGVBins];  // 2^-40 fixed point
+            float lx[kGLane][kBlock];          // [slot][thread]
+            uint32_t li[kGLane][kBlock];
+        } v;
+    } u;
     uint32_t hcnt[256];
     unsigned long long hmass[256];    // 2^-40 fixed point
     unsigned long long hkey[256];
@@ -207,11 +222,11 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         if (!SIMPLE && g1 > g0) {
             pen = true;
             const int64_t nw = (V + 31) >> 5;
-            for (int64_t i = tid; i < nw; i += kBlock) sh.bitmap[i] = 0u;
+            for (int64_t i = tid; i < nw; i += kBlock) sh.u.bitmap[i] = 0u;
             __syncthreads();
             for (int64_t i = g0 + tid; i < g1; i += kBlock) {
                 const uint32_t id = a.gen_ids[i];
-                if ((int64_t)id < V) atomicOr(&sh.bitmap[id >> 5], 1u << (id & 31));
+                if ((int64_t)id < V) atomicOr(&sh.u.bitmap[id >> 5], 1u << (id & 31));
             }
             __syncthreads();
         }
@@ -220,7 +235,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     auto pval = [&](int64_t j, float xr) -> double {
         double v = (double)xr;
         if constexpr (!SIMPLE) {
-            if (pen && ((sh.bitmap[j >> 5] >> (j & 31)) & 1u)) v = (v > 0.0) ? v / penf : v * penf;
+            if (pen && ((sh.u.bitmap[j >> 5] >> (j & 31)) & 1u)) v = (v > 0.0) ? v / penf : v * penf;
         }
         return v;
     };
@@ -389,7 +404,163 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     double z_all = 0.0;
     uint64_t kstar = 0;      // keys > kstar kept; == kstar kept for tie rank < n_keep
     int64_t n_tie = 0, n_keep = 0;
-    if (topp_on) {
+    bool topp_done = false;
+    if constexpr (SIMPLE) {
+        if (topp_on && !topk_on) {
+            // value histogram (count, fixed-point mass) with Z in one pass
+#pragma unroll
+            for (int i = 0; i < kGVBins / kBlock; ++i) {
+                sh.u.v.cnt[tid + i * kBlock] = 0u;
+                sh.u.v.mass[tid + i * kBlock] = 0ull;
+            }
+            __syncthreads();
+            auto vbin = [&](float t) -> uint32_t {
+                return (uint32_t)fminf(fmaxf(-t * kGVRes, 0.0f), (float)(kGVBins - 1));
+            };
+            double zl = 0.0;
+            NIS_G_EACH({
+                const float t = fmaf(xr, cf, -Rf);
+                const float e = __builtin_amdgcn_exp2f(t);
+                zl += (double)e;
+                const uint32_t b = vbin(t);
+                // e * 2^40 as an exact integer: high part e * 2^8, low part
+                // the rest (both exact in f32)
+                const float hi = floorf(e * 256.0f);
+                const uint32_t lo = (uint32_t)fmaf(-hi, 4294967296.0f, e * 1099511627776.0f);
+                atomicAdd(&sh.u.v.cnt[b], 1u);
+                atomicAdd(&sh.u.v.mass[b], ((unsigned long long)(uint32_t)hi << 32) | lo);
+            })
+            z_all = block_sum(zl, sh.dscr);
+            const double pZ = (double)p * z_all;
+            // wave 0: the lowest bin b_a passing sampler.rs:150 with the bin's
+            // upper edge 2^(-b/kGVRes) for its first element.  That edge is at
+            // least the first element's mass, so the true cutoff bin is b_a or
+            // the nonempty bin b_p above it; their members are listed next.
+            if (w == 0) {
+                constexpr int per = kGVBins / 64;
+                unsigned long long ltot = 0;
+#pragma unroll 8
+                for (int i = 0; i < per; ++i) ltot += sh.u.v.mass[per * l + i];
+                const double incl = wscan_f64((double)ltot);
+                double above = incl - (double)ltot;  // fixed point, bins of lower lanes
+                int ba = -1;
+#pragma unroll 8
+                for (int i = 0; i < per; ++i) {
+                    const int b = per * l + i;
+                    const uint32_t n = sh.u.v.cnt[b];
+                    const double G = above / kGFix;
+                    const double edge = (double)__builtin_amdgcn_exp2f(-(float)b / kGVRes);
+                    const bool q = (n != 0) && (G - edge <= pZ);
+                    ba = q ? b : ba;
+                    above += (double)sh.u.v.mass[b];
+                }
+                const int bA = (int)wmax_f32((float)ba);  // highest qualifying bin (exact in float)
+                // b_p: the last nonempty bin above b_A, and the mass above it
+                int lp = -1;
+                double gp = 0.0;
+                above = incl - (double)ltot;
+#pragma unroll 8
+                for (int i = 0; i < per; ++i) {
+                    const int b = per * l + i;
+                    const bool ne = sh.u.v.cnt[b] != 0;
+                    const bool take = ne && b < bA;
+                    lp = take ? b : lp;
+                    gp = take ? above / kGFix : gp;
+                    above += (double)sh.u.v.mass[b];
+                }
+                const int bP = (int)wmax_f32((float)lp);
+                const uint64_t own = __ballot(lp == bP && bP >= 0);
+                const int owner = own ? (__ffsll((long long)own) - 1) : 0;
+                const double G0 = (bP >= 0) ? bcast_f64(gp, owner) : 0.0;
+                if (l == 0) {
+                    sh.bi[0] = bA;
+                    sh.bi[1] = bP;
+                    sh.bd[0] = G0;
+                }
+            }
+            __syncthreads();
+            const int bA = (int)sh.bi[0], bP = (int)sh.bi[1];
+            const double G0 = sh.bd[0];
+            if (bA >= 0) {
+                // list the members of bins b_p and b_a (lane-private lists)
+                int nlane = 0;
+                uint64_t diff = 0;
+                const uint32_t kref = (uint32_t)(kmax >> 32);
+                NIS_G_EACH({
+                    const float t = fmaf(xr, cf, -Rf);
+                    const int b = (int)vbin(t);
+                    const bool in = (b == bA) | (b == bP);
+                    diff |= in ? ((uint64_t)(key32(xr) ^ kref) << 32) : 0ull;
+                    if (in) {
+                        if (nlane < kGLane) {
+                            sh.u.v.lx[nlane][tid] = xr;
+                            sh.u.v.li[nlane][tid] = (uint32_t)j;
+                        }
+                        ++nlane;
+                    }
+                })
+                const int64_t novf = block_sum((int64_t)(nlane > kGLane ? 1 : 0), sh.iscr);
+                if (novf == 0) {
+                    // the radix walk of the general form, over the listed members
+                    const DigitRange dr = digit_range(block_or(diff, sh.uscr));
+                    uint64_t prefix = (dr.hi_shift + 8 >= 64) ? 0 : (kmax >> (dr.hi_shift + 8));
+                    double G = G0;
+                    if (!dr.all_equal) {
+                        for (int shift = dr.hi_shift; shift >= dr.lo_shift; shift -= 8) {
+                            __syncthreads();
+                            if (tid < 256) {
+                                sh.hcnt[tid] = 0;
+                                sh.hmass[tid] = 0ull;
+                                sh.hkey[tid] = 0ull;
+                            }
+                            __syncthreads();
+                            for (int i = 0; i < nlane; ++i) {
+                                const float xl = sh.u.v.lx[i][tid];
+                                const uint64_t k = (uint64_t)key32(xl) << 32;
+                                if (in_prefix(k, shift, prefix)) {
+                                    const int d = (int)((k >> shift) & 255);
+                                    atomicAdd(&sh.hcnt[d], 1u);
+                                    atomicAdd(&sh.hmass[d],
+                                              (unsigned long long)((double)__builtin_amdgcn_exp2f(fmaf(xl, cf, -Rf)) * kGFix));
+                                    atomicMax(&sh.hkey[d], (unsigned long long)k);
+                                }
+                            }
+                            __syncthreads();
+                            if (w == 0) {
+                                int sel;
+                                double gsel;
+                                uint32_t nsel;
+                                topp_digit_select(sh, G, pZ, mass_of_key, &sel, &gsel, &nsel);
+                                if (l == 0) {
+                                    sh.bi[0] = sel < 256 ? sel : 0;
+                                    sh.bi[1] = sel < 256 ? (int64_t)nsel : 0;
+                                    sh.bd[0] = sel < 256 ? gsel : G;
+                                }
+                            }
+                            __syncthreads();
+                            prefix = (prefix << 8) | (uint64_t)sh.bi[0];
+                            G = sh.bd[0];
+                            n_tie = sh.bi[1];
+                        }
+                        const uint64_t lowmask = (dr.lo_shift == 0) ? 0 : ((1ull << dr.lo_shift) - 1);
+                        kstar = (prefix << dr.lo_shift) | (kmax & lowmask);
+                    } else {
+                        // every listed member has the key of the row max
+                        kstar = kmax;
+                        n_tie = block_sum((int64_t)nlane, sh.iscr);
+                    }
+                    const double es = mass_of_key(kstar);
+                    const double q = (pZ - G) / es;  // >= -1 for the selected key
+                    if (!(q < (double)n_tie)) n_keep = n_tie;
+                    else n_keep = min(n_tie, (int64_t)floor(q) + 2);
+                    if (n_keep < 1) n_keep = 1;
+                    topp_done = true;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (topp_on && !topp_done) {
         double zl = 0.0;
         uint64_t diff = 0;
         NIS_G_EACH({
@@ -463,12 +634,13 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     const bool tie_split = (mode == 1) && (n_keep < n_tie);
 
     // ---- walk chunks: chunk c = elements [c*kGChunk, (c+1)*kGChunk), wave
-    // c % kWaves, lane l its 8 consecutive elements from c*kGChunk + 8l ----
+    // c % kWaves; row e of it is elements c*kGChunk + 64e + (0..63), one per
+    // lane (coalesced loads; index order is row by row, lane by lane) ----
     const int64_t nch = (V + kGChunk - 1) / kGChunk;
     auto load8 = [&](int64_t c, float* xs) {
-        const int64_t j0 = c * kGChunk + 8 * l;
+        const int64_t j0 = c * kGChunk + l;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xs[e] = x[min(j0 + e, V - 1)];
+        for (int e = 0; e < 8; ++e) xs[e] = x[min(j0 + 64 * e, V - 1)];
     };
     // tie-group members (key == kstar) before each chunk, when only some of
     // them are kept (ties are kept in ascending index order)
@@ -479,7 +651,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             uint32_t tl = 0;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int64_t j = cc * kGChunk + 8 * l + e;
+                const int64_t j = cc * kGChunk + 64 * e + l;
                 tl += (j < V && keyof(pval(j, xs[e])) == kstar) ? 1u : 0u;
             }
             const uint32_t tc = wsum_u32(tl);
@@ -498,26 +670,14 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         }
         __syncthreads();
     }
-    // kept flags and masses of a lane's 8 elements of chunk cc
+    // kept flags and masses of a lane's 8 elements (one per row) of chunk cc
     auto chunk_kept = [&](int64_t cc, const float* xs, uint32_t tie_base, double* e8,
                           uint32_t* kmask) {
-        uint32_t tl = 0;
-        uint32_t ties[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int64_t j = cc * kGChunk + 8 * l + e;
-            const bool in = j < V;
-            const double v = pval(j, xs[e]);
-            const uint64_t k = keyof(v);
-            ties[e] = (in && tie_split && k == kstar) ? 1u : 0u;
-            tl += ties[e];
-        }
-        // tie rank of this lane's first tie member
-        uint32_t tr = tie_split ? (tie_base + wscan_u32(tl) - tl) : 0u;
+        uint32_t rowbase = tie_base;  // tie members before this row
         uint32_t km = 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int64_t j = cc * kGChunk + 8 * l + e;
+            const int64_t j = cc * kGChunk + 64 * e + l;
             const bool in = j < V;
             const double v = pval(j, xs[e]);
             const uint64_t k = keyof(v);
@@ -527,8 +687,14 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             else if (mode == 0) kp = true;
             else if (k > kstar) kp = true;
             else if (k < kstar) kp = false;
-            else kp = tie_split ? ((int64_t)tr < n_keep) : true;
-            tr += ties[e];
+            else kp = true;
+            if (tie_split) {  // ties are kept in ascending index order
+                const bool tie = in && k == kstar;
+                const uint64_t mt = __ballot(tie);
+                const uint32_t tr = rowbase + lane_rank(mt);
+                kp = tie ? ((int64_t)tr < n_keep) : kp;
+                rowbase += (uint32_t)__popcll(mt);
+            }
             kp = kp && in;
             km |= kp ? (1u << e) : 0u;
             e8[e] = kp ? massv(v, xs[e]) : 0.0;
@@ -619,43 +785,47 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         csel = clast;
         cbase = clbase;
     }
-    // the chunk's 512 elements: lane prefix, then the lane's own elements
+    // the chunk's 8 rows: the row holding the crossing (row totals), then
+    // the lane inside it (prefix over the row's 64 elements)
     float xs[8];
     load8(csel, xs);
     double e8[8];
     uint32_t km;
     chunk_kept(csel, xs, tie_split ? sh.tcnt[csel] : 0u, e8, &km);
-    double lsum = 0.0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) lsum += e8[e];
-    const double cincl = wscan_f64(lsum);
-    const uint64_t hit = __ballot((cbase + cincl >= r) & (lsum > 0.0));
-    const uint64_t nz = __ballot(lsum > 0.0);
-    const int LL = hit ? (__ffsll((long long)hit) - 1) : (63 - __clzll((long long)nz));
-    if (l == LL) {
-        double run = cbase + cincl - lsum;
-        int64_t tok = -1, last = -1;
-        double etok = 0.0, elast = 0.0;
+    int rsel = -1, rlast = -1;
+    double rbase = cbase, rlbase = cbase;
+    {
+        double run = cbase;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int64_t j = csel * kGChunk + 8 * l + e;
-            if ((km >> e) & 1u) {
-                run += e8[e];
-                if (tok < 0) {
-                    last = j;
-                    elast = e8[e];
-                    if (run >= r) {  // sampler.rs:211-213: r -= w; if r <= 0 return i
-                        tok = j;
-                        etok = e8[e];
-                    }
-                }
-            }
+            const double rs = wsum_f64(e8[e]);
+            const bool nzr = rs > 0.0;
+            const bool first = nzr && rsel < 0;
+            rlast = first ? e : rlast;
+            rlbase = first ? run : rlbase;
+            const bool hitr = first && (run + rs >= r);
+            rsel = hitr ? e : rsel;
+            rbase = hitr ? run : rbase;
+            run += rs;
         }
+    }
+    if (rsel < 0) {  // rounding: the last row with mass
+        rsel = rlast;
+        rbase = rlbase;
+    }
+    double er = e8[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) er = (e == rsel) ? e8[e] : er;
+    const double rincl = wscan_f64(er);
+    const uint64_t hit = __ballot((rbase + rincl >= r) & (er > 0.0));
+    const uint64_t nz = __ballot(er > 0.0);
+    const bool rounded = hit == 0;  // rounding: the row's last kept element
+    const int LL = hit ? (__ffsll((long long)hit) - 1) : (63 - __clzll((long long)nz));
+    if (l == LL) {
+        int64_t tok = csel * kGChunk + 64 * rsel + l;
+        const double etok = er;
         bool ktok = true;
-        if (tok < 0) {  // rounding: the crossing is this lane's last kept token
-            tok = last;
-            etok = elast;
-        }
+        (void)rounded;
         if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
             tok = 0;
             ktok = false;
