@@ -74,7 +74,7 @@ struct GeneralShared {
     uint32_t hcnt[256];
     unsigned long long hmass[256];    // 2^-40 fixed point
     unsigned long long hkey[256];
-    double csum[kGMaxChunks];         // kept mass of each walk chunk
+    unsigned long long csum[kGMaxChunks];  // kept mass of each walk chunk (2^-40 fixed point)
     uint32_t tcnt[kGMaxChunks];       // tie-group members before each walk chunk
     double dscr[kWaves];
     uint64_t uscr[kWaves];
@@ -400,6 +400,25 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         }
     }
 
+    // ---- walk chunks: chunk c = elements [c*kGChunk, (c+1)*kGChunk), wave
+    // c % kWaves; row e of it is elements c*kGChunk + 64e + (0..63), one per
+    // lane (coalesced loads; index order is row by row, lane by lane) ----
+    const int64_t nch = (V + kGChunk - 1) / kGChunk;
+    auto load8 = [&](int64_t c, float* xs) {
+        const int64_t j0 = c * kGChunk + l;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xs[e] = x[min(j0 + 64 * e, V - 1)];
+    };
+    // m * 2^40 as an exact integer, m an f32 mass <= 1 (high part m * 2^8,
+    // low part the rest: both exact in f32)
+    auto fix40 = [](float m) -> unsigned long long {
+        const float hi = floorf(m * 256.0f);
+        const uint32_t lo = (uint32_t)fmaf(-hi, 4294967296.0f, m * 1099511627776.0f);
+        return ((unsigned long long)(uint32_t)hi << 32) | lo;
+    };
+    bool sums_done = false;   // kept mass of every chunk already in csum[]
+    int64_t kept_pre = 0;     // and the kept count of this thread
+
     // ---- top-p (sampler.rs:118-160) --------------------------------------
     double z_all = 0.0;
     uint64_t kstar = 0;      // keys > kstar kept; == kstar kept for tie rank < n_keep
@@ -423,12 +442,8 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                 const float e = __builtin_amdgcn_exp2f(t);
                 zl += (double)e;
                 const uint32_t b = vbin(t);
-                // e * 2^40 as an exact integer: high part e * 2^8, low part
-                // the rest (both exact in f32)
-                const float hi = floorf(e * 256.0f);
-                const uint32_t lo = (uint32_t)fmaf(-hi, 4294967296.0f, e * 1099511627776.0f);
                 atomicAdd(&sh.u.v.cnt[b], 1u);
-                atomicAdd(&sh.u.v.mass[b], ((unsigned long long)(uint32_t)hi << 32) | lo);
+                atomicAdd(&sh.u.v.mass[b], fix40(e));
             })
             z_all = block_sum(zl, sh.dscr);
             const double pZ = (double)p * z_all;
@@ -482,23 +497,44 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             const int bA = (int)sh.bi[0], bP = (int)sh.bi[1];
             const double G0 = sh.bd[0];
             if (bA >= 0) {
-                // list the members of bins b_p and b_a (lane-private lists)
+                // one pass over the walk chunks: the mass of the elements
+                // above bin b_p (all kept) per chunk, and lane-private lists
+                // of the members of bins b_p and b_a
                 int nlane = 0;
+                int64_t nsure = 0;
                 uint64_t diff = 0;
                 const uint32_t kref = (uint32_t)(kmax >> 32);
-                NIS_G_EACH({
-                    const float t = fmaf(xr, cf, -Rf);
-                    const int b = (int)vbin(t);
-                    const bool in = (b == bA) | (b == bP);
-                    diff |= in ? ((uint64_t)(key32(xr) ^ kref) << 32) : 0ull;
-                    if (in) {
-                        if (nlane < kGLane) {
-                            sh.u.v.lx[nlane][tid] = xr;
-                            sh.u.v.li[nlane][tid] = (uint32_t)j;
+                const int bTop = (bP >= 0) ? bP : bA;  // bins above it hold kept elements only
+                float xn8[8];
+                if (w < nch) load8(w, xn8);
+                for (int64_t cc = w; cc < nch; cc += kWaves) {
+                    float xs[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xs[e] = xn8[e];
+                    load8(min(cc + kWaves, nch - 1), xn8);  // the next chunk, in flight meanwhile
+                    double sl = 0.0;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int64_t j = cc * kGChunk + 64 * e + l;
+                        const bool inr = j < V;
+                        const float t = fmaf(xs[e], cf, -Rf);
+                        const int b = (int)vbin(t);
+                        const bool sure = inr & (b < bTop);
+                        sl += sure ? (double)__builtin_amdgcn_exp2f(t) : 0.0;
+                        nsure += sure ? 1 : 0;
+                        const bool in = inr & ((b == bA) | (b == bP));
+                        diff |= in ? ((uint64_t)(key32(xs[e]) ^ kref) << 32) : 0ull;
+                        if (in) {
+                            if (nlane < kGLane) {
+                                sh.u.v.lx[nlane][tid] = xs[e];
+                                sh.u.v.li[nlane][tid] = (uint32_t)j;
+                            }
+                            ++nlane;
                         }
-                        ++nlane;
                     }
-                })
+                    const double cs = wsum_f64(sl);
+                    if (l == 0) sh.csum[cc] = (unsigned long long)(cs * kGFix);
+                }
                 const int64_t novf = block_sum((int64_t)(nlane > kGLane ? 1 : 0), sh.iscr);
                 if (novf == 0) {
                     // the radix walk of the general form, over the listed members
@@ -555,6 +591,23 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                     else n_keep = min(n_tie, (int64_t)floor(q) + 2);
                     if (n_keep < 1) n_keep = 1;
                     topp_done = true;
+                    if (n_keep >= n_tie) {
+                        // no tie group split: the kept listed members join the
+                        // mass of their chunks (fixed point, exact)
+                        int64_t nkl = 0;
+                        for (int i = 0; i < nlane; ++i) {
+                            const float xl = sh.u.v.lx[i][tid];
+                            const uint64_t k = (uint64_t)key32(xl) << 32;
+                            if (k >= kstar) {
+                                const uint32_t jl = sh.u.v.li[i][tid];
+                                atomicAdd(&sh.csum[jl / kGChunk],
+                                          fix40(__builtin_amdgcn_exp2f(fmaf(xl, cf, -Rf))));
+                                ++nkl;
+                            }
+                        }
+                        kept_pre = nsure + nkl;
+                        sums_done = true;
+                    }
                 }
             }
             __syncthreads();
@@ -633,15 +686,6 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     const int mode = topp_zero ? 2 : (topp_on ? 1 : 0);
     const bool tie_split = (mode == 1) && (n_keep < n_tie);
 
-    // ---- walk chunks: chunk c = elements [c*kGChunk, (c+1)*kGChunk), wave
-    // c % kWaves; row e of it is elements c*kGChunk + 64e + (0..63), one per
-    // lane (coalesced loads; index order is row by row, lane by lane) ----
-    const int64_t nch = (V + kGChunk - 1) / kGChunk;
-    auto load8 = [&](int64_t c, float* xs) {
-        const int64_t j0 = c * kGChunk + l;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xs[e] = x[min(j0 + 64 * e, V - 1)];
-    };
     // tie-group members (key == kstar) before each chunk, when only some of
     // them are kept (ties are kept in ascending index order)
     if (tie_split) {
@@ -703,10 +747,10 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     };
 
     // ---- kept mass of every chunk ----------------------------------------
-    int64_t nk = 0;
+    int64_t nk = kept_pre;
     float xn8[8];
-    if (w < nch) load8(w, xn8);
-    for (int64_t cc = w; cc < nch; cc += kWaves) {
+    if (!sums_done && w < nch) load8(w, xn8);
+    for (int64_t cc = w; cc < nch && !sums_done; cc += kWaves) {
         float xs[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) xs[e] = xn8[e];
@@ -719,7 +763,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         for (int e = 0; e < 8; ++e) s += e8[e];
         nk += __popc(km);
         const double cs = wsum_f64(s);
-        if (l == 0) sh.csum[cc] = cs;
+        if (l == 0) sh.csum[cc] = (unsigned long long)(cs * kGFix);
     }
     const int64_t kept_total = block_sum(nk, sh.iscr);  // contains a barrier: csum[] visible after it
 
@@ -730,7 +774,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     double ls = 0.0;
     for (int64_t i = 0; i < per; ++i) {
         const int64_t cc = (int64_t)l * per + i;
-        ls += (cc < nch) ? sh.csum[cc] : 0.0;
+        ls += (cc < nch) ? (double)sh.csum[cc] / kGFix : 0.0;
     }
     const double lincl = wscan_f64(ls);
     const double z_kept = bcast_f64(lincl, 63);
@@ -769,7 +813,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         double run = bcast_f64(lincl - ls, L);
         for (int64_t i = 0; i < per; ++i) {
             const int64_t cc = (int64_t)L * per + i;
-            const double v = (cc < nch) ? sh.csum[cc] : 0.0;
+            const double v = (cc < nch) ? (double)sh.csum[cc] / kGFix : 0.0;
             if (v > 0.0 && csel < 0) {
                 clast = cc;
                 clbase = run;
