@@ -272,6 +272,14 @@ __device__ __forceinline__ void lds_put_u32x2(uint64_t mask, uint32_t a, uint32_
         : "memory");
 }
 
+// m * 2^40 as an exact integer, m an f32 mass in [0, 1] (high part m * 2^8,
+// low part the rest: both exact in f32).
+__device__ __forceinline__ unsigned long long fix40(float m) {
+    const float hi = floorf(m * 256.0f);
+    const uint32_t lo = (uint32_t)fmaf(-hi, 4294967296.0f, m * 1099511627776.0f);
+    return ((unsigned long long)(uint32_t)hi << 32) | lo;
+}
+
 // Fine-histogram bucket of an element in [x_lo, x_top] (monotone in x).
 __device__ __forceinline__ int fine_bucket(float x, float x_lo, float inv_w) {
     return min(max((int)((x - x_lo) * inv_w), 0), kFineBins - 1);
@@ -541,6 +549,23 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         lds_put_rec(lds_addr(&sh.tc[w]), (double)thw, nw, nc);
     }
     NIS_TS(2);
+    // sampler.rs:209: the row's single RNG advance, drawn here by wave 0
+    // (which waits for the slower waves anyway) into LDS; written back to
+    // memory only when the row completes on this path.
+    if (w == 0) {
+        const uint64_t rsv =
+            ((const __attribute__((address_space(1))) uint64_t*)(a.rng + 4 * (int64_t)row))[l & 3];
+        uint64_t st[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
+        const double u0 = rng_next_f64(st);
+        NIS_PUT(l == 0, sh.bd[1], u0);
+        NIS_PUT(l == 1, sh.rng[0], st[0]);
+        NIS_PUT(l == 2, sh.rng[1], st[1]);
+        NIS_PUT(l == 3, sh.rng[2], st[2]);
+        NIS_PUT(l == 4, sh.rng[3], st[3]);
+    }
 
     // ---- T1: row max, reference R, Z ---------------------------------------
     mx = wmax_f32(mx);
@@ -573,24 +598,6 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const double rho = (double)__builtin_amdgcn_exp2f(-tM);
     const double pZ = (double)p * ZR * rho;
     const double pZR = (double)p * ZR;
-    // The row's RNG state: one word per lane 0..3 of wave 0 (a vector load,
-    // so no LDS wait depends on it), consumed just before the walk.
-    const uint64_t rsv =
-        ((const __attribute__((address_space(1))) uint64_t*)(a.rng + 4 * (int64_t)row))[l & 3];
-    // sampler.rs:209: the row's single RNG advance, into LDS (written back to
-    // memory only when the row completes here)
-#define NIS_RNG_DRAW()                                                                          \
-    if (w == 0) {                                                                               \
-        uint64_t st[4];                                                                         \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j)                                           \
-            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j); \
-        const double u0 = rng_next_f64(st);                                                     \
-        NIS_PUT(l == 0, sh.bd[1], u0);                                                          \
-        NIS_PUT(l == 1, sh.rng[0], st[0]);                                                      \
-        NIS_PUT(l == 2, sh.rng[1], st[1]);                                                      \
-        NIS_PUT(l == 3, sh.rng[2], st[2]);                                                      \
-        NIS_PUT(l == 4, sh.rng[3], st[3]);                                                      \
-    }
 
     uint32_t reject = NIS_REJECT_NONE;  // reason of a failed sparse attempt
     if (topp) {
@@ -629,7 +636,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         sh.s.cb[w][(j)] = (uint16_t)b;                                            \
         g += (double)e;                                                           \
         atomicAdd(&sh.fcnt[b], 1u);                                               \
-        atomicAdd(&sh.fmass[b], (unsigned long long)((double)e * kFix));          \
+        atomicAdd(&sh.fmass[b], fix40(e));                                        \
         atomicMax(&sh.fkmax[b], key32(xs));                                       \
     }
                 NIS_CAND(ja, xa)
@@ -803,12 +810,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                         const double Tincl = wscan_f64(T);
                         const double zk = bcast_f64(Tincl, 63);
                         const uint32_t kept_total = wsum_u32(TN);
-                        uint64_t st[4];
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) |
-                                    bcast_u32((uint32_t)rsv, j);
-                        const double u = rng_next_f64(st);  // sampler.rs:209
+                        const double u = sh.bd[1];  // the draw (sampler.rs:209), made before T1
                         const double r = u * zk;
                         // the first wave whose running total reaches r (and has
                         // mass); rounding: the last wave with mass
@@ -822,50 +824,73 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                         const int ncs = (int)min(nsel, (uint32_t)kWaveCand);
                         NIS_TS(8);
                         // ---- S7: inverse-CDF walk over the chosen wave's list ------
-                        int tok = -1, last = -1;
-                        float xt = 0.0f, xlast = 0.0f;
-                        #pragma unroll 1
-                        for (int j0 = 0; j0 < ncs; j0 += 64) {
-                            const int j = j0 + l;  // < ncs + 64 <= kWaveCand + 64: inside the list
-                            const float x = sh.s.cx[wsel][j];
-                            const uint32_t id = sh.s.ci[wsel][j];
-                            const float e = sh.s.ce[wsel][j];
-                            const uint32_t k = key32(x);
-                            const bool kj = (j < ncs) & ((k > kc) | ((k == kc) & (id <= ic)));
-                            const double emj = kj ? (double)e : 0.0;
-                            const double inc = wscan_f64(emj);
-                            const uint64_t hit = __ballot(kj & (run + inc >= r));
-                            if (hit) {
-                                const int L = __ffsll((long long)hit) - 1;
-                                tok = (int)bcast_u32(id, L);
-                                xt = bcast_f32(x, L);
-                                break;
+                        // lane l sums the kept masses of list entries
+                        // [l*sg, l*sg + sg); the lane whose running total reaches
+                        // r then walks its own entries
+                        constexpr int kSeg = (kWaveCand + 63) / 64;
+                        const int sg = (ncs + 63) >> 6;
+                        float xe[kSeg], ee[kSeg];
+                        uint32_t ie[kSeg];
+                        uint32_t kmask = 0;
+                        double lsum = 0.0;
+#pragma unroll
+                        for (int i = 0; i < kSeg; ++i) {
+                            const int j = l * sg + i;
+                            const int jc = min(j, kWaveCand - 1);
+                            xe[i] = sh.s.cx[wsel][jc];
+                            ie[i] = sh.s.ci[wsel][jc];
+                            ee[i] = sh.s.ce[wsel][jc];
+                        }
+#pragma unroll
+                        for (int i = 0; i < kSeg; ++i) {
+                            const int j = l * sg + i;
+                            const uint32_t k = key32(xe[i]);
+                            const bool kj = (i < sg) & (j < ncs) & ((k > kc) | ((k == kc) & (ie[i] <= ic)));
+                            kmask |= kj ? (1u << i) : 0u;
+                            lsum += kj ? (double)ee[i] : 0.0;
+                        }
+                        const double sincl = wscan_f64(lsum);
+                        const uint64_t hitl = __ballot((run + sincl >= r) & (lsum > 0.0));
+                        const uint64_t nzl = __ballot(lsum > 0.0);
+                        const int Ls = hitl ? (__ffsll((long long)hitl) - 1) : (63 - __clzll((long long)nzl));
+                        if (l == Ls) {
+                            double run2 = run + sincl - lsum;
+                            int tok = -1, last = -1;
+                            float xt = 0.0f, xlast = 0.0f;
+#pragma unroll
+                            for (int i = 0; i < kSeg; ++i) {
+                                if ((kmask >> i) & 1u) {
+                                    run2 += (double)ee[i];
+                                    if (tok < 0) {
+                                        last = (int)ie[i];
+                                        xlast = xe[i];
+                                        if (run2 >= r) {
+                                            tok = (int)ie[i];
+                                            xt = xe[i];
+                                        }
+                                    }
+                                }
                             }
-                            const uint64_t kmk = __ballot(kj);
-                            const int Lk = kmk ? (63 - __clzll((long long)kmk)) : 0;
-                            last = kmk ? (int)bcast_u32(id, Lk) : last;
-                            xlast = kmk ? bcast_f32(x, Lk) : xlast;
-                            run += bcast_f64(inc, 63);
-                        }
-                        bool tkept = true;
-                        if (tok < 0) {  // rounding: the last kept token of that wave
-                            tok = last;
-                            xt = xlast;
-                        }
-                        if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
-                            tok = 0;
-                            tkept = false;
-                        }
-                        if (l == 0) {
+                            bool tkept = true;
+                            if (tok < 0) {  // rounding: the last kept token of that wave
+                                tok = last;
+                                xt = xlast;
+                            }
+                            if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
+                                tok = 0;
+                                tkept = false;
+                            }
                             const double zkM = zk * rho;
                             const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
                             write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
                                              zkM, ZR * rho, u, prob, (uint64_t)kept_total, 1);
+                        }
+                        if (l == 0) {
                             uint64_t* sp = a.rng + 4 * (int64_t)row;
-                            sp[0] = st[0];
-                            sp[1] = st[1];
-                            sp[2] = st[2];
-                            sp[3] = st[3];
+                            sp[0] = sh.rng[0];
+                            sp[1] = sh.rng[1];
+                            sp[2] = sh.rng[2];
+                            sp[3] = sh.rng[3];
                         }
                         NIS_TS(9);
                         return NIS_REJECT_NONE;
@@ -1203,7 +1228,6 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             sh.ia[w] = wk;
         }
     }
-    NIS_RNG_DRAW()
     lds_barrier();
     // per-wave totals (lanes 0..7), their prefix and the wave holding the
     // crossing: the first whose running total reaches r (and has mass);
@@ -1312,7 +1336,6 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     return NIS_REJECT_NONE;
 #undef NIS_FIX
 #undef NIS_INDEX
-#undef NIS_RNG_DRAW
 }
 
 }  // namespace nis
