@@ -2,8 +2,9 @@
 // workgroup (V <= 53245), the hot path of nis_sample_batch.
 //
 // HBM is touched once: every lane issues its 26 nontemporal 16-byte loads up
-// front (wave-contiguous layout: wave w owns float4 slots
-// [w*26*64, (w+1)*26*64), chunk k / lane l holds slot w*1664 + 64k + l), and
+// front (wave-contiguous layout: the row's float4 slots are split evenly
+// over the waves in whole 64-slot chunks, S per wave; chunk k / lane l of
+// wave w holds slot w*S + 64k + l), and
 // the row then lives in VGPRs (104 logits per lane; 8 waves per workgroup
 // leave each wave up to 256 VGPRs).  While the loads stream in, each wave
 // adds the masses e = 2^(x*c - R_w) of its elements to Z (c = log2(e)/T,
@@ -46,9 +47,15 @@ typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 // global-address-space views, so loads are global_load with an SGPR base
 typedef const __attribute__((address_space(1))) f4v* gf4p;
 typedef const __attribute__((address_space(1))) float* gfp;
+typedef int32_t i4v __attribute__((ext_vector_type(4)));
+
+// Raw buffer load of 16 bytes (LLVM's llvm.amdgcn.raw.buffer.load): an
+// offset at or past the descriptor's byte count reads zeros and makes no
+// memory request.  aux = 2 marks it nontemporal.
+__device__ f4v nis_buffer_load_f4(i4v rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
 
 constexpr int kNch = 26;                      // float4 chunks per lane
-constexpr int kWaveSlots = kNch * 64;         // float4 slots per wave
 constexpr int kFastMaxV = kBlock * 4 * kNch - 3;
 constexpr int kSampleBins = 512;              // 32 octaves at 1/16 octave
 constexpr float kSampleRes = 16.0f;
@@ -71,6 +78,10 @@ constexpr float kTopRes = 8.0f;
 constexpr float kTopHead = 8.0f;
 constexpr int kWaveEnt = 384;                 // listed float4s per wave
 constexpr int kWaveCand = 448;                // candidates per wave
+// mass histogram of the candidates: kHRes buckets per octave of x*c on an
+// absolute grid (bucket floor(64 x c), so every wave agrees on it without
+// knowing the row max), kept in a ring of kHB buckets
+constexpr int kHB = 2048;
 
 struct DenseShared {
     float cell[kWaves][kNch][64];    // kept mass of each lane's 4 elements per chunk
@@ -89,17 +100,18 @@ struct SparseShared {
             f4v ent_x[kWaves][kWaveEnt];         // listed float4s, wave-compacted in index order
             uint16_t ent_pos[kWaves][kWaveEnt];  //   their chunk * 64 + lane
         } l;
-        struct {  // members of the cutoff bucket, per wave (the listing is dead by then)
+        struct {  // members of the cutoff buckets, per wave (the listing is dead by then)
             float gx[kWaves][kMaxFinal];
             uint32_t gi[kWaves][kMaxFinal];
             float ge[kWaves][kMaxFinal];
         } g;
     } u;
-    uint16_t cb[kWaves][kWaveCand + 64];      // candidates' fine bucket
-    float cx[kWaves][kWaveCand + 64];         // candidates (x >= x_lo) in index order: logit
+    float cx[kWaves][kWaveCand + 64];         // candidates (x >= th_w) in index order: logit
     uint32_t ci[kWaves][kWaveCand + 64];      //   row index
-    float ce[kWaves][kWaveCand + 64];         //   mass 2^(x*c - R)
-    double gab[kFineBins];               // candidate mass above each fine bucket
+    // [bucket & (kHB-1)]: count << 48 | sum of the members' 2^frac(x c) * 2^24;
+    // [kHB + lane]: dummy buckets
+    unsigned long long hist[kHB + 64];
+    unsigned long long chist[32 + 64];        // the same per octave (ring of 32; dummies)
 };
 
 // One 16-byte record per wave, written by the wave's lane 0 and read whole
@@ -145,6 +157,8 @@ struct FastShared {
     float bf[8];
     double bd[8];
     int32_t bi[8];
+    int32_t bi2[kWaves];
+    alignas(16) uint32_t ncnt[kWaves];  // candidates per list
 };
 
 // Optional per-phase timestamps of each workgroup's wave 0 (profiling
@@ -159,6 +173,10 @@ __device__ unsigned long long nis_phase_ts[8192 * 16];
 #define NIS_TS(i) \
     do {          \
     } while (0)
+#endif
+
+#ifndef NIS_SETPRIO
+#define NIS_SETPRIO() __builtin_amdgcn_s_setprio(2)
 #endif
 
 // Workgroup barrier that orders LDS only, so global loads still in flight
@@ -233,6 +251,47 @@ __device__ __forceinline__ void lds_put_u32x3(uint64_t mask, uint32_t a, uint32_
         : "s"(mask), "v"(a), "v"(va), "v"(b), "v"(vb), "v"(c), "v"(vc)
         : "memory");
 }
+__device__ __forceinline__ void lds_put_u32x4(uint64_t mask, uint32_t a, uint32_t va, uint32_t b,
+                                              uint32_t vb, uint32_t c, uint32_t vc, uint32_t d,
+                                              uint32_t vd) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_write_b32 %2, %3\n\t"
+        "ds_write_b32 %4, %5\n\t"
+        "ds_write_b32 %6, %7\n\t"
+        "ds_write_b32 %8, %9\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(va), "v"(b), "v"(vb), "v"(c), "v"(vc), "v"(d), "v"(vd)
+        : "memory");
+}
+// Two 64-bit LDS atomic adds of v by the lanes of `mask` only.
+__device__ __forceinline__ void lds_add_u64x2(uint64_t mask, uint32_t a, uint32_t b, uint64_t v) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_add_u64 %2, %4\n\t"
+        "ds_add_u64 %3, %4\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(b), "v"(v)
+        : "memory");
+}
+// one u32 by the wave's lane 0
+__device__ __forceinline__ void lds_put_lane0(uint32_t a, uint32_t v) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, 1\n\t"
+        "ds_write_b32 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "v"(a), "v"(v)
+        : "memory");
+}
 // a WaveRec by the wave's lane 0
 __device__ __forceinline__ void lds_put_rec(uint32_t a, double d, uint32_t x, uint32_t y) {
     const uint64_t db = (uint64_t)__double_as_longlong(d);
@@ -280,6 +339,18 @@ __device__ __forceinline__ unsigned long long fix40(float m) {
     return ((unsigned long long)(uint32_t)hi << 32) | lo;
 }
 
+// Candidate-histogram bucket of a logit: floor(64 x c), monotone in x.
+__device__ __forceinline__ int hbucket(float x, float c) {
+    return (int)floorf((x * c) * 64.0f);
+}
+// Mass of a candidate relative to the integer reference R, in the form the
+// candidate histogram sums exactly: 2^frac(x c) scaled by 2^(floor(x c) - R).
+__device__ __forceinline__ float canon_mass(float x, float c, int R) {
+    const float t = x * c;
+    const float fl = floorf(t);
+    return ldexpf(__builtin_amdgcn_exp2f(t - fl), (int)fl - R);
+}
+
 // Fine-histogram bucket of an element in [x_lo, x_top] (monotone in x).
 __device__ __forceinline__ int fine_bucket(float x, float x_lo, float inv_w) {
     return min(max((int)((x - x_lo) * inv_w), 0), kFineBins - 1);
@@ -302,6 +373,72 @@ __device__ __forceinline__ f4v fix_slot(f4v v, int f, int f_lo, int f_hi, int mi
         o[q] = y;
     }
     return f4v{o[0], o[1], o[2], o[3]};
+}
+
+// Adds the candidates of the lanes in `ok` to the candidate histograms:
+// count << 48 | 2^frac(x c) * 2^24 (LDS atomics by those lanes only).
+__device__ __forceinline__ void hist_add(FastShared& sh, float x, float c, bool ok) {
+    const float t = x * c;
+    const float fl = floorf(t);
+    const uint32_t fx = (uint32_t)(__builtin_amdgcn_exp2f(t - fl) * 16777216.0f);
+    const uint32_t b = (uint32_t)((int)floorf(t * 64.0f) & (kHB - 1));
+    const uint32_t bo = (uint32_t)((int)fl & 31);
+    const uint64_t v = (1ull << 48) | (uint64_t)fx;
+    lds_add_u64x2(__ballot(ok), lds_addr(&sh.s.hist[0]) + 8 * b, lds_addr(&sh.s.chist[0]) + 8 * bo, v);
+}
+
+// Takes wave o's listed float4s [0, ne): every element >= th joins o's
+// candidate list (index order; past the capacity the count still grows and
+// the row is rejected later).  Lane l takes entries 128 i + 2 l and
+// 128 i + 2 l + 1 of step i, and one scan of the per-lane hit counts places
+// all hits of the step at once.  Returns the candidate count.  Called by
+// the whole wave.
+__device__ __forceinline__ uint32_t take_entries(FastShared& sh, int o, uint32_t ne, float th,
+                                                 int S, int mis) {
+    const int l = lane_id();
+    const uint32_t cx0 = lds_addr(&sh.s.cx[o][0]);
+    const uint32_t ci0 = lds_addr(&sh.s.ci[o][0]);
+    uint32_t nc = 0;
+    #pragma unroll 1
+    for (uint32_t e0 = 0; e0 < ne; e0 += 128u) {
+        const uint32_t e = e0 + 2u * (uint32_t)l;
+        const uint32_t ec = min(e, (uint32_t)kWaveEnt - 2u);
+        const f4v v0 = sh.s.u.l.ent_x[o][ec];
+        const f4v v1 = sh.s.u.l.ent_x[o][ec + 1];
+        const uint32_t pp = *reinterpret_cast<const uint32_t*>(&sh.s.u.l.ent_pos[o][ec]);
+        uint32_t okm = 0;  // bits 0-3: entry e, bits 4-7: entry e + 1
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            okm |= ((e < ne) & (elem(v0, q) >= th)) ? (1u << q) : 0u;
+            okm |= ((e + 1 < ne) & (elem(v1, q) >= th)) ? (16u << q) : 0u;
+        }
+        const uint32_t cnt = (uint32_t)__popc(okm);
+        const uint32_t incl = wscan_u32(cnt);
+        const uint32_t base = nc + incl - cnt;
+        const int i0 = 4 * (o * S + (int)(pp & 0xFFFFu)) - mis;  // row index of entry e's element 0
+        const int i1 = 4 * (o * S + (int)(pp >> 16)) - mis;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const bool ok = (okm >> q) & 1u;
+            const uint32_t slot = min(base + (uint32_t)__popc(okm & ((1u << q) - 1u)), (uint32_t)kWaveCand - 1);
+            const float x = q < 4 ? elem(v0, q) : elem(v1, q - 4);
+            lds_put_u32x2(__ballot(ok), cx0 + 4 * slot, __float_as_uint(x), ci0 + 4 * slot,
+                          (uint32_t)((q < 4 ? i0 : i1) + (q & 3)));
+        }
+        nc += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    }
+    return nc;
+}
+
+// Adds wave o's candidates [0, n) to the candidate histograms.
+__device__ __forceinline__ void hist_list(FastShared& sh, int o, uint32_t n, float c) {
+    const int l = lane_id();
+    const int nn = (int)min(n, (uint32_t)kWaveCand);
+    #pragma unroll 1
+    for (int j0 = 0; j0 < nn; j0 += 64) {
+        const int j = j0 + l;
+        hist_add(sh, sh.s.cx[o][min(j, kWaveCand - 1)], c, j < nn);
+    }
 }
 
 __device__ __forceinline__ bool fast_eligible(const RowArgs a, int row) {
@@ -327,7 +464,16 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const gf4p base = (gf4p)(rowp - mis);
     const int f_lo = mis ? 1 : 0;          // first float4 slot lying fully inside the row
     const int f_hi = (V + mis - 4) >> 2;   // last one
-    const int slot0 = w * kWaveSlots + l;
+    // The slots touching the row are split evenly over the waves in whole
+    // chunks: wave w owns slots [w*S, w*S + S).  Kw of its chunks reach into
+    // the row; the stream processes Kp of them (at least the sample chunks).
+    // The loads of chunks past Kw read nothing (out-of-range buffer offsets)
+    // and those chunks hold -inf.
+    const int nsl = (V + mis + 3) >> 2;
+    const int S = 64 * ((nsl + 64 * kWaves - 1) / (64 * kWaves));
+    const int Kw = min(max((nsl - w * S + 63) >> 6, 0), S >> 6);
+    const int Kp = max(Kw, kTopS);
+    const int slot0 = w * S + l;
     const bool sampling = a.temperature > 0.0f;
 
     NIS_TS(0);
@@ -336,13 +482,28 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const float h0 = rowp[0], h1 = rowp[1], h2 = rowp[2];
     const float t0 = rowp[V - 3], t1 = rowp[V - 2], t2 = rowp[V - 1];
     __builtin_amdgcn_sched_barrier(0);
+    // buffer descriptor over the row's whole float4 slots [0, f_hi]: slots
+    // past the row read zeros (fixed below); the partial head slot is
+    // redirected to f_lo so nothing before the row is touched
+    const uint64_t bptr = (uint64_t)(uintptr_t)base;
+    const i4v rsrc = {(int32_t)(uint32_t)bptr, (int32_t)(uint32_t)((bptr >> 32) & 0xFFFFu),
+                      16 * (f_hi + 1), 0x00020000};
     f4v xv[kNch];
 #pragma unroll
     for (int k = 0; k < kNch; ++k) {
         const int f = slot0 + k * 64;
-        xv[k] = __builtin_nontemporal_load(base + min(max(f, f_lo), f_hi));
+        const int off = (k < Kw) ? 16 * max(f, f_lo) : 0x7FFFFFF0;
+        xv[k] = nis_buffer_load_f4(rsrc, off, 0, 2);
         __builtin_amdgcn_sched_barrier(0);  // keep chunk order = issue order
     }
+    // the row's RNG state (sampler.rs:209 draws from it once), loaded behind
+    // the logits so that the draw does not wait for it later.  Greedy calls
+    // may pass no states (the C ABI allows that only for temperature <= 0):
+    // the load then reads the row's first whole float4 slots instead, and
+    // the value is never used.
+    typedef const __attribute__((address_space(1))) uint64_t* gu64p;
+    const gu64p rng_src = a.rng ? (gu64p)(a.rng + 4 * (int64_t)row) : (gu64p)(rowp - mis + 4 * f_lo);
+    const uint64_t rsv = rng_src[l & 3];
 
     // LDS store by the lanes where `cond` holds; the other lanes write their
     // own spare slot, so no exec-mask branch is needed
@@ -364,10 +525,10 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     }
     NIS_PUT(tid == 0, sh.ncand, 0u);
     NIS_PUT(tid == 0, sh.overflow, 0u);
-    // this wave's histogram of float4 maxima (in its own candidate-mass row,
-    // which is written only after the stream)
+    // this wave's histogram of float4 maxima (in its own candidate row, which
+    // is written only after the histogram is read)
     static_assert(kTopBins == 4 * 64 && kTopBins <= kWaveCand + 64, "4 bins per lane, inside a row");
-    *reinterpret_cast<u4v*>(reinterpret_cast<uint32_t*>(&sh.s.ce[w][0]) + 4 * l) = u4v{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u4v*>(reinterpret_cast<uint32_t*>(&sh.s.cx[w][0]) + 4 * l) = u4v{0u, 0u, 0u, 0u};
 
     // slots not fully inside the row get their exact values or -inf; only
     // the one or two waves holding such slots take the (wave-uniform) branch.
@@ -377,14 +538,14 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     asm volatile("" : "+v"(slot0x));
 #define NIS_FIX(k)                                                                          \
     do {                                                                                    \
-        const int fb0 = w * kWaveSlots + (k) * 64;                                          \
+        const int fb0 = w * S + (k) * 64;                                                   \
         if (fb0 < f_lo || fb0 + 63 > f_hi)                                                  \
             xv[k] = fix_slot(xv[k], slot0x + (k) * 64, f_lo, f_hi, mis, V, h0, h1, h2, t0, t1, t2); \
     } while (0)
 #define NIS_INDEX(k, q) (4 * (slot0x + 64 * (k)) + (q) - mis)
     // does this wave hold any slot not fully inside the row?  Only such
     // waves run the per-chunk checks (each one is a branch).
-    const bool edge_wave = (w * kWaveSlots < f_lo) || (w * kWaveSlots + kWaveSlots - 1 > f_hi);
+    const bool edge_wave = (w * S < f_lo) || (w * S + 64 * Kw - 1 > f_hi);
 
     // ------------------------------------------------------------------
     // greedy (sampler.rs:172-181): first index of the maximum; NaN is
@@ -393,7 +554,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         float best = -INFINITY;
         int bidx = INT_MAX;
 #define NIS_GREEDY(FIX)                                      \
-    _Pragma("unroll") for (int k = 0; k < kNch; ++k) {      \
+    _Pragma("unroll") for (int k = 0; k < kNch; ++k) if (k < Kw) { \
         if (FIX) NIS_FIX(k);                                 \
         _Pragma("unroll") for (int q = 0; q < 4; ++q) {     \
             const float x = elem(xv[k], q);                  \
@@ -438,8 +599,22 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     const float p = a.top_p;
     const bool topp = p < 1.0f;  // p <= 0 is excluded by fast_eligible
 
-    // wave-local reference from the wave's first chunk (no barrier)
-    if (edge_wave) NIS_FIX(0);
+    // The candidate histograms are cleared by the first half of the waves
+    // (whose loads were issued first and land first); the second half runs
+    // at a raised priority, ahead of the first half's work on the same
+    // SIMDs once its data arrives.
+    if (w >= kWaves / 2) {
+        NIS_SETPRIO();
+    } else {
+        for (int i = tid; i < kHB + 64; i += kBlock / 2) sh.s.hist[i] = 0ull;
+        if (tid < 32 + 64) sh.s.chist[tid] = 0ull;
+    }
+
+    // wave-local reference from the wave's first chunk
+    if (Kw == 0)
+        xv[0] = f4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    else if (edge_wave)
+        NIS_FIX(0);
     const float m0 = wmax_f32(max4(xv[0]));
     const float Rw = (m0 > -INFINITY && fabsf(m0 * c) < 1e30f) ? ceilf(m0 * c) : 0.0f;
     const float RwH = Rw + kTopHead;
@@ -457,19 +632,18 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     // list (index order, only the hit lanes store; past the capacity they
     // all write the last slot and the overflow is caught after the stream).
     // x_lo = max over the waves of th_w is a threshold at and above which
-    // every element is listed; it is proven safe after the stream
-    // (sampler.rs:150 for the largest element below it).  th_w = +inf when
-    // no bin fits, and without top-p.
+    // every element is listed; th_w = +inf when no bin fits, and without
+    // top-p.
     double z = 0.0;
     float mx = -INFINITY;
     float mx4[kNch];
     float cz = c, Rz = Rw;
     asm volatile("" : "+v"(cz), "+v"(Rz));
-    uint32_t* const whist = reinterpret_cast<uint32_t*>(&sh.s.ce[w][0]);
+    uint32_t* const whist = reinterpret_cast<uint32_t*>(&sh.s.cx[w][0]);
     const uint32_t ent_x0 = lds_addr(&sh.s.u.l.ent_x[w][0]);
     const uint32_t ent_p0 = lds_addr(&sh.s.u.l.ent_pos[w][0]);
     float thw = INFINITY;
-    uint32_t nw = 0, nc = 0;
+    uint32_t nw = 0;
 #define NIS_LIST(k)                                                                      \
     {                                                                                    \
         const uint64_t mk = __ballot(mx4[k] >= thw);                                     \
@@ -478,8 +652,11 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         nw += (uint32_t)__popcll(mk);                                                    \
     }
 #define NIS_STREAM(FIX)                                                                 \
-    _Pragma("unroll") for (int k = 0; k < kNch; ++k) {                                 \
-        if (FIX && k > 0) NIS_FIX(k);                                                   \
+    _Pragma("unroll") for (int k = 0; k < kNch; ++k) if (k >= Kp) {                     \
+        xv[k] = f4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};                        \
+    } else {                                                                            \
+        if (k >= Kw) xv[k] = f4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};           \
+        else if (FIX && k > 0) NIS_FIX(k);                                              \
         const f4v x = xv[k];                                                            \
         f4v e;                                                                          \
         e.x = mass_of(x.x, cz, Rz);                                                     \
@@ -516,45 +693,16 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
 #undef NIS_LIST
     NIS_TS(1);
 
-    // ---- this wave's candidates: compaction of its list to single elements
-    // >= th_w, in index order (while other waves' loads still land)
-    if (topp) {
-        lds_wave_fence();
-        const int ns = 4 * (int)min(nw, (uint32_t)kWaveEnt);
-        const float* entf = reinterpret_cast<const float*>(&sh.s.u.l.ent_x[w][0]);
-        const uint32_t cx0 = lds_addr(&sh.s.cx[w][0]);
-        const uint32_t ci0 = lds_addr(&sh.s.ci[w][0]);
-        // four groups of 64 slots per step, their reads issued together
-        // (clamped into the list; slots past ns take no part)
-        #pragma unroll 1
-        for (int s0 = 0; s0 < ns; s0 += 256) {
-            float xq[4];
-            uint32_t pq[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int s = min(s0 + 64 * u + l, 4 * kWaveEnt - 1);
-                xq[u] = entf[s];
-                pq[u] = sh.s.u.l.ent_pos[w][s >> 2];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int s = s0 + 64 * u + l;
-                const uint64_t mk = __ballot((s < ns) & (xq[u] >= thw));
-                const uint32_t slot = min(nc + lane_rank(mk), (uint32_t)kWaveCand - 1);
-                lds_put_u32x2(mk, cx0 + 4 * slot, __float_as_uint(xq[u]), ci0 + 4 * slot,
-                              (uint32_t)(4 * (w * kWaveSlots + (int)pq[u]) + (s & 3) - mis));
-                nc += (uint32_t)__popcll(mk);
-            }
-        }
-        lds_put_rec(lds_addr(&sh.tc[w]), (double)thw, nw, nc);
-    }
-    NIS_TS(2);
+    // ---- stream end: this wave's totals, threshold and list length -------
+    mx = wmax_f32(mx);
+    z = wsum_f64(z);
+    lds_put_rec(lds_addr(&sh.t1[w]), z, __float_as_uint(mx), __float_as_uint(Rw));
+    lds_put_rec(lds_addr(&sh.tc[w]), (double)thw, nw, 0u);
+
     // sampler.rs:209: the row's single RNG advance, drawn here by wave 0
-    // (which waits for the slower waves anyway) into LDS; written back to
-    // memory only when the row completes on this path.
+    // into LDS; written back to memory only when the row completes on this
+    // path.
     if (w == 0) {
-        const uint64_t rsv =
-            ((const __attribute__((address_space(1))) uint64_t*)(a.rng + 4 * (int64_t)row))[l & 3];
         uint64_t st[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -567,10 +715,29 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
         NIS_PUT(l == 4, sh.rng[3], st[3]);
     }
 
+    // ---- candidates: every wave takes its own list once its stream ends.
+    // One barrier orders the clearing of the histograms before any addition:
+    // the first half compacts its list before it (its data came first) and
+    // adds to the histograms after it; the second half takes the barrier at
+    // its stream end, where the first half is already waiting.
+    if (w < kWaves / 2) {
+        const uint32_t nco = topp ? take_entries(sh, w, min(nw, (uint32_t)kWaveEnt), thw, S, mis) : 0u;
+        lds_barrier();
+        if (topp) {
+            hist_list(sh, w, nco, c);
+            lds_put_lane0(lds_addr(&sh.ncnt[w]), nco);
+        }
+    } else {
+        lds_barrier();
+        if (topp) {
+            const uint32_t nco = take_entries(sh, w, min(nw, (uint32_t)kWaveEnt), thw, S, mis);
+            hist_list(sh, w, nco, c);
+            lds_put_lane0(lds_addr(&sh.ncnt[w]), nco);
+        }
+    }
+    NIS_TS(2);
+
     // ---- T1: row max, reference R, Z ---------------------------------------
-    mx = wmax_f32(mx);
-    z = wsum_f64(z);
-    lds_put_rec(lds_addr(&sh.t1[w]), z, __float_as_uint(mx), __float_as_uint(Rw));
     lds_barrier();
     double zw[kWaves];
     uint32_t mxw[kWaves], rww[kWaves];
@@ -602,299 +769,325 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     uint32_t reject = NIS_REJECT_NONE;  // reason of a failed sparse attempt
     if (topp) {
         double thv[kWaves];
-        uint32_t nwv[kWaves], ncv[kWaves];
-        read_recs(sh.tc, thv, nwv, ncv);
-        float x_lo = -INFINITY;
+        uint32_t nwv[kWaves], unused[kWaves];
+        read_recs(sh.tc, thv, nwv, unused);
+        const u4v nca = *reinterpret_cast<const u4v*>(&sh.ncnt[0]);
+        const u4v ncb = *reinterpret_cast<const u4v*>(&sh.ncnt[4]);
+        uint32_t ncv[kWaves];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            ncv[q] = elemu(nca, q);
+            ncv[q + 4] = elemu(ncb, q);
+        }
+        float x_lo = -INFINITY, th_min = INFINITY;
         uint32_t nwmax = 0, ncmax = 0;
 #pragma unroll
         for (int i = 0; i < kWaves; ++i) {
             x_lo = fmaxf(x_lo, (float)thv[i]);
+            th_min = fminf(th_min, (float)thv[i]);
             nwmax = max(nwmax, nwv[i]);
             ncmax = max(ncmax, ncv[i]);
         }
         NIS_TS(3);
+        // the histogram rings must hold every candidate without aliasing, and
+        // bucket numbers must fit an int
+        const bool fits = (x_lo < INFINITY) & (x_lo <= M) & (fabsf(M * c) < 1e6f) &
+                          (fabsf(th_min * c) < 1e6f);
+        const int bM = fits ? hbucket(M, c) : 0;
+        const int blo = fits ? hbucket(x_lo, c) : 0;
+        const int bmn = fits ? hbucket(th_min, c) : 0;
         reject = NIS_REJECT_CAPACITY;
-        if ((x_lo < INFINITY) & (nwmax <= (uint32_t)kWaveEnt) & (ncmax <= (uint32_t)kWaveCand)) {
-            // ---- candidate masses and their fine histogram over [x_lo, M]
-            // (a wave's candidates below x_lo, listed against a lower th_w,
-            // take no part: dummy bucket, no mass)
-            const int ncc = (int)min(nc, (uint32_t)kWaveCand);
-            const float inv_w = (M > x_lo) ? (float)kFineBins / (M - x_lo) : 0.0f;
-            double g = 0.0;
-            // two groups of 64 per step (indices past the list read its spare slots)
-            #pragma unroll 1
-            for (int j0 = 0; j0 < ncc; j0 += 128) {
-                const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
-                const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
-#define NIS_CAND(j, x)                                                            \
-    {                                                                             \
-        const bool ok = ((j) < ncc) & ((x) >= x_lo);                              \
-        const float xs = ok ? (x) : x_lo;                                         \
-        const float e = ok ? mass_of(xs, c, R) : 0.0f;                            \
-        const int b = ok ? fine_bucket(xs, x_lo, inv_w) : kFineBins + l;          \
-        sh.s.ce[w][(j)] = e;                                                      \
-        sh.s.cb[w][(j)] = (uint16_t)b;                                            \
-        g += (double)e;                                                           \
-        atomicAdd(&sh.fcnt[b], 1u);                                               \
-        atomicAdd(&sh.fmass[b], fix40(e));                                        \
-        atomicMax(&sh.fkmax[b], key32(xs));                                       \
-    }
-                NIS_CAND(ja, xa)
-                NIS_CAND(jb, xb)
-#undef NIS_CAND
-            }
-            NIS_TS(4);
-            g = wsum_f64(g);
-            lds_put_rec(lds_addr(&sh.wc[w]), g, nw, nc);
-            lds_barrier();
-            NIS_TS(5);
-            double gw[kWaves];
-            uint32_t nww[kWaves], ncw[kWaves];
-            read_recs(sh.wc, gw, nww, ncw);
-            double Gc = 0.0;
-#pragma unroll
-            for (int i = 0; i < kWaves; ++i) Gc += gw[i];
-            if (!(Gc - (double)mass_of(x_lo, c, R) > pZR)) {
-                // the largest element below x_lo might be kept
-                reject = NIS_REJECT_WINDOW;
-            } else {
-                // ---- S4: the fine bucket holding the cutoff (block-wide) ---
-                // lane t owns buckets 1023-2t (upper) and 1022-2t
-                const int bA = kFineBins - 1 - 2 * tid, bB = bA - 1;
-                const uint32_t cA = sh.fcnt[bA], cB = sh.fcnt[bB];
-                const double mA = (double)sh.fmass[bA] * (1.0 / kFix);
-                const double mB = (double)sh.fmass[bB] * (1.0 / kFix);
-                // mass of each bucket's largest element (an empty bucket's
-                // key 0 gives NaN, and its test below is false anyway)
-                const float eA = mass_of(unkey32(sh.fkmax[bA]), c, R);
-                const float eB = mass_of(unkey32(sh.fkmax[bB]), c, R);
-                const double mt = mA + mB;
-                const double inc = wscan_f64(mt);
-                NIS_PUT(l == 63, sh.da[w], inc);
-                lds_barrier();
-                double gbase = 0.0;
-#pragma unroll
-                for (int i = 0; i < kWaves; ++i) gbase += (i < w) ? sh.da[i] : 0.0;
-                const double GA = gbase + (inc - mt);  // candidate mass above bucket bA
-                const double GB = GA + mA;
-                // sampler.rs:150 for the largest element of the bucket
-                const bool kA = (cA != 0) & (GA - (double)eA <= pZR);
-                const bool kB = (cB != 0) & (GB - (double)eB <= pZR);
-                sh.s.gab[bA] = GA;
-                sh.s.gab[bB] = GB;
-                const int lowk =
-                    (int)(-wmax_f32(-(float)(kB ? bB : (kA ? bA : kFineBins))));  // DPP wave min
-                NIS_PUT(l == 0, sh.ia[w], lowk);
-                lds_barrier();
-                int bstar = kFineBins;
-#pragma unroll
-                for (int i = 0; i < kWaves; ++i) bstar = min(bstar, sh.ia[i]);
-                NIS_TS(6);
-                const uint32_t nstar = (bstar < kFineBins) ? sh.fcnt[bstar] : 0u;
-                if (bstar >= kFineBins || nstar > (uint32_t)kMaxFinal) {
-                    reject = NIS_REJECT_CAPACITY;
+        if (fits & (nwmax <= (uint32_t)kWaveEnt) & (ncmax <= (uint32_t)kWaveCand) &
+            (bM - bmn < kHB) & ((bM >> 6) - (bmn >> 6) < 32)) {
+            const int Ri = (int)R;
+            // ---- S4: the cutoff, located by every wave on its own (no
+            // barrier).  sampler.rs:150 is tested on each bucket's largest
+            // element with the bucket's upper edge standing in for it: a
+            // permissive test, so the cutoff lies in the lowest passing
+            // non-empty bucket or in the next non-empty one above it.
+            // Octaves first (lane l: octave oM - l), then the 1/64-octave
+            // buckets of the two candidate octaves.  Everything above x_lo's
+            // bucket is complete in the histograms.
+            const int oM = bM >> 6, olo = blo >> 6;
+            const int nco = oM - olo;  // octaves above x_lo's, < 32
+            const int oc = oM - l;
+            const bool cin = l <= nco;
+            const unsigned long long cv = cin ? sh.s.chist[oc & 31] : 0ull;
+            const double cm = ldexp((double)(cv & 0xFFFFFFFFFFFFull), oc - Ri - 24);
+            const double cG = wscan_f64(cm) - cm;  // mass of the octaves above
+            const double cup = ldexp(1.0001, oc + 1 - Ri);
+            const bool cne = cin & ((cv >> 48) != 0ull);
+            const uint64_t cpass = __ballot(cne & (cG - cup <= pZR));
+            const uint64_t cnem = __ballot(cne);
+            // octave x_lo lies in: everything up to its top is removed
+            const bool clo_ok = __builtin_amdgcn_readlane((int)(cG - cup > pZR), nco) != 0;
+            const int lp = cpass ? 63 - __clzll((long long)cpass) : -1;  // deepest passing octave
+            const uint64_t above_p = (lp > 0) ? (cnem & ((1ull << lp) - 1ull)) : 0ull;
+            const int la = above_p ? 63 - __clzll((long long)above_p) : -1;
+            const int Cp = oM - lp, Ca = (la >= 0) ? oM - la : Cp;
+            const double Gcp = bcast_f64(cG, max(lp, 0));
+            const double Gca = bcast_f64(cG, max(la, 0));
+            // fine level: lane l holds bucket 64 C + 63 - l of C = Cp and of C = Ca
+            const int bp_l = 64 * Cp + 63 - l, ba_l = 64 * Ca + 63 - l;
+            const unsigned long long fpv = sh.s.hist[bp_l & (kHB - 1)];
+            const unsigned long long fav = sh.s.hist[ba_l & (kHB - 1)];
+            const double fpm = ldexp((double)(fpv & 0xFFFFFFFFFFFFull), Cp - Ri - 24);
+            const double fam = ldexp((double)(fav & 0xFFFFFFFFFFFFull), Ca - Ri - 24);
+            const double Gp_l = Gcp + (wscan_f64(fpm) - fpm);  // mass above each bucket
+            const double Ga_l = Gca + (wscan_f64(fam) - fam);
+            const float fe = __builtin_amdgcn_exp2f((float)(63 - l + 1) * (1.0f / 64.0f)) * 1.0001f;
+            const double eup_p = ldexp((double)fe, Cp - Ri), eup_a = ldexp((double)fe, Ca - Ri);
+            const bool pne = ((fpv >> 48) != 0ull) & (bp_l > blo);
+            const bool ane = ((fav >> 48) != 0ull) & (la >= 0);
+            const uint64_t ppass = __ballot(pne & (Gp_l - eup_p <= pZR));
+            const uint64_t apass = __ballot(ane & (Ga_l - eup_a <= pZR));
+            const uint64_t pnem = __ballot(pne), anem = __ballot(ane);
+            // the deepest passing bucket b_p, and the next non-empty one above
+            int b_p, b_a, lgp, lga;  // lgp / lga: lanes whose running masses give G
+            bool gin_p, gin_a;       // ... taken in the Cp (true) or Ca (false) octave
+            if (ppass) {
+                const int lb = 63 - __clzll((long long)ppass);
+                b_p = 64 * Cp + 63 - lb;
+                lgp = lb;
+                gin_p = true;
+                const uint64_t up = pnem & ((1ull << lb) - 1ull);
+                if (up) {
+                    lga = 63 - __clzll((long long)up);
+                    b_a = 64 * Cp + 63 - lga;
+                    gin_a = true;
+                } else if (anem) {
+                    lga = 63 - __clzll((long long)anem);
+                    b_a = 64 * Ca + 63 - lga;
+                    gin_a = false;
                 } else {
-                    const double gab = sh.s.gab[bstar];
-                    // ---- gather the cutoff bucket's members; sum the mass and
-                    // count of the candidates above it (all kept) per wave ------
-                    // (members go to the wave's own list: no slot allocation
-                    // across waves, so no atomic round trip)
-                    double sw = 0.0;
-                    uint32_t sn = 0, nm = 0;
-                    const uint32_t gx0 = lds_addr(&sh.s.u.g.gx[w][0]);
-                    const uint32_t gi0 = lds_addr(&sh.s.u.g.gi[w][0]);
-                    const uint32_t ge0 = lds_addr(&sh.s.u.g.ge[w][0]);
-                    #pragma unroll 1
-                    for (int j0 = 0; j0 < ncc; j0 += 128) {
-                        const int ja = j0 + l, jb = min(j0 + 64 + l, kWaveCand + 63);
-                        const int ba = sh.s.cb[w][ja], bb = sh.s.cb[w][jb];
-                        const float ea = sh.s.ce[w][ja], eb = sh.s.ce[w][jb];
-                        const float xa = sh.s.cx[w][ja], xb = sh.s.cx[w][jb];
-                        const uint32_t ia = sh.s.ci[w][ja], ib = sh.s.ci[w][jb];
-                        const bool va = ja < ncc, vb = jb < ncc;
-                        // (dummy buckets >= kFineBins: candidates below x_lo)
-                        const bool sa = va & (ba > bstar) & (ba < kFineBins);
-                        const bool sb = vb & (bb > bstar) & (bb < kFineBins);
-                        sw += (sa ? (double)ea : 0.0) + (sb ? (double)eb : 0.0);
-                        sn += (sa ? 1u : 0u) + (sb ? 1u : 0u);
-#define NIS_GATHER(v, b, x, i, e)                                                      \
-    {                                                                                  \
-        const uint64_t mk = __ballot((v) & ((b) == bstar));                            \
-        const uint32_t sc = min(nm + lane_rank(mk), (uint32_t)kMaxFinal - 1);          \
-        lds_put_u32x3(mk, gx0 + 4 * sc, __float_as_uint(x), gi0 + 4 * sc, (i), ge0 + 4 * sc, \
-                      __float_as_uint(e));                                             \
-        nm += (uint32_t)__popcll(mk);                                                  \
-    }
-                        NIS_GATHER(va, ba, xa, ia, ea)
-                        NIS_GATHER(vb, bb, xb, ib, eb)
-#undef NIS_GATHER
+                    b_a = b_p;
+                    lga = lgp;
+                    gin_a = true;
+                }
+            } else {
+                const int lb = apass ? 63 - __clzll((long long)apass) : 0;
+                b_p = 64 * Ca + 63 - lb;
+                lgp = lb;
+                gin_p = false;
+                const uint64_t up = anem & ((1ull << lb) - 1ull);
+                lga = up ? 63 - __clzll((long long)up) : lb;
+                b_a = 64 * Ca + 63 - lga;
+                gin_a = false;
+            }
+            const double gtop = bcast_f64(gin_a ? Gp_l : Ga_l, lga);  // mass above b_a
+            // x_lo's bucket and everything below it is removed
+            const int llo = 64 * Cp + 63 - blo;
+            const bool flo_ok = __builtin_amdgcn_readlane(
+                                    (int)(Gp_l - ldexp((double)fe, Cp - Ri) > pZR), min(max(llo, 0), 63)) != 0;
+            const bool lo_ok = (Cp > olo) ? clo_ok : flo_ok;
+            NIS_TS(4);
+            if (!lo_ok || lp < 0 || !(ppass | apass)) {
+                reject = NIS_REJECT_WINDOW;  // the cutoff may lie at or below x_lo
+            } else {
+                // ---- each wave over its own candidates: the members of the
+                // two buckets, and the kept mass of everything above them, in
+                // 64 index-ordered segments ---------------------------------
+                const int ncw = (int)min(ncv[w], (uint32_t)kWaveCand);
+                const int sg = (ncw + 63) >> 6;
+                constexpr int kSeg = (kWaveCand + 63) / 64;
+                float xs[kSeg];
+                uint32_t is[kSeg];
+#pragma unroll
+                for (int i = 0; i < kSeg; ++i) {
+                    const int jc = min(l * sg + i, kWaveCand - 1);
+                    xs[i] = sh.s.cx[w][jc];
+                    is[i] = sh.s.ci[w][jc];
+                }
+                double ssum = 0.0;
+                uint32_t scount = 0, memm = 0;
+                float es[kSeg];
+#pragma unroll
+                for (int i = 0; i < kSeg; ++i) {
+                    const int j = l * sg + i;
+                    const bool v = (i < sg) & (j < ncw);
+                    const int b = hbucket(xs[i], c);
+                    es[i] = canon_mass(xs[i], c, Ri);
+                    const bool sure = v & (b > b_a);
+                    ssum += sure ? (double)es[i] : 0.0;
+                    scount += sure ? 1u : 0u;
+                    memm |= (v & ((b == b_p) | (b == b_a))) ? (1u << i) : 0u;
+                }
+                const uint32_t nml = (uint32_t)__popc(memm);
+                const uint32_t mincl = wscan_u32(nml);
+                const uint32_t nm = (uint32_t)__builtin_amdgcn_readlane((int)mincl, 63);
+                const uint32_t gx0 = lds_addr(&sh.s.u.g.gx[w][0]);
+                const uint32_t gi0 = lds_addr(&sh.s.u.g.gi[w][0]);
+                const uint32_t ge0 = lds_addr(&sh.s.u.g.ge[w][0]);
+#pragma unroll
+                for (int i = 0; i < kSeg; ++i) {
+                    const uint32_t sc =
+                        min(mincl - nml + (uint32_t)__popc(memm & ((1u << i) - 1u)), (uint32_t)kMaxFinal - 1);
+                    lds_put_u32x3(__ballot((memm >> i) & 1u), gx0 + 4 * sc, __float_as_uint(xs[i]),
+                                  gi0 + 4 * sc, is[i], ge0 + 4 * sc, __float_as_uint(es[i]));
+                }
+                const double sw = wsum_f64(ssum);
+                const uint32_t sn = wsum_u32(scount);
+                lds_put_rec(lds_addr(&sh.wg[w]), sw, sn, nm);
+                lds_barrier();
+                NIS_TS(5);
+                double sww[kWaves];
+                uint32_t snw[kWaves], nmw[kWaves];
+                read_recs(sh.wg, sww, snw, nmw);
+                uint32_t nmtot = 0;
+#pragma unroll
+                for (int i = 0; i < kWaves; ++i) nmtot += nmw[i];
+                if (nmtot > (uint32_t)kMaxFinal) {
+                    reject = NIS_REJECT_BUCKET;
+                } else {
+                    // ---- wave 0 alone from here: the exact rule among the
+                    // members, the draw, and the walk ----------------------------
+                    if (w != 0) return NIS_REJECT_NONE;
+                    const int n = (int)nmtot;
+                    const bool valid = l < n;
+                    // member l of the waves' lists taken in wave order
+                    int mwv = 0;
+                    uint32_t mbase = 0, acc = 0;
+#pragma unroll
+                    for (int i = 0; i < kWaves; ++i) {
+                        const bool here = (uint32_t)l >= acc;
+                        mwv = here ? i : mwv;
+                        mbase = here ? acc : mbase;
+                        acc += nmw[i];
                     }
-                    sw = wsum_f64(sw);
-                    sn = wsum_u32(sn);
-                    lds_put_rec(lds_addr(&sh.wg[w]), sw, sn, nm);
-                    lds_barrier();
-                    NIS_TS(7);
-                    double sww[kWaves];
-                    uint32_t snw[kWaves], nmw[kWaves];
-                    read_recs(sh.wg, sww, snw, nmw);
-                    uint32_t nmtot = 0;
+                    const int mj = min(l - (int)mbase, kMaxFinal - 1);  // in bounds for every lane
+                    const float gxv = sh.s.u.g.gx[mwv][mj];
+                    const uint32_t giv = sh.s.u.g.gi[mwv][mj];
+                    const float gev = sh.s.u.g.ge[mwv][mj];
+                    const float xm = valid ? gxv : -INFINITY;
+                    const uint32_t im = valid ? giv : 0xFFFFFFFFu;
+                    const float em = valid ? gev : 0.0f;
+                    // sort key: value descending, then index ascending
+                    const uint64_t km = ((uint64_t)key32(xm) << 32) | (uint64_t)(~im);
+                    // mass of the members ahead of this one in the reference's
+                    // stable descending order
+                    double pre = 0.0;
+                    #pragma unroll 1
+                    for (int j0 = 0; j0 < n; j0 += 4) {
 #pragma unroll
-                    for (int i = 0; i < kWaves; ++i) nmtot += nmw[i];
-                    if (nmtot != nstar) {
-                        reject = NIS_REJECT_BUCKET;
-                    } else {
-                        // ---- wave 0 alone from here: the exact rule inside the
-                        // bucket, the draw, and the walk over the list of the wave
-                        // that holds the crossing (all of it in LDS) -------------
-                        if (w != 0) return NIS_REJECT_NONE;
-                        const int n = (int)nstar;
-                        const bool valid = l < n;
-                        // member l of the waves' lists taken in wave order
-                        int mwv = 0;
-                        uint32_t mbase = 0, acc = 0;
-#pragma unroll
-                        for (int i = 0; i < kWaves; ++i) {
-                            const bool here = (uint32_t)l >= acc;
-                            mwv = here ? i : mwv;
-                            mbase = here ? acc : mbase;
-                            acc += nmw[i];
+                        for (int u = 0; u < 4; ++u) {
+                            const int j = min(j0 + u, 63);
+                            const uint64_t kj = ((uint64_t)bcast_u32((uint32_t)(km >> 32), j) << 32) |
+                                                bcast_u32((uint32_t)km, j);
+                            const float ej = bcast_f32(em, j);
+                            pre += ((j0 + u < n) & (kj > km)) ? (double)ej : 0.0;
                         }
-                        const int mj = min(l - (int)mbase, kMaxFinal - 1);  // in bounds for every lane
-                        const float gxv = sh.s.u.g.gx[mwv][mj];
-                        const uint32_t giv = sh.s.u.g.gi[mwv][mj];
-                        const float gev = sh.s.u.g.ge[mwv][mj];
-                        const float xm = valid ? gxv : -INFINITY;
-                        const uint32_t km = key32(xm);
-                        const uint32_t im = valid ? giv : 0u;
-                        const float em = valid ? gev : 0.0f;
-                        // mass of the members ahead of this one in the
-                        // reference's stable descending order
-                        double pre = 0.0;
-                        #pragma unroll 1
-                        for (int j0 = 0; j0 < n; j0 += 4) {
+                    }
+                    const bool kept = valid & (gtop + pre - (double)em <= pZR);
+                    // the last kept member: smallest value, then largest index
+                    // (DPP maxima; indices < 2^24 are exact in float)
+                    const float xcut = -wmax_f32(kept ? -xm : -INFINITY);
+                    const float icut = wmax_f32((kept & (xm == xcut)) ? (float)im : -1.0f);
+                    const uint32_t kc = key32(xcut), ic = (uint32_t)icut;
+                    // per-wave kept mass and count (lanes 0..7): the wave's sure
+                    // part plus its kept members, which sit in lanes
+                    // [start_w, start_w + nm_w) in wave order
+                    const double kin = wscan_f64(kept ? (double)em : 0.0);
+                    const uint32_t kcn = wscan_u32(kept ? 1u : 0u);
+                    const int li = min(l, kWaves - 1);
+                    uint32_t st = 0, nmi = nmw[0];
+                    double T = sww[0];
+                    uint32_t TN = snw[0];
 #pragma unroll
-                            for (int u = 0; u < 4; ++u) {
-                                const int j = min(j0 + u, 63);
-                                const uint32_t kj = bcast_u32(km, j), ij = bcast_u32(im, j);
-                                const float ej = bcast_f32(em, j);
-                                const bool before = (j0 + u < n) & ((kj > km) | ((kj == km) & (ij < im)));
-                                pre += before ? (double)ej : 0.0;
-                            }
-                        }
-                        const bool kept = valid & (gab + pre - (double)em <= pZR);
-                        // the last kept member: smallest value, then largest
-                        // index (DPP maxima; indices < 2^24 are exact in float)
-                        const float xcut = -wmax_f32(kept ? -xm : -INFINITY);
-                        const float icut = wmax_f32((kept & (xm == xcut)) ? (float)im : -1.0f);
-                        const uint32_t kc = key32(xcut), ic = (uint32_t)icut;
-                        // per-wave kept mass (lanes 0..7): the wave's sure mass plus
-                        // its kept members, added in member order
-                        const int mw = min((int)((im + (uint32_t)mis) / (uint32_t)(4 * kWaveSlots)), kWaves - 1);
-                        const int li = min(l, kWaves - 1);
-                        double T = sww[0];
-                        uint32_t TN = snw[0];
+                    for (int i = 1; i < kWaves; ++i) {
+                        st += (i <= li) ? nmw[i - 1] : 0u;
+                        nmi = (li == i) ? nmw[i] : nmi;
+                        T = (li == i) ? sww[i] : T;
+                        TN = (li == i) ? snw[i] : TN;
+                    }
+                    const int hi = (int)(st + nmi) - 1, lo = (int)st - 1;
+                    const double khi = __shfl(kin, max(hi, 0)), klo = __shfl(kin, max(lo, 0));
+                    const uint32_t chi = __shfl(kcn, max(hi, 0)), clo = __shfl(kcn, max(lo, 0));
+                    T += (nmi != 0u) ? (khi - ((lo >= 0) ? klo : 0.0)) : 0.0;
+                    TN += (nmi != 0u) ? (chi - ((lo >= 0) ? clo : 0u)) : 0u;
+                    T = (l < kWaves) ? T : 0.0;
+                    TN = (l < kWaves) ? TN : 0u;
+                    const double Tincl = wscan_f64(T);
+                    const double zk = bcast_f64(Tincl, 63);
+                    const uint32_t kept_total = wsum_u32(TN);
+                    const double u = sh.bd[1];  // the draw (sampler.rs:209), made before T1
+                    const double r = u * zk;
+                    // the first wave whose running total reaches r (and has
+                    // mass); rounding: the last wave with mass
+                    const uint64_t hw = __ballot((l < kWaves) & (T > 0.0) & (Tincl >= r));
+                    const uint64_t nzw = __ballot((l < kWaves) & (T > 0.0));
+                    const int wsel = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)nzw));
+                    const double run = bcast_f64(Tincl - T, wsel);
+                    int ncsel = (int)min(ncv[0], (uint32_t)kWaveCand);
 #pragma unroll
-                        for (int i = 1; i < kWaves; ++i) {
-                            T = (li == i) ? sww[i] : T;
-                            TN = (li == i) ? snw[i] : TN;
-                        }
-                        #pragma unroll 1
-                        for (uint64_t km_ = __ballot(kept); km_ != 0; km_ &= km_ - 1) {
-                            const int j = __ffsll((long long)km_) - 1;
-                            const bool mine = (int)bcast_u32((uint32_t)mw, j) == l;
-                            T += mine ? (double)bcast_f32(em, j) : 0.0;
-                            TN += mine ? 1u : 0u;
-                        }
-                        T = (l < kWaves) ? T : 0.0;
-                        TN = (l < kWaves) ? TN : 0u;
-                        const double Tincl = wscan_f64(T);
-                        const double zk = bcast_f64(Tincl, 63);
-                        const uint32_t kept_total = wsum_u32(TN);
-                        const double u = sh.bd[1];  // the draw (sampler.rs:209), made before T1
-                        const double r = u * zk;
-                        // the first wave whose running total reaches r (and has
-                        // mass); rounding: the last wave with mass
-                        const uint64_t hw = __ballot((l < kWaves) & (T > 0.0) & (Tincl >= r));
-                        const uint64_t nzw = __ballot((l < kWaves) & (T > 0.0));
-                        const int wsel = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)nzw));
-                        double run = bcast_f64(Tincl - T, wsel);
-                        uint32_t nsel = ncw[0];
+                    for (int i = 1; i < kWaves; ++i)
+                        ncsel = (i == wsel) ? (int)min(ncv[i], (uint32_t)kWaveCand) : ncsel;
+                    const int sgs = (ncsel + 63) >> 6;
+                    NIS_TS(6);
+                    // ---- S7: the walk (sampler.rs:209-216) over the chosen
+                    // wave's candidates: lane l sums the kept masses of its
+                    // segment, the lane whose running total reaches r walks it
 #pragma unroll
-                        for (int i = 1; i < kWaves; ++i) nsel = (i == wsel) ? ncw[i] : nsel;
-                        const int ncs = (int)min(nsel, (uint32_t)kWaveCand);
-                        NIS_TS(8);
-                        // ---- S7: inverse-CDF walk over the chosen wave's list ------
-                        // lane l sums the kept masses of list entries
-                        // [l*sg, l*sg + sg); the lane whose running total reaches
-                        // r then walks its own entries
-                        constexpr int kSeg = (kWaveCand + 63) / 64;
-                        const int sg = (ncs + 63) >> 6;
-                        float xe[kSeg], ee[kSeg];
-                        uint32_t ie[kSeg];
-                        uint32_t kmask = 0;
-                        double lsum = 0.0;
+                    for (int i = 0; i < kSeg; ++i) {
+                        const int jc = min(l * sgs + i, kWaveCand - 1);
+                        xs[i] = sh.s.cx[wsel][jc];
+                        is[i] = sh.s.ci[wsel][jc];
+                    }
+                    double lsum = 0.0;
+                    uint32_t kmask = 0;
+#pragma unroll
+                    for (int i = 0; i < kSeg; ++i) {
+                        const int j = l * sgs + i;
+                        const uint32_t k = key32(xs[i]);
+                        const bool kj = (i < sgs) & (j < ncsel) & ((k > kc) | ((k == kc) & (is[i] <= ic)));
+                        es[i] = canon_mass(xs[i], c, Ri);
+                        kmask |= kj ? (1u << i) : 0u;
+                        lsum += kj ? (double)es[i] : 0.0;
+                    }
+                    const double sincl = wscan_f64(lsum);
+                    const uint64_t hitl = __ballot((run + sincl >= r) & (lsum > 0.0));
+                    const uint64_t nzl = __ballot(lsum > 0.0);
+                    const int Ls = hitl ? (__ffsll((long long)hitl) - 1) : (63 - __clzll((long long)nzl));
+                    if (l == Ls) {
+                        double run2 = run + sincl - lsum;
+                        int tok = -1, last = -1;
+                        float et = 0.0f, elast = 0.0f;
 #pragma unroll
                         for (int i = 0; i < kSeg; ++i) {
-                            const int j = l * sg + i;
-                            const int jc = min(j, kWaveCand - 1);
-                            xe[i] = sh.s.cx[wsel][jc];
-                            ie[i] = sh.s.ci[wsel][jc];
-                            ee[i] = sh.s.ce[wsel][jc];
-                        }
-#pragma unroll
-                        for (int i = 0; i < kSeg; ++i) {
-                            const int j = l * sg + i;
-                            const uint32_t k = key32(xe[i]);
-                            const bool kj = (i < sg) & (j < ncs) & ((k > kc) | ((k == kc) & (ie[i] <= ic)));
-                            kmask |= kj ? (1u << i) : 0u;
-                            lsum += kj ? (double)ee[i] : 0.0;
-                        }
-                        const double sincl = wscan_f64(lsum);
-                        const uint64_t hitl = __ballot((run + sincl >= r) & (lsum > 0.0));
-                        const uint64_t nzl = __ballot(lsum > 0.0);
-                        const int Ls = hitl ? (__ffsll((long long)hitl) - 1) : (63 - __clzll((long long)nzl));
-                        if (l == Ls) {
-                            double run2 = run + sincl - lsum;
-                            int tok = -1, last = -1;
-                            float xt = 0.0f, xlast = 0.0f;
-#pragma unroll
-                            for (int i = 0; i < kSeg; ++i) {
-                                if ((kmask >> i) & 1u) {
-                                    run2 += (double)ee[i];
-                                    if (tok < 0) {
-                                        last = (int)ie[i];
-                                        xlast = xe[i];
-                                        if (run2 >= r) {
-                                            tok = (int)ie[i];
-                                            xt = xe[i];
-                                        }
+                            if ((kmask >> i) & 1u) {
+                                run2 += (double)es[i];
+                                if (tok < 0) {
+                                    last = (int)is[i];
+                                    elast = es[i];
+                                    if (run2 >= r) {
+                                        tok = (int)is[i];
+                                        et = es[i];
                                     }
                                 }
                             }
-                            bool tkept = true;
-                            if (tok < 0) {  // rounding: the last kept token of that wave
-                                tok = last;
-                                xt = xlast;
-                            }
-                            if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
-                                tok = 0;
-                                tkept = false;
-                            }
-                            const double zkM = zk * rho;
-                            const double prob = tkept ? (double)mass_of(xt, c, R) / zk : 0.0;
-                            write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
-                                             zkM, ZR * rho, u, prob, (uint64_t)kept_total, 1);
                         }
-                        if (l == 0) {
-                            uint64_t* sp = a.rng + 4 * (int64_t)row;
-                            sp[0] = sh.rng[0];
-                            sp[1] = sh.rng[1];
-                            sp[2] = sh.rng[2];
-                            sp[3] = sh.rng[3];
+                        bool tkept = true;
+                        if (tok < 0) {  // rounding: the last kept token of that segment
+                            tok = last;
+                            et = elast;
                         }
-                        NIS_TS(9);
-                        return NIS_REJECT_NONE;
+                        if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
+                            tok = 0;
+                            tkept = false;
+                        }
+                        const double zkM = zk * rho;
+                        const double prob = tkept ? (double)et / zk : 0.0;
+                        write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
+                                         zkM, ZR * rho, u, prob, (uint64_t)kept_total, 1);
                     }
+                    if (l == 0) {
+                        uint64_t* sp = a.rng + 4 * (int64_t)row;
+                        sp[0] = sh.rng[0];
+                        sp[1] = sh.rng[1];
+                        sp[2] = sh.rng[2];
+                        sp[3] = sh.rng[3];
+                    }
+                    NIS_TS(9);
+                    return NIS_REJECT_NONE;
                 }
             }
         }

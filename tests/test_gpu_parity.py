@@ -211,6 +211,25 @@ def test_padded_and_misaligned_rows(sampler, ld_extra):
            label=f"ld+{ld_extra}-greedy")
 
 
+@pytest.mark.parametrize("V", [256, 300, 1000, 2053, 4100, 16383, 16389, 30001, 53245])
+def test_register_layout_sizes(sampler, V):
+    # the register-resident path splits a row's float4 slots evenly over its
+    # eight waves in whole 64-slot chunks: sizes with fewer chunks than the
+    # sample, waves holding nothing, partial last chunks, and the largest V
+    rnd = np.random.Generator(np.random.PCG64(V))
+    B = 48
+    x = rnd.standard_normal((B, V), dtype=np.float32) * np.float32(3.0)
+    for ld in (V, V + 1, V + 3):
+        _check(sampler, x, V, _params(temperature=0.8, top_p=0.9), list(range(B)), ld=ld,
+               label=f"layout-V{V}-ld{ld}")
+    _check(sampler, x, V, _params(temperature=1.1, top_p=0.995), list(range(B)), ld=V + 2,
+           label=f"layout-V{V}-dense")
+    _check(sampler, x, V, _params(temperature=0.9, top_p=1.0), list(range(B)), ld=V + 1,
+           label=f"layout-V{V}-p1")
+    _check(sampler, x, V, _params(temperature=0.0), list(range(B)), ld=V + 3,
+           label=f"layout-V{V}-greedy")
+
+
 def test_penalty_and_top_k_full_vocab(sampler):
     rnd = np.random.Generator(np.random.PCG64(77))
     B, V = 48, 50257
