@@ -104,6 +104,9 @@ struct SparseShared {
             float gx[kWaves][kMaxFinal];
             uint32_t gi[kWaves][kMaxFinal];
             float ge[kWaves][kMaxFinal];
+            uint32_t gj[kWaves][kMaxFinal];  // position in the owner's candidate list
+            double seg[kWaves][64];          // kept mass above the cutoff buckets, per list segment
+            double mseg[64];                 // the chosen list's kept members, per segment
         } g;
     } u;
     float cx[kWaves][kWaveCand + 64];         // candidates (x >= th_w) in index order: logit
@@ -699,22 +702,6 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     lds_put_rec(lds_addr(&sh.t1[w]), z, __float_as_uint(mx), __float_as_uint(Rw));
     lds_put_rec(lds_addr(&sh.tc[w]), (double)thw, nw, 0u);
 
-    // sampler.rs:209: the row's single RNG advance, drawn here by wave 0
-    // into LDS; written back to memory only when the row completes on this
-    // path.
-    if (w == 0) {
-        uint64_t st[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
-        const double u0 = rng_next_f64(st);
-        NIS_PUT(l == 0, sh.bd[1], u0);
-        NIS_PUT(l == 1, sh.rng[0], st[0]);
-        NIS_PUT(l == 2, sh.rng[1], st[1]);
-        NIS_PUT(l == 3, sh.rng[2], st[2]);
-        NIS_PUT(l == 4, sh.rng[3], st[3]);
-    }
-
     // ---- candidates: every wave takes its own list once its stream ends.
     // One barrier orders the clearing of the histograms before any addition:
     // the first half compacts its list before it (its data came first) and
@@ -735,6 +722,22 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             lds_put_lane0(lds_addr(&sh.ncnt[w]), nco);
         }
     }
+    // sampler.rs:209: the row's single RNG advance, drawn here by wave 0
+    // into LDS; written back to memory only when the row completes on this
+    // path.
+    if (w == 0) {
+        uint64_t st[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
+        const double u0 = rng_next_f64(st);
+        NIS_PUT(l == 0, sh.bd[1], u0);
+        NIS_PUT(l == 1, sh.rng[0], st[0]);
+        NIS_PUT(l == 2, sh.rng[1], st[1]);
+        NIS_PUT(l == 3, sh.rng[2], st[2]);
+        NIS_PUT(l == 4, sh.rng[3], st[3]);
+    }
+
     NIS_TS(2);
 
     // ---- T1: row max, reference R, Z ---------------------------------------
@@ -895,35 +898,41 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
 #pragma unroll
                 for (int i = 0; i < kSeg; ++i) {
                     const int jc = min(l * sg + i, kWaveCand - 1);
-                    xs[i] = sh.s.cx[w][jc];
-                    is[i] = sh.s.ci[w][jc];
+                    xs[i] = (i < sg) ? sh.s.cx[w][jc] : -INFINITY;
+                    is[i] = (i < sg) ? sh.s.ci[w][jc] : 0u;
                 }
                 double ssum = 0.0;
                 uint32_t scount = 0, memm = 0;
                 float es[kSeg];
 #pragma unroll
                 for (int i = 0; i < kSeg; ++i) {
-                    const int j = l * sg + i;
-                    const bool v = (i < sg) & (j < ncw);
-                    const int b = hbucket(xs[i], c);
-                    es[i] = canon_mass(xs[i], c, Ri);
-                    const bool sure = v & (b > b_a);
-                    ssum += sure ? (double)es[i] : 0.0;
-                    scount += sure ? 1u : 0u;
-                    memm |= (v & ((b == b_p) | (b == b_a))) ? (1u << i) : 0u;
+                    es[i] = 0.0f;
+                    if (i < sg) {  // (wave-uniform)
+                        const int j = l * sg + i;
+                        const bool v = j < ncw;
+                        const int b = hbucket(xs[i], c);
+                        es[i] = canon_mass(xs[i], c, Ri);
+                        const bool sure = v & (b > b_a);
+                        ssum += sure ? (double)es[i] : 0.0;
+                        scount += sure ? 1u : 0u;
+                        memm |= (v & ((b == b_p) | (b == b_a))) ? (1u << i) : 0u;
+                    }
                 }
+                sh.s.u.g.seg[w][l] = ssum;
                 const uint32_t nml = (uint32_t)__popc(memm);
                 const uint32_t mincl = wscan_u32(nml);
                 const uint32_t nm = (uint32_t)__builtin_amdgcn_readlane((int)mincl, 63);
                 const uint32_t gx0 = lds_addr(&sh.s.u.g.gx[w][0]);
                 const uint32_t gi0 = lds_addr(&sh.s.u.g.gi[w][0]);
                 const uint32_t ge0 = lds_addr(&sh.s.u.g.ge[w][0]);
+                const uint32_t gj0 = lds_addr(&sh.s.u.g.gj[w][0]);
 #pragma unroll
                 for (int i = 0; i < kSeg; ++i) {
                     const uint32_t sc =
                         min(mincl - nml + (uint32_t)__popc(memm & ((1u << i) - 1u)), (uint32_t)kMaxFinal - 1);
-                    lds_put_u32x3(__ballot((memm >> i) & 1u), gx0 + 4 * sc, __float_as_uint(xs[i]),
-                                  gi0 + 4 * sc, is[i], ge0 + 4 * sc, __float_as_uint(es[i]));
+                    lds_put_u32x4(__ballot((memm >> i) & 1u), gx0 + 4 * sc, __float_as_uint(xs[i]),
+                                  gi0 + 4 * sc, is[i], ge0 + 4 * sc, __float_as_uint(es[i]), gj0 + 4 * sc,
+                                  (uint32_t)(l * sg + i));
                 }
                 const double sw = wsum_f64(ssum);
                 const uint32_t sn = wsum_u32(scount);
@@ -958,6 +967,8 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                     const float gxv = sh.s.u.g.gx[mwv][mj];
                     const uint32_t giv = sh.s.u.g.gi[mwv][mj];
                     const float gev = sh.s.u.g.ge[mwv][mj];
+                    const uint32_t gjv = sh.s.u.g.gj[mwv][mj];
+                    sh.s.u.g.mseg[l] = 0.0;
                     const float xm = valid ? gxv : -INFINITY;
                     const uint32_t im = valid ? giv : 0xFFFFFFFFu;
                     const float em = valid ? gev : 0.0f;
@@ -1024,58 +1035,38 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
                     const int sgs = (ncsel + 63) >> 6;
                     NIS_TS(6);
                     // ---- S7: the walk (sampler.rs:209-216) over the chosen
-                    // wave's candidates: lane l sums the kept masses of its
-                    // segment, the lane whose running total reaches r walks it
-#pragma unroll
-                    for (int i = 0; i < kSeg; ++i) {
-                        const int jc = min(l * sgs + i, kWaveCand - 1);
-                        xs[i] = sh.s.cx[wsel][jc];
-                        is[i] = sh.s.ci[wsel][jc];
-                    }
-                    double lsum = 0.0;
-                    uint32_t kmask = 0;
-#pragma unroll
-                    for (int i = 0; i < kSeg; ++i) {
-                        const int j = l * sgs + i;
-                        const uint32_t k = key32(xs[i]);
-                        const bool kj = (i < sgs) & (j < ncsel) & ((k > kc) | ((k == kc) & (is[i] <= ic)));
-                        es[i] = canon_mass(xs[i], c, Ri);
-                        kmask |= kj ? (1u << i) : 0u;
-                        lsum += kj ? (double)es[i] : 0.0;
-                    }
+                    // wave's candidates: the segment whose running total
+                    // reaches r (sure mass from the scan plus the kept members,
+                    // whose masses within the two buckets add exactly in any
+                    // order), then that segment's entries, one per lane
+                    if (kept & (mwv == wsel)) atomicAdd(&sh.s.u.g.mseg[min((int)gjv / max(sgs, 1), 63)], (double)em);
+                    const double lsum = sh.s.u.g.seg[wsel][l] + sh.s.u.g.mseg[l];
                     const double sincl = wscan_f64(lsum);
                     const uint64_t hitl = __ballot((run + sincl >= r) & (lsum > 0.0));
                     const uint64_t nzl = __ballot(lsum > 0.0);
-                    const int Ls = hitl ? (__ffsll((long long)hitl) - 1) : (63 - __clzll((long long)nzl));
-                    if (l == Ls) {
-                        double run2 = run + sincl - lsum;
-                        int tok = -1, last = -1;
-                        float et = 0.0f, elast = 0.0f;
-#pragma unroll
-                        for (int i = 0; i < kSeg; ++i) {
-                            if ((kmask >> i) & 1u) {
-                                run2 += (double)es[i];
-                                if (tok < 0) {
-                                    last = (int)is[i];
-                                    elast = es[i];
-                                    if (run2 >= r) {
-                                        tok = (int)is[i];
-                                        et = es[i];
-                                    }
-                                }
-                            }
-                        }
+                    const int Ls = hitl ? (__ffsll((long long)hitl) - 1) : max(63 - __clzll((long long)nzl), 0);
+                    const double run2 = bcast_f64(run + sincl - lsum, Ls);
+                    const int je = Ls * sgs + l;
+                    const bool ve = (l < sgs) & (je < ncsel);
+                    const float xe = sh.s.cx[wsel][min(je, kWaveCand - 1)];
+                    const uint32_t ie = sh.s.ci[wsel][min(je, kWaveCand - 1)];
+                    const uint32_t ke = key32(xe);
+                    const bool kj = ve & ((ke > kc) | ((ke == kc) & (ie <= ic)));
+                    const float ee = kj ? canon_mass(xe, c, Ri) : 0.0f;
+                    const double pe = wscan_f64((double)ee);
+                    const uint64_t hite = __ballot(kj & (run2 + pe >= r));
+                    const uint64_t kje = __ballot(kj);
+                    // rounding: the segment's last kept token
+                    const int Le = hite ? (__ffsll((long long)hite) - 1) : max(63 - __clzll((long long)kje), 0);
+                    if (l == Le) {
+                        int tok = (int)ie;
                         bool tkept = true;
-                        if (tok < 0) {  // rounding: the last kept token of that segment
-                            tok = last;
-                            et = elast;
-                        }
                         if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
                             tok = 0;
                             tkept = false;
                         }
                         const double zkM = zk * rho;
-                        const double prob = tkept ? (double)et / zk : 0.0;
+                        const double prob = tkept ? (double)ee / zk : 0.0;
                         write_row_result(a, row, (uint32_t)tok, NIS_PATH_DRAW, (double)M / temp,
                                          zkM, ZR * rho, u, prob, (uint64_t)kept_total, 1);
                     }
