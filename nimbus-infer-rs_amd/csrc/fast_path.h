@@ -682,7 +682,18 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
             const uint32_t nok = (uint32_t)(c0 <= kTopT) + (uint32_t)(c1 <= kTopT) +    \
                                  (uint32_t)(c2 <= kTopT) + (uint32_t)(c3 <= kTopT);     \
             const int bw = (int)wsum_u32(nok) - 1; /* the last bin whose count fits */  \
-            thw = (!topp || bw < 0) ? INFINITY : (RwH - (float)(bw + 1) * (1.0f / kTopRes)) / c; \
+            /* mass of the sampled maxima below the threshold (lower bound), and */    \
+            /* of all sampled elements (upper bound: 4x the maxima): when the */        \
+            /* first already exceeds what top-p may drop, the row is not sparse */     \
+            const float e0 = __builtin_amdgcn_exp2f(-(float)(4 * l) * (1.0f / kTopRes)); \
+            const float mq0 = (float)hc.x * e0, mq1 = (float)hc.y * e0 * 0.917004043f;   \
+            const float mq2 = (float)hc.z * e0 * 0.840896415f, mq3 = (float)hc.w * e0 * 0.771105413f; \
+            const float mlo = ((4 * l + 0 > bw) ? (float)hc.x * e0 * 0.917004043f : 0.0f) + \
+                              ((4 * l + 1 > bw) ? (float)hc.y * e0 * 0.840896415f : 0.0f) + \
+                              ((4 * l + 2 > bw) ? (float)hc.z * e0 * 0.771105413f : 0.0f) + \
+                              ((4 * l + 3 > bw) ? (float)hc.w * e0 * 0.707106781f : 0.0f); \
+            const bool flat = wsum_f32(mlo) > 4.0f * (1.0f - p) * wsum_f32(mq0 + mq1 + mq2 + mq3); \
+            thw = (!topp || bw < 0 || flat) ? INFINITY : (RwH - (float)(bw + 1) * (1.0f / kTopRes)) / c; \
             _Pragma("unroll") for (int j = 0; j < kTopS; ++j) NIS_LIST(j)               \
         }                                                                               \
         if (k >= kTopS) NIS_LIST(k)                                                     \
