@@ -84,7 +84,9 @@ typedef struct nis_row_stats {
 #define NIS_REJECT_NONFINITE 2  /* NaN / inf / empty row or exponent range */
 #define NIS_REJECT_WINDOW 3     /* the estimated cutoff window missed the cutoff */
 #define NIS_REJECT_CAPACITY 4   /* candidate list or cutoff bucket over capacity */
-#define NIS_REJECT_BUCKET 5     /* cutoff bucket membership did not match its histogram */
+#define NIS_REJECT_BUCKET 5     /* cutoff bucket membership did not match its histogram,
+                                   or the cutoff buckets hold more members than one
+                                   wave ranks */
 
 typedef struct nis_ctx nis_ctx;
 

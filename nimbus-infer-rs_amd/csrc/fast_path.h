@@ -1,15 +1,18 @@
 // fast_path.h — register-resident sampler for one row per 512-lane
 // workgroup (V <= 53245), the hot path of nis_sample_batch.
 //
-// HBM is touched once: every lane issues its 26 nontemporal 16-byte loads up
-// front (wave-contiguous layout: the row's float4 slots are split evenly
-// over the waves in whole 64-slot chunks, S per wave; chunk k / lane l of
-// wave w holds slot w*S + 64k + l), and
-// the row then lives in VGPRs (104 logits per lane; 8 waves per workgroup
-// leave each wave up to 256 VGPRs).  While the loads stream in, each wave
-// adds the masses e = 2^(x*c - R_w) of its elements to Z (c = log2(e)/T,
-// R_w a reference from the wave's own first chunk, so no workgroup barrier
-// is needed until the stream ends) and keeps the maximum of every float4.
+// HBM is touched once: every lane issues its (up to 26) nontemporal 16-byte
+// buffer loads up front.  The row's float4 slots are split evenly over the
+// eight waves in whole 64-slot chunks, S per wave (chunk k / lane l of wave
+// w holds slot w*S + 64k + l, so every wave owns a contiguous index range),
+// and the row then lives in VGPRs (up to 104 logits per lane; 8 waves per
+// workgroup leave each wave up to 256 VGPRs).  While the loads stream in,
+// each wave adds the masses e = 2^(x*c - R_w) of its elements to Z
+// (c = log2(e)/T, R_w a reference from the wave's own first chunk, so no
+// workgroup barrier is needed until the stream ends) and keeps the maximum
+// of every float4.  The waves' loads are served in wave order, so the first
+// half of the waves finishes its stream long before the second half; the
+// second half runs at a raised priority.
 //
 // The top-p cutoff of src/sampler.rs:118-160 is then found without sorting
 // the row.  The reference keeps sorted position pos iff
@@ -17,22 +20,28 @@
 // the kept set is a prefix of the sorted order and one threshold suffices:
 //
 // Sparse route (few kept tokens, the common case):
-//   1. a count histogram of a 4096-element sample (1/64-octave bins) gives a
-//      threshold x_lo with an estimated mass below it of at most
-//      (1 - p) * Z / 2; every float4 holding an element >= x_lo is appended to
-//      its wave's list (in index order) and compacted to single candidates;
-//   2. x_lo is proven safe: the largest element below it is removed iff
-//      G(candidates) - e(x_lo) > p * Z;
-//   3. a 1024-bucket histogram of the candidates (count, fixed-point mass,
-//      largest key) locates the bucket holding the cutoff: the lowest bucket
-//      whose largest element is kept; its members are ranked exactly;
-//   4. the inverse-CDF walk (sampler.rs:209-216) runs over the index-ordered
-//      candidate lists.
+//   1. in the stream, each wave's sample (the float4 maxima of its first 8
+//      chunks) gives a threshold th_w, and every float4 holding an element
+//      >= th_w is appended to the wave's list, in index order;
+//   2. at its stream end the wave compacts its list to single candidates and
+//      adds them to two histograms on an absolute grid (whole octaves of x*c
+//      and 1/64 octaves, so no wave needs the row max): count and the exact
+//      fixed-point sum of 2^frac(x c);
+//   3. after the one barrier the stream ends with, every wave on its own
+//      finds the cutoff: the deepest octave, then the deepest 1/64-octave
+//      bucket, passing a permissive test of sampler.rs:150 (the bucket's
+//      upper edge standing in for its largest element), so the cutoff lies
+//      in that bucket or the next non-empty one above; x_lo = max th_w is
+//      proven safe on the way;
+//   4. each wave scans its candidates for the members of those two buckets
+//      and the kept mass above them (per 64 index-ordered segments), wave 0
+//      ranks the members exactly, and the inverse-CDF walk (sampler.rs:
+//      209-216) goes waves -> segments -> the crossing segment's entries.
 // Dense route (most tokens kept, or top-p off): a value window around the
-// cutoff from the same sample, one register pass that adds the mass above
-// the window into per-(wave, chunk, lane) cells and lists the window
-// elements, a fine histogram of the window, an exact pass over the cutoff
-// bucket, and a walk waves -> chunks -> lanes -> elements.
+// cutoff from a sample, one register pass that adds the mass above the
+// window into per-(wave, chunk, lane) cells and lists the window elements,
+// a fine histogram of the window, an exact pass over the cutoff bucket, and
+// a walk waves -> chunks -> lanes -> elements.
 //
 // Every step that cannot prove its result (non-finite input, reference
 // overflow, a threshold or window that misses the cutoff, list or bucket
