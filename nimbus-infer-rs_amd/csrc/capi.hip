@@ -177,8 +177,21 @@ int nis_sample_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B,
     a.gen_off = d_gen_offsets;
     a.tokens = d_tokens;
     a.stats = d_stats;
-    hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
-                       ctx->stream, a);
+    // Rows whose nucleus is likely a small share of the vocabulary (top-p
+    // well below 1, no top-k, no penalty lists) go to the 1024-lane sparse
+    // kernel; everything else (greedy, top-p off or near 1, top-k, penalty,
+    // V outside its range) to the 512-lane register-resident / general one.
+    // Either kernel computes every row exactly; this only picks the faster.
+    const bool sparse = V >= 256 && V <= nis::kSMaxV && params->temperature > 0.0f &&
+                        params->top_p > 0.0f && params->top_p <= 0.98f &&
+                        (params->top_k == 0 || params->top_k >= (uint64_t)V) &&
+                        (params->repetition_penalty == 1.0f || d_gen_ids == nullptr);
+    if (sparse)
+        hipLaunchKernelGGL(nis::sample_rows_sparse_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
+                           ctx->stream, a);
+    else
+        hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
+                           ctx->stream, a);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "sample kernel launch");
 }
@@ -278,5 +291,13 @@ int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_par
 #undef NIS_TRY
     return NIS_OK;
 }
+
+#ifdef NIS_PHASE_TIMING
+// Profiling builds only: copy the sparse path's phase timestamps to the host.
+int nis_debug_sparse_ts(void* dst, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(nis::nis_sparse_ts), bytes, 0,
+                                    hipMemcpyDeviceToHost);
+}
+#endif
 
 }  // extern "C"

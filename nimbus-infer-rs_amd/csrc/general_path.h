@@ -207,7 +207,9 @@ __device__ __forceinline__ void topp_digit_select(const GeneralShared& sh, doubl
 // `reject` is recorded in the row's stats: why the fast path declined it.
 // SIMPLE: a row without a penalty whose masses have a finite f32 reference;
 // the SIMPLE form returns false, having written nothing, for any other row.
-template <bool SIMPLE>
+// TAG only separates the copies called from kernels of different workgroup
+// sizes, so each is compiled for its own register budget.
+template <bool SIMPLE, int TAG>
 __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, GeneralShared& sh,
                                            const uint32_t reject) {
     const int tid = threadIdx.x, l = lane_id(), w = wave_id();
@@ -883,11 +885,12 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
 
 // The general path: the SIMPLE form (f32 masses, no penalty lookups in the
 // passes) when it applies, else the general one.
+template <int TAG = 0>
 __device__ __forceinline__ void general_row(const RowArgs a, const int row, GeneralShared& sh,
                                             const uint32_t reject) {
-    if (!general_row_t<true>(a, row, sh, reject)) {
+    if (!general_row_t<true, TAG>(a, row, sh, reject)) {
         __syncthreads();
-        general_row_t<false>(a, row, sh, reject);
+        general_row_t<false, TAG>(a, row, sh, reject);
     }
 }
 

@@ -1,6 +1,6 @@
 // kernels.h — __global__ entry points of the sampler library (gfx950).
 #pragma once
-#include "fast_path.h"
+#include "sparse_path.h"
 
 namespace nis {
 
@@ -24,6 +24,28 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(RowArgs a) {
         __syncthreads();
     }
     general_row(a, row, sh.g, reject);
+}
+
+// Sparse top-p rows: one 1024-lane workgroup per row.  A row the sparse
+// path declines (or cannot take) runs the general path on the first 512
+// lanes; the other waves leave first, so the general path's barriers count
+// only its own eight waves.
+__global__ __launch_bounds__(kSB) void sample_rows_sparse_kernel(RowArgs a) {
+    __shared__ union {
+        GeneralShared g;
+        WideShared s;
+    } sh;
+    const int row = (int)blockIdx.x;
+    asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
+                 "s"(a.penalty), "s"(a.top_k), "s"(a.gen_ids), "s"(a.gen_off));
+    uint32_t reject = NIS_REJECT_SHAPE;
+    if (sparse_eligible(a, row)) {
+        reject = sparse_row(a, row, sh.s);
+        if (reject == NIS_REJECT_NONE) return;
+    }
+    if (threadIdx.x >= kBlock) return;
+    __syncthreads();
+    general_row<1>(a, row, sh.g, reject);
 }
 
 // General path only (used by tests to cross-check the two paths).

@@ -1,0 +1,829 @@
+// sparse_path.h — sparse top-p sampler: one row per 1024-lane workgroup
+// (16 wave64s, four per SIMD), for rows whose nucleus holds a small share of
+// the vocabulary (V <= 53245, 0 < top_p < 1, T > 0, no penalty, no top-k).
+//
+// Stream.  Every lane issues its 13 nontemporal 16-byte buffer loads up
+// front (chunk k / lane l of wave w holds float4 slot w*S + 64k + l, so each
+// wave owns a contiguous index range).  As the chunks land each wave adds the
+// masses 2^(x c - R_w) to Z in f64 (c = log2(e)/T, R_w an integer reference
+// from the wave's first chunk), keeps its max, and appends every float4
+// holding an element at or above its listing threshold thc_w to its LDS
+// list (index order, one ballot per chunk).  thc_w comes from the wave's
+// first four chunks: the lower edge of the 1/8-octave bins of x c holding at
+// most 44 of their 256 float4 maxima.  Four waves share a SIMD, so one
+// wave's dependent chain overlaps the others' and the stream ends close to
+// the last load.
+//
+// Cutoff (src/sampler.rs:118-160) without a sort.  The reference keeps
+// sorted position pos iff D(pos) = cum_excl(pos) - q(pos) <= p*Z; D is
+// non-decreasing in pos, so the kept set is a prefix of the stable order.
+// Each wave adds its candidates to its own histogram on an absolute grid of
+// 1/64 octave of x*c (bucket floor(64 * x*c), monotone in x), each bucket
+// holding its count and the exact sum of its members' masses in fixed point
+// relative to the bucket's octave; the search adds the sixteen histograms.
+// Private histograms need no cross-wave ordering before the stream-end
+// barrier: a barrier any earlier would wait until every wave has issued all
+// of its loads, which the CU allows only as the row's data arrives.  Every
+// element at or above x_lo = max_w thc_w is listed by its wave, so buckets
+// from blo = 16 x_lo up are complete.  With G(b) the
+// mass of the buckets above b and m_up(b) an upper bound of any mass in b,
+// b_p is the deepest non-empty bucket with G(b) - m_up(b) <= p Z:
+//   - every bucket below it fails, so its first element and everything after
+//     it in sorted order is removed;
+//   - every element of the buckets above b_p is kept (the last element y of
+//     the next non-empty bucket above has D(y) <= G(b_p) - 2 m(y) < p Z);
+//   - the cutoff therefore lies among b_p's members, which are ranked exactly
+//     (descending value, ascending index) against sampler.rs:150.
+// Elements below blo are removed once G(blo - 1) - m_up(blo - 1) > p Z.
+//
+// Masses in the tail are integers in units of 2^(R - 40) (R = ceil(M c)),
+// held in f64: every sum of them is exact and order-independent, so the
+// kept total, the per-wave and per-segment totals and the element walk
+// agree to the last bit and the inverse-CDF walk (sampler.rs:209-216)
+// always finds its crossing.
+//
+// Three barriers follow the stream: after the histograms (wave 0 then finds
+// b_p), after the search (every wave then lists its members of b_p and sums
+// its buckets above b_p), and after that scan (wave 0 ranks the members and
+// walks waves -> the chosen wave's list segments -> elements).  Any step that cannot
+// prove its result returns a reject code before the last barrier; the caller
+// then runs the general path on the row.
+#pragma once
+#include "fast_path.h"
+
+namespace nis {
+
+constexpr int kSB = 1024;                   // lanes per workgroup
+constexpr int kSW = kSB / 64;               // waves per workgroup
+constexpr int kSN = 13;                     // float4 chunks per lane
+constexpr int kSMaxV = kSB * 4 * kSN - 3;   // 53245
+constexpr int kSS = 4;                      // sample chunks per wave
+constexpr uint32_t kSTop = 44;              // sampled float4 maxima allowed above thc_w
+constexpr int kSE = 256;                    // listed float4s per wave
+constexpr int kSSeg = kSE / 64;             // list entries per lane segment (at most)
+constexpr int kSRes = 64;                   // histogram buckets per octave of x*c
+constexpr int kSLog = 6;                    // log2(kSRes)
+constexpr int kSHB = 32 * kSRes;            // bucket ring: 32 octaves
+constexpr int kSPer = kSHB / 64;            // search rounds (64 buckets each, at most)
+constexpr int kSMem = 64;                   // members of the cutoff bucket
+constexpr double kS40 = 1099511627776.0;    // 2^40
+
+// Optional per-wave phase timestamps (profiling builds only; compiled out
+// unless NIS_PHASE_TIMING is defined): slot 256 * row + 8 * wave + i for the
+// per-wave phases, 256 * row + 128 + j for the single-wave ones.
+#ifdef NIS_PHASE_TIMING
+__device__ unsigned long long nis_sparse_ts[2048 * 256];
+#define NIS_TSLOT(s)                                                                        \
+    do {                                                                                    \
+        if (lane_id() == 0 && blockIdx.x < 2048)                                            \
+            nis_sparse_ts[blockIdx.x * 256 + (s)] = wall_clock64();                         \
+    } while (0)
+#else
+#define NIS_TSLOT(s) \
+    do {             \
+    } while (0)
+#endif
+#define NIS_STS(i) NIS_TSLOT(8 * wave_id() + (i))
+#define NIS_STS1(j) NIS_TSLOT(128 + (j))
+
+// Stream-end record of one wave (32 bytes, written by its lane 0).
+struct alignas(16) SRec {
+    double z;     // sum of 2^(x c - R_w) over the wave's elements
+    float mx;     // wave max logit
+    float rw;     // R_w
+    float thc;    // listing threshold in units of x*c (-inf: the wave holds no data)
+    uint32_t n;   // float4s listed (may exceed kSE: overflow)
+    uint32_t nc;  // candidates in the compact list (may exceed kSC: overflow)
+    uint32_t pad;
+};
+// A member of the cutoff bucket.
+struct alignas(16) SMem {
+    float x;
+    uint32_t idx;  // row index
+    uint32_t fm;   // octave-relative fixed-point mass
+    uint32_t loc;  // owner wave << 16 | lane segment of its compact list
+};
+// Result of the cutoff search (written by wave 0 between barriers).
+struct alignas(16) SCut {
+    double gp;        // mass of the buckets above b_p (2^(R-40) units, an integer)
+    double pz;        // p * Z (2^(R-40) units)
+    double zr;        // Z (units of 2^R)
+    int32_t bp;       // b_p
+    uint32_t nabove;  // candidates above b_p
+    uint32_t reject;
+    uint32_t pad;
+};
+
+constexpr int kSC = 320;           // compact candidates per wave
+constexpr int kSCL = kSC / 64;     // ... per lane segment
+
+struct WideShared {
+    f4v ent[kSW][kSE];             // listed float4s, index order per wave
+    uint16_t epos[kSW][kSE];       //   their chunk * 64 + lane
+    float cx[kSW][kSC];            // compact candidates, index order: logit
+    uint32_t ci[kSW][kSC];         //   row index
+    uint32_t cf[kSW][kSC];         //   fm; a wave's sample histogram during its stream
+    unsigned long long hist[kSHB]; // [b & (kSHB-1)]: count << 48 | sum of fm, buckets >= blo
+    unsigned long long oct[32];    // the same per octave
+    double seg[kSW][64];           // kept mass above b_p per compact-list lane segment
+    double tw[kSW];                // per-wave kept mass (2^(R-40) units, integers)
+    SMem mem[kSMem];               // members of b_p
+    SRec rec[kSW];
+    SCut cut;
+    uint32_t nmem;
+};
+
+// Octave-relative fixed-point mass of a logit with t = x*c already rounded:
+// 2^(x c - floor(t)) * 2^24, one rounding in the fma (bounded by 2^25 + eps).
+__device__ __forceinline__ uint32_t s_fm(float x, float c, float t) {
+    return (uint32_t)(__builtin_amdgcn_exp2f(fmaf(x, c, -floorf(t))) * 16777216.0f);
+}
+// A sum of fm of octave o in 2^(R - 40) units, as an integer-valued f64:
+// exact for o >= R - 16, truncated below.  Sums of these stay below 2^53 and
+// are therefore exact and independent of their order.
+__device__ __forceinline__ double s_m40(unsigned long long fm, int o, int R) {
+    const int sh = o - R + 16;
+    const double v = ldexp((double)fm, sh);
+    return sh >= 0 ? v : floor(v);
+}
+// Bucket of t = x*c on the absolute grid: floor(64 t), monotone in x.
+__device__ __forceinline__ int s_bucket(float t) { return (int)floorf(t * (float)kSRes); }
+// Upper bound of the 2^(R - 40)-unit mass of any element in bucket b (its
+// upper edge, inflated for the roundings of x*c and exp2).
+__device__ __forceinline__ double s_mup(int b, int R) {
+    return ldexp((double)__builtin_amdgcn_exp2f((float)((b + 1) & (kSRes - 1)) * (1.0f / kSRes)) *
+                     1.0001,
+                 ((b + 1) >> kSLog) - R + 40);
+}
+// max of a float4 and of two floats without the canonicalising moves fmaxf
+// adds (NaN inputs are caught through Z later)
+__device__ __forceinline__ float s_max4(const f4v& v) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(v.x), "v"(v.y), "v"(v.z));
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(r), "v"(v.w));
+    return r;
+}
+__device__ __forceinline__ float s_max(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// u64 DPP scans (inclusive).  Whole wave, and within each 16-lane row.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ unsigned long long dpp0_u64(unsigned long long v) {
+    const uint32_t lo = dpp0<CTRL, ROW_MASK>((uint32_t)v), hi = dpp0<CTRL, ROW_MASK>((uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wscan_u64(unsigned long long v) {
+    v += dpp0_u64<0x111, 0xF>(v);
+    v += dpp0_u64<0x112, 0xF>(v);
+    v += dpp0_u64<0x114, 0xF>(v);
+    v += dpp0_u64<0x118, 0xF>(v);
+    v += dpp0_u64<0x142, 0xA>(v);
+    v += dpp0_u64<0x143, 0xC>(v);
+    return v;
+}
+__device__ __forceinline__ unsigned long long rscan_u64(unsigned long long v) {
+    v += dpp0_u64<0x111, 0xF>(v);
+    v += dpp0_u64<0x112, 0xF>(v);
+    v += dpp0_u64<0x114, 0xF>(v);
+    v += dpp0_u64<0x118, 0xF>(v);
+    return v;
+}
+__device__ __forceinline__ double rscan_f64(double v) {
+#define NIS_DPPR(C)                                                                    \
+    {                                                                                  \
+        const uint64_t b_ = (uint64_t)__double_as_longlong(v);                         \
+        const uint64_t lo_ = dpp0<C, 0xF>((uint32_t)b_), hi_ = dpp0<C, 0xF>((uint32_t)(b_ >> 32)); \
+        v += __longlong_as_double((long long)((hi_ << 32) | lo_));                     \
+    }
+    NIS_DPPR(0x111)
+    NIS_DPPR(0x112)
+    NIS_DPPR(0x114)
+    NIS_DPPR(0x118)
+#undef NIS_DPPR
+    return v;
+}
+__device__ __forceinline__ uint32_t rscan_u32(uint32_t v) {
+    v += dpp0<0x111>(v);
+    v += dpp0<0x112>(v);
+    v += dpp0<0x114>(v);
+    v += dpp0<0x118>(v);
+    return v;
+}
+__device__ __forceinline__ unsigned long long bcast_u64(unsigned long long v, int src) {
+    return ((unsigned long long)bcast_u32((uint32_t)(v >> 32), src) << 32) | bcast_u32((uint32_t)v, src);
+}
+// Reductions over lanes 0..15 (one DPP row), uniform result.
+__device__ __forceinline__ float r16_max(float v) {
+    v = fmaxf(v, dpp_ninf<0x111>(v));
+    v = fmaxf(v, dpp_ninf<0x112>(v));
+    v = fmaxf(v, dpp_ninf<0x114>(v));
+    v = fmaxf(v, dpp_ninf<0x118>(v));
+    return bcast_f32(v, 15);
+}
+__device__ __forceinline__ double r16_sum(double v) {
+#define NIS_DPPD16(C)                                                                  \
+    {                                                                                  \
+        const uint64_t b_ = (uint64_t)__double_as_longlong(v);                         \
+        const uint64_t lo_ = dpp0<C, 0xF>((uint32_t)b_), hi_ = dpp0<C, 0xF>((uint32_t)(b_ >> 32)); \
+        v += __longlong_as_double((long long)((hi_ << 32) | lo_));                     \
+    }
+    NIS_DPPD16(0x111)
+    NIS_DPPD16(0x112)
+    NIS_DPPD16(0x114)
+    NIS_DPPD16(0x118)
+#undef NIS_DPPD16
+    return bcast_f64(v, 15);
+}
+__device__ __forceinline__ uint32_t r16_maxu(uint32_t v) {
+    v = max(v, dpp0<0x111>(v));
+    v = max(v, dpp0<0x112>(v));
+    v = max(v, dpp0<0x114>(v));
+    v = max(v, dpp0<0x118>(v));
+    return bcast_u32(v, 15);
+}
+
+// One 64-bit LDS atomic add by the lanes of `mask` only.
+__device__ __forceinline__ void lds_add_u64_m(uint64_t mask, uint32_t a, uint64_t v) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_add_u64 %2, %3\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(v)
+        : "memory");
+}
+// Two 64-bit LDS atomic adds by the lanes of `mask` only.
+__device__ __forceinline__ void lds_add2_u64_m(uint64_t mask, uint32_t a, uint32_t b, uint64_t v) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_add_u64 %2, %4\n\t"
+        "ds_add_u64 %3, %4\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(b), "v"(v)
+        : "memory");
+}
+// One f64 LDS atomic add by the lanes of `mask` only.
+__device__ __forceinline__ void lds_add_f64_m(uint64_t mask, uint32_t a, double v) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_add_f64 %2, %3\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(v)
+        : "memory");
+}
+// Two f64 LDS atomic adds by the lanes of `mask` only.
+__device__ __forceinline__ void lds_add2_f64_m(uint64_t mask, uint32_t a, uint32_t b, double v) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_add_f64 %2, %4\n\t"
+        "ds_add_f64 %3, %4\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(b), "v"(v)
+        : "memory");
+}
+// One 16-byte LDS store by the lanes of `mask` only.
+__device__ __forceinline__ void lds_put_b128_m(uint64_t mask, uint32_t a, u4v v) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_write_b128 %2, %3\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(v)
+        : "memory");
+}
+// Two 4-byte LDS stores by the lanes of `mask` only.
+__device__ __forceinline__ void lds_put2_u32_m(uint64_t mask, uint32_t a, uint32_t va, uint32_t b,
+                                               uint32_t vb) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_write_b32 %2, %3\n\t"
+        "ds_write_b32 %4, %5\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(va), "v"(b), "v"(vb)
+        : "memory");
+}
+
+__device__ __forceinline__ bool sparse_eligible(const RowArgs a, int row) {
+    if (a.V < 256 || a.V > kSMaxV) return false;
+    if (!(a.temperature > 0.0f) || !(a.top_p > 0.0f) || !(a.top_p < 1.0f)) return false;
+    if (a.top_k > 0 && a.top_k < (uint64_t)a.V) return false;
+    if (a.penalty != 1.0f && a.gen_ids != nullptr && a.gen_off != nullptr &&
+        a.gen_off[row + 1] > a.gen_off[row])
+        return false;
+    return true;
+}
+
+// Returns NIS_REJECT_NONE when the row is done, else (uniformly across the
+// workgroup) why it must be recomputed; nothing has been written then.
+__device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, WideShared& sh) {
+    const int l = lane_id();
+    const int w = __builtin_amdgcn_readfirstlane(wave_id());
+    const int V = (int)a.V;
+    const gfp rowp = (gfp)(a.logits + (int64_t)row * a.ld);
+    const int mis = (int)(((uintptr_t)rowp >> 2) & 3);  // elements before the row in its 16 B block
+    const gf4p base = (gf4p)(rowp - mis);
+    const int f_lo = mis ? 1 : 0;          // first float4 slot lying fully inside the row
+    const int f_hi = (V + mis - 4) >> 2;   // last one
+    const int nsl = (V + mis + 3) >> 2;    // slots touching the row
+    const int S = 64 * ((nsl + 64 * kSW - 1) / (64 * kSW));  // slots per wave
+    const int Kw = min(max((nsl - w * S + 63) >> 6, 0), S >> 6);
+    const int slot0 = w * S + l;
+    NIS_STS(0);
+
+    // the (at most 3 + 3) elements of partial head / tail slots, by one
+    // vector load (lane i < 3: element i, lane 3 + i: element V - 6 + 3 + i)
+    const float hv = rowp[(l < 3) ? l : ((l < 6) ? V - 6 + l : 0)];
+    __builtin_amdgcn_sched_barrier(0);
+    // buffer descriptor over the whole slots [0, f_hi]; the partial head slot
+    // is redirected to f_lo, slots past f_hi read zeros (both fixed below)
+    const uint64_t bptr = (uint64_t)(uintptr_t)base;
+    const i4v rsrc = {(int32_t)(uint32_t)bptr, (int32_t)(uint32_t)((bptr >> 32) & 0xFFFFu),
+                      16 * (f_hi + 1), 0x00020000};
+    f4v xv[kSN];
+#pragma unroll
+    for (int k = 0; k < kSN; ++k) {
+        const int f = slot0 + k * 64;
+        const int off = (k < Kw) ? 16 * max(f, f_lo) : 0x7FFFFFF0;
+        xv[k] = nis_buffer_load_f4(rsrc, off, 0, 2);
+        __builtin_amdgcn_sched_barrier(0);  // chunk order = issue order
+    }
+    // the row's RNG state (sampler.rs:209 draws from it once), wave 0 only
+    typedef const __attribute__((address_space(1))) uint64_t* gu64p;
+    uint64_t rsv = 0;
+    if (w == 0) rsv = ((gu64p)(a.rng + 4 * (int64_t)row))[l & 3];
+
+    // The CU serves the waves' loads in wave order, so later waves get their
+    // data later and sit on the critical path: they run at a higher priority
+    // than the waves ahead of them (dropped to 0 at each wave's stream end).
+    __builtin_amdgcn_s_setprio(0);
+    if (w >= kSW / 4) __builtin_amdgcn_s_setprio(1);
+    if (w >= kSW / 2) __builtin_amdgcn_s_setprio(2);
+    if (w >= 3 * kSW / 4) __builtin_amdgcn_s_setprio(3);
+    // No workgroup barrier before the stream ends: each wave clears only its
+    // own sample histogram.
+    uint32_t* const whist = &sh.cf[w][0];
+    *reinterpret_cast<u4v*>(&whist[4 * l]) = u4v{0u, 0u, 0u, 0u};
+
+    const bool edge_wave = (w * S < f_lo) || (w * S + 64 * Kw - 1 > f_hi);
+    // (used only by edge waves; the broadcasts wait for the first load only)
+    const float h0 = bcast_f32(hv, 0), h1 = bcast_f32(hv, 1), h2 = bcast_f32(hv, 2);
+    const float t0 = bcast_f32(hv, 3), t1 = bcast_f32(hv, 4), t2 = bcast_f32(hv, 5);
+#define NIS_SFIX(k)                                                                           \
+    do {                                                                                      \
+        const int fb0 = w * S + (k) * 64;                                                     \
+        if (fb0 < f_lo || fb0 + 63 > f_hi)                                                    \
+            xv[k] = fix_slot(xv[k], slot0 + (k) * 64, f_lo, f_hi, mis, V, h0, h1, h2, t0, t1, t2); \
+    } while (0)
+
+    const double temp = fmax((double)a.temperature, 1e-6);  // sampler.rs:183
+    const float c = (float)(1.4426950408889634 / temp);     // log2(e) / T
+    const float p = a.top_p;
+    const f4v ninf4 = f4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+
+    // wave reference from the first chunk
+    if (Kw == 0) xv[0] = ninf4;
+    else if (edge_wave) NIS_SFIX(0);
+    const float m0 = wmax_f32(max4(xv[0]));
+    const float Rw = (m0 > -INFINITY && fabsf(m0 * c) < 1e30f) ? ceilf(m0 * c) : 0.0f;
+    const float RwH = Rw + 8.0f;  // top of the sample histogram (8 octaves of head room)
+    NIS_STS(5);
+
+    // ---- stream: masses, Z, max, listing --------------------------------
+    // cz / Rz are opaque copies of c / Rw, so the masses are not merged with
+    // identical expressions elsewhere and kept live.
+    double z = 0.0;
+    float mx = -INFINITY;
+    float cz = c, Rz = Rw;
+    asm volatile("" : "+v"(cz), "+v"(Rz));
+    const uint32_t ent0 = lds_addr(&sh.ent[w][0]), pos0 = lds_addr(&sh.epos[w][0]);
+    float thc = INFINITY;  // listing threshold (x*c units, a multiple of 1/8)
+    uint32_t nw = 0;
+    float mcs[kSS];
+#define NIS_SLIST(k, mc)                                                                    \
+    {                                                                                       \
+        const uint64_t mk = __ballot((mc) >= thc);                                          \
+        const uint32_t slot = min(nw + lane_rank(mk), (uint32_t)kSE - 1);                   \
+        lds_put_x4_u16(mk, ent0 + 16 * slot, xv[k], pos0 + 2 * slot, (uint32_t)((k) * 64 + l)); \
+        nw += (uint32_t)__popcll(mk);                                                       \
+    }
+#define NIS_SSTREAM(FIX)                                                                     \
+    _Pragma("unroll") for (int k = 0; k < kSN; ++k) {                                        \
+        if (k >= Kw && k >= kSS) continue;                                                   \
+        if (k > 0) {                                                                         \
+            if (k >= Kw) xv[k] = ninf4;                                                      \
+            else if (FIX) NIS_SFIX(k);                                                       \
+        }                                                                                    \
+        const f4v x = xv[k];                                                                 \
+        const float e0 = __builtin_amdgcn_exp2f(fmaf(x.x, cz, -Rz));                         \
+        const float e1 = __builtin_amdgcn_exp2f(fmaf(x.y, cz, -Rz));                         \
+        const float e2 = __builtin_amdgcn_exp2f(fmaf(x.z, cz, -Rz));                         \
+        const float e3 = __builtin_amdgcn_exp2f(fmaf(x.w, cz, -Rz));                         \
+        z += (double)((e0 + e1) + (e2 + e3));                                                \
+        const float m4 = s_max4(x);                                                          \
+        mx = s_max(mx, m4);                                                                  \
+        const float mc = m4 * c;                                                             \
+        if (k < kSS) {                                                                       \
+            mcs[k] = mc;                                                                     \
+            const float tb = floorf((RwH - mc) * 8.0f); /* -inf -> +inf */                   \
+            atomicAdd(&whist[(uint32_t)fminf(fmaxf(tb, 0.0f), 255.0f)], 1u);                 \
+        }                                                                                    \
+        if (k == kSS - 1) {                                                                  \
+            lds_wave_fence();                                                                \
+            const u4v hc = *reinterpret_cast<const u4v*>(&whist[4 * l]); /* bins 4l.. */     \
+            const uint32_t hs = hc.x + hc.y + hc.z + hc.w;                                   \
+            const uint32_t hi = wscan_u32(hs);                                               \
+            const uint32_t c0 = hi - hs + hc.x, c1 = c0 + hc.y, c2 = c1 + hc.z, c3 = c2 + hc.w; \
+            const uint32_t nok = (uint32_t)(c0 <= kSTop) + (uint32_t)(c1 <= kSTop) +         \
+                                 (uint32_t)(c2 <= kSTop) + (uint32_t)(c3 <= kSTop);          \
+            const int bw = (int)wsum_u32(nok) - 1; /* last bin whose cumulative count fits */ \
+            thc = (bw < 0 || Kw == 0) ? INFINITY : RwH - (float)(bw + 1) * 0.125f;           \
+            _Pragma("unroll") for (int j = 0; j < kSS; ++j) NIS_SLIST(j, mcs[j])             \
+            NIS_STS(6);                                                                      \
+        }                                                                                    \
+        if (k >= kSS) NIS_SLIST(k, mc)                                                       \
+    }
+    if (edge_wave) {
+        NIS_SSTREAM(true)
+    } else {
+        NIS_SSTREAM(false)
+    }
+#undef NIS_SSTREAM
+#undef NIS_SLIST
+#undef NIS_SFIX
+
+    // ---- stream end: compact this wave's candidates ----------------------
+    NIS_STS(1);
+    __builtin_amdgcn_s_setprio(0);
+    mx = wmax_f32(mx);
+    z = wsum_f64(z);
+    const uint32_t ne = min(nw, (uint32_t)kSE);
+    const int sg = (int)((ne + 63u) >> 6);  // lane l reads entries [l sg, l sg + sg)
+    // every element of the lane's entries at or above thc is a candidate;
+    // one scan of the per-lane counts places them all, in index order
+    // (branch-free: the stores of each position run under its ballot)
+    f4v ex[kSSeg];
+    uint32_t ep[kSSeg];
+    uint32_t cb = 0;  // bit 4i + q: element q of entry i
+#pragma unroll
+    for (int i = 0; i < kSSeg; ++i) {
+        ex[i] = ninf4;
+        ep[i] = 0u;
+        if (i < sg) {
+            const int j = l * sg + i;
+            const int jc = min(j, kSE - 1);
+            const f4v v = sh.ent[w][jc];
+            ep[i] = sh.epos[w][jc];
+            if (j < (int)ne) ex[i] = v;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cb |= (elem(ex[i], q) * c >= thc) ? (1u << (4 * i + q)) : 0u;
+    }
+    const uint32_t ccnt = (uint32_t)__popc(cb);
+    const uint32_t cincl = wscan_u32(ccnt);
+    const uint32_t nc = (uint32_t)__builtin_amdgcn_readlane((int)cincl, 63);
+    const uint32_t cbase = cincl - ccnt;
+    {
+        const uint32_t cx0 = lds_addr(&sh.cx[w][0]), ci0 = lds_addr(&sh.ci[w][0]);
+#pragma unroll
+        for (int i = 0; i < kSSeg; ++i) {
+            if (i < sg) {
+                const uint32_t idx0 = (uint32_t)(4 * (w * S + (int)ep[i]) - mis);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int bit = 4 * i + q;
+                    const uint32_t slot = min(cbase + (uint32_t)__popc(cb & ((1u << bit) - 1u)),
+                                              (uint32_t)kSC - 1);
+                    lds_put2_u32_m(__ballot((cb >> bit) & 1u), cx0 + 4 * slot,
+                                   __float_as_uint(elem(ex[i], q)), ci0 + 4 * slot, idx0 + (uint32_t)q);
+                }
+            }
+        }
+    }
+    {
+        const uint64_t zb = (uint64_t)__double_as_longlong(z);
+        const uint32_t ra = lds_addr(&sh.rec[w]);
+        lds_put_b128_m(1ull, ra, u4v{(uint32_t)zb, (uint32_t)(zb >> 32), __float_as_uint(mx),
+                                     __float_as_uint(Rw)});
+        lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, nc, 0u});
+    }
+    // this wave's slices of the shared histograms, its kept total (and the
+    // member count) are cleared before B1; they are added to only after it
+    *reinterpret_cast<u4v*>(&sh.hist[w * (kSHB / kSW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
+    if (l < 32 / kSW) sh.oct[w * (32 / kSW) + l] = 0ull;
+    if (w == 0 && l == 0) sh.nmem = 0u;
+    // the row's one draw (sampler.rs:209), made by wave 0 off the critical path
+    double u0 = 0.0;
+    uint64_t st[4];
+    if (w == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
+        u0 = rng_next_f64(st);
+    }
+
+    // ---- B1: records and compact lists complete ---------------------------
+    NIS_STS(2);
+    lds_barrier();
+    NIS_STS(3);
+    const int li = min(l, kSW - 1);
+    const bool rv = l < kSW;
+    const u4v ra = *reinterpret_cast<const u4v*>(&sh.rec[li]);
+    const u4v rb = *reinterpret_cast<const u4v*>(reinterpret_cast<const char*>(&sh.rec[li]) + 16);
+    const float rmx = __uint_as_float(ra.z), rthc = __uint_as_float(rb.x);
+    const uint32_t rn = rb.y, rnc = rb.z;
+    const float M = r16_max(rv ? rmx : -INFINITY);
+    const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
+    const int Ri = (int)R;
+    const float xlo = r16_max(rv ? rthc : -INFINITY);
+    const bool addok = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * c) < 1e6f) & (xlo < INFINITY) &
+                       (xlo <= M * c);
+    const int blo = addok ? (int)(xlo * (float)kSRes) : 0;  // xlo is a multiple of 1/8
+    const int bM = addok ? s_bucket(M * c) : 0;
+    const uint32_t ncl = min(nc, (uint32_t)kSC);
+    // this wave's candidates in the complete range into the shared histograms
+    // (their fm kept for later)
+    if (addok) {
+        const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
+#pragma unroll
+        for (int r0 = 0; r0 < kSC; r0 += 64) {
+            if (r0 < (int)ncl) {
+                const int j = r0 + l;
+                const bool v = j < (int)ncl;
+                const int jc = min(j, kSC - 1);
+                const float x = sh.cx[w][jc];
+                const float t = x * c;
+                const float o = floorf(t);
+                const uint32_t fm = s_fm(x, c, t);
+                const int b = s_bucket(t);
+                sh.cf[w][jc] = fm;
+                lds_add2_u64_m(__ballot(v & (b >= blo)), hist0 + 8 * ((uint32_t)b & (kSHB - 1)),
+                               oct0 + 8 * ((uint32_t)(int)o & 31u), (1ull << 48) | (uint64_t)fm);
+            }
+        }
+    }
+    // ---- B1.5: histograms complete ----------------------------------------
+    lds_barrier();
+
+    if (w == 0) {
+        // ---- the cutoff search (wave 0; the others wait at B2) ------------
+        __builtin_amdgcn_s_setprio(3);
+        const double rz = __longlong_as_double((long long)(((uint64_t)ra.y << 32) | ra.x));
+        const float rrw = __uint_as_float(ra.w);
+        const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
+        const float thmin = -r16_max((rv && rn > 0u) ? -rthc : -INFINITY);
+        const uint32_t nmax = r16_maxu(rv ? rn : 0u), ncmax = r16_maxu(rv ? rnc : 0u);
+        // a wave whose reference sits far below the row max may have overflowed
+        const bool range_ok = r16_max((rv && rmx > -INFINITY) ? fmaf(M, c, -rrw) : -INFINITY) <= 120.0f;
+        const double pz = (double)p * ZR * kS40;
+        NIS_STS1(8);
+        SCut cut;
+        cut.reject = NIS_REJECT_NONE;
+        cut.gp = 0.0;
+        cut.pz = pz;
+        cut.zr = ZR;
+        cut.bp = 0;
+        cut.nabove = 0u;
+        const int oM = bM >> kSLog, olo = blo >> kSLog;
+        if (!(M > -INFINITY) || !(M < INFINITY) || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok ||
+            !(fabsf(M * c) < 1e6f)) {
+            cut.reject = NIS_REJECT_NONFINITE;
+        } else if (!addok || nmax > (uint32_t)kSE || ncmax > (uint32_t)kSC ||
+                   !(bM - (int)(thmin * (float)kSRes) < kSHB - kSRes) || oM - olo > 30) {
+            cut.reject = NIS_REJECT_CAPACITY;
+        } else {
+            // level 1: octave oM - l for l <= oM - olo
+            const int o = oM - l;
+            const bool oin = l <= oM - olo;
+            const unsigned long long ov = oin ? sh.oct[(uint32_t)o & 31u] : 0ull;
+            const uint32_t on = (uint32_t)(ov >> 48);
+            const double om = s_m40(ov & 0xFFFFFFFFFFFFull, o, Ri);
+            const double oincl = wscan_f64(om);
+            const double Go = oincl - om;  // mass of the octaves above
+            const uint32_t ocincl = wscan_u32(on);
+            const uint32_t Co = ocincl - on;
+            const double gtot = bcast_f64(oincl, 63);  // everything >= blo
+            const uint64_t P = __ballot(oin & (on != 0u) & (Go - ldexp(1.0001, o + 1 - Ri + 40) <= pz));
+            const uint64_t NEo = __ballot(oin & (on != 0u));
+            // everything below blo is removed: G(blo - 1) - m_up(blo - 1) > p Z
+            const bool lo_ok = gtot - s_mup(blo - 1, Ri) > pz;
+            if (!P || !lo_ok) {
+                cut.reject = NIS_REJECT_WINDOW;
+            } else {
+                const int lp = 63 - __clzll((long long)P);  // deepest passing octave
+                const uint64_t up = NEo & ((1ull << lp) - 1ull);
+                const int la = up ? 63 - __clzll((long long)up) : -1;  // next non-empty above
+                NIS_STS1(9);
+                // level 2: lane l takes bucket 64 O + 63 - l of O = Op (then Oa)
+                int L = -1, bsel = 0;
+                double gsel = 0.0;
+                uint32_t csel = 0, nsel = 0;
+#pragma unroll
+                for (int pass2 = 0; pass2 < 2; ++pass2) {
+                    if (L < 0 && (pass2 == 0 || la >= 0)) {
+                        const int lo2 = pass2 == 0 ? lp : la;
+                        const int O = oM - lo2;
+                        const double GO = bcast_f64(Go, lo2);
+                        const uint32_t CO = bcast_u32(Co, lo2);
+                        const int b = kSRes * O + (kSRes - 1) - l;
+                        const bool bin = (b >= blo) & (b <= bM);
+                        const unsigned long long bv = bin ? sh.hist[(uint32_t)b & (kSHB - 1)] : 0ull;
+                        const uint32_t bn = (uint32_t)(bv >> 48);
+                        const double bm = s_m40(bv & 0xFFFFFFFFFFFFull, O, Ri);
+                        const double Gb = GO + (wscan_f64(bm) - bm);
+                        const uint32_t Cb = CO + (wscan_u32(bn) - bn);
+                        // Op: its deepest passing bucket; Oa (when Op has none):
+                        // its lowest non-empty bucket, which then passes
+                        const uint64_t sel = pass2 == 0
+                                                 ? __ballot((bn != 0u) & (Gb - s_mup(b, Ri) <= pz))
+                                                 : __ballot(bn != 0u);
+                        if (sel) {
+                            L = 63 - __clzll((long long)sel);
+                            bsel = b;
+                            gsel = Gb;
+                            csel = Cb;
+                            nsel = bn;
+                        }
+                    }
+                }
+                if (L < 0) {
+                    cut.reject = NIS_REJECT_WINDOW;
+                } else {
+                    cut.bp = (int32_t)bcast_u32((uint32_t)bsel, L);
+                    cut.gp = bcast_f64(gsel, L);
+                    cut.nabove = bcast_u32(csel, L);
+                    // the kept range stays within 16 octaves of R (exact fixed point)
+                    if ((cut.bp >> kSLog) < Ri - 16) cut.reject = NIS_REJECT_WINDOW;
+                    else if (bcast_u32(nsel, L) > (uint32_t)kSMem) cut.reject = NIS_REJECT_BUCKET;
+                }
+            }
+        }
+        NIS_STS1(10);
+        if (l == 0) sh.cut = cut;
+        __builtin_amdgcn_s_setprio(0);
+    }
+    // ---- B2: the cutoff bucket is known ------------------------------------
+    if (w == 0) NIS_STS1(0);
+    lds_barrier();
+    if (w == 0) NIS_STS1(1);
+    const SCut cut = sh.cut;
+    if (cut.reject != NIS_REJECT_NONE) return cut.reject;
+    const int bp = cut.bp;
+    {
+        // this wave's kept mass above b_p per lane segment of its compact
+        // list (lane l: candidates [4 l, 4 l + 4)), and its members of b_p
+        uint32_t vx[kSCL], vf[kSCL], vi[kSCL];
+#pragma unroll
+        for (int i = 0; i < kSCL; ++i) {
+            vx[i] = __float_as_uint(sh.cx[w][kSCL * l + i]);
+            vf[i] = sh.cf[w][kSCL * l + i];
+            vi[i] = sh.ci[w][kSCL * l + i];
+        }
+        double ssum = 0.0;
+        uint32_t mb = 0u;
+#pragma unroll
+        for (int i = 0; i < kSCL; ++i) {
+            const float x = __uint_as_float(vx[i]);
+            const float t = x * c;
+            const int b = s_bucket(t);
+            const bool v = kSCL * l + i < (int)ncl;
+            ssum += (v & (b > bp)) ? s_m40(vf[i], (int)floorf(t), Ri) : 0.0;
+            mb |= (v & (b == bp)) ? (1u << i) : 0u;
+        }
+        sh.seg[w][l] = ssum;
+        const double tsum = wsum_f64(ssum);
+        const uint32_t mcnt = (uint32_t)__popc(mb);
+        const uint32_t mincl = wscan_u32(mcnt);
+        const uint32_t mtot = (uint32_t)__builtin_amdgcn_readlane((int)mincl, 63);
+        if (mtot) {
+            uint32_t base = 0u;
+            if (l == 0) base = atomicAdd(&sh.nmem, mtot);
+            base = bcast_u32(base, 0) + mincl - mcnt;
+            const uint32_t mem0 = lds_addr(&sh.mem[0]);
+#pragma unroll
+            for (int i = 0; i < kSCL; ++i) {
+                const uint32_t slot = min(base + (uint32_t)__popc(mb & ((1u << i) - 1u)), (uint32_t)kSMem - 1);
+                lds_put_b128_m(__ballot((mb >> i) & 1u), mem0 + 16 * slot,
+                               u4v{vx[i], vi[i], vf[i], ((uint32_t)w << 16) | (uint32_t)l});
+            }
+        }
+        if (l == 0) sh.tw[w] = tsum;
+    }
+    // ---- B3: per-wave sums and members listed ------------------------------
+    if (w == 1) NIS_STS1(2);
+    lds_barrier();
+    if (w != 0) return NIS_REJECT_NONE;
+    NIS_STS1(3);
+    __builtin_amdgcn_s_setprio(3);
+
+    // ---- wave 0: rank the members, then the walk -----------------------------
+    const double pz = cut.pz, gp = cut.gp;
+    const int n = (int)min(sh.nmem, (uint32_t)kSMem);
+    const bool valid = l < n;
+    const u4v mr = *reinterpret_cast<const u4v*>(&sh.mem[min(l, kSMem - 1)]);
+    const float xm = __uint_as_float(mr.x);
+    const uint32_t im = mr.y;
+    const float tm = xm * c;
+    const double em = valid ? s_m40(mr.z, (int)floorf(tm), Ri) : 0.0;
+    // stable descending order of sampler.rs:140: value, then index
+    const unsigned long long Km = valid ? (((unsigned long long)key32(xm) << 32) | (uint32_t)~im) : 0ull;
+    NIS_STS1(11);
+    double pre = 0.0;
+#pragma unroll 4
+    for (int j = 0; j < n; ++j) {
+        const unsigned long long Kj = bcast_u64(Km, j);
+        const double ej = bcast_f64(em, j);
+        pre += (Kj > Km) ? ej : 0.0;
+    }
+    NIS_STS1(12);
+    const bool kept = valid & (gp + pre - em <= pz);  // sampler.rs:150
+    const uint64_t keptm = __ballot(kept);
+    const uint32_t nkept = (uint32_t)__popcll(keptm);
+    // the last kept member (the smallest key); elements of b_p at or above it are kept
+    unsigned long long Kcut = kept ? Km : ~0ull;
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1) {
+        const unsigned long long y = ((unsigned long long)(uint32_t)__shfl_xor((int)(uint32_t)(Kcut >> 32), o2) << 32) |
+                                     (uint32_t)__shfl_xor((int)(uint32_t)Kcut, o2);
+        Kcut = y < Kcut ? y : Kcut;
+    }
+    // the kept members join their wave's and their segment's kept mass
+    {
+        const int mw = min((int)(mr.w >> 16), kSW - 1), ms = (int)(mr.w & 63u);
+        lds_add2_f64_m(keptm, lds_addr(&sh.tw[mw]), lds_addr(&sh.seg[mw][ms]), em);
+    }
+    lds_wave_fence();
+    const double T = rv ? sh.tw[li] : 0.0;
+    const double Tincl = wscan_f64(T);
+    const double zk = bcast_f64(Tincl, 63);
+    const double u = u0;
+    const double r = u * zk;
+    const uint64_t hw = __ballot(rv & (T > 0.0) & (Tincl >= r));
+    const int ws = hw ? (__ffsll((long long)hw) - 1) : 0;
+    const double runw = bcast_f64(Tincl - T, ws);
+    NIS_STS1(4);
+    // the chosen wave's list segments
+    const double Sl = sh.seg[ws][l];
+    NIS_STS1(5);
+    const double Sincl = wscan_f64(Sl);
+    const uint64_t hs = __ballot((Sl > 0.0) & (runw + Sincl >= r));
+    const int ls = hs ? (__ffsll((long long)hs) - 1) : 0;
+    const double runl = bcast_f64(runw + Sincl - Sl, ls);
+    // that segment's candidates, one per lane
+    const uint32_t ncs = min(bcast_u32(rnc, ws), (uint32_t)kSC);
+    const int je = kSCL * ls + l;
+    const int jec = min(je, kSC - 1);
+    const float xe = sh.cx[ws][jec];
+    const uint32_t fme = sh.cf[ws][jec];
+    const uint32_t ide = sh.ci[ws][jec];
+    const float te = xe * c;
+    const int be = s_bucket(te);
+    const unsigned long long Ke = ((unsigned long long)key32(xe) << 32) | (uint32_t)~ide;
+    const bool kje = (l < kSCL) & (je < (int)ncs) & ((be > bp) | ((be == bp) & (Ke >= Kcut)));
+    const double ee = kje ? s_m40(fme, (int)floorf(te), Ri) : 0.0;
+    NIS_STS1(6);
+    const double pe_incl = rscan_f64(ee);
+    const uint64_t he = __ballot(kje & (runl + pe_incl >= r));
+    const int le = he ? (__ffsll((long long)he) - 1) : 0;
+    if (l == le) {
+        uint32_t tok = ide;
+        double prob = ee / zk;
+        if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
+            tok = 0u;
+            prob = 0.0;
+        }
+        // 2^(R - M c): units of 2^R -> units of the max element's mass
+        const double rho = (double)__builtin_amdgcn_exp2f(-fmaf(M, c, -R));
+        write_row_result(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zk / kS40 * rho,
+                         cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
+    }
+    NIS_STS1(7);
+    if (l == 0) {
+        uint64_t* sp = a.rng + 4 * (int64_t)row;
+        sp[0] = st[0];
+        sp[1] = st[1];
+        sp[2] = st[2];
+        sp[3] = st[3];
+    }
+    return NIS_REJECT_NONE;
+}
+
+}  // namespace nis
