@@ -3,7 +3,7 @@
 // the vocabulary (V <= 53245, 0 < top_p < 1, T > 0, no penalty, no top-k).
 //
 // Stream.  Every lane issues its 13 nontemporal 16-byte buffer loads up
-// front (chunk k / lane l of wave w holds float4 slot w*S + 64k + l, so each
+// front (chunk k / lane l of wave w holds float4 slot base_w + 64k + l, so each
 // wave owns a contiguous index range).  As the chunks land each wave adds the
 // masses 2^(x c - R_w) to Z in f64 (c = log2(e)/T, R_w an integer reference
 // from the wave's first chunk), keeps its max, and appends every float4
@@ -55,8 +55,12 @@ namespace nis {
 
 constexpr int kSB = 1024;                   // lanes per workgroup
 constexpr int kSW = kSB / 64;               // waves per workgroup
-constexpr int kSN = 13;                     // float4 chunks per lane
-constexpr int kSMaxV = kSB * 4 * kSN - 3;   // 53245
+constexpr int kSN = 13;                     // float4 chunks per lane (at most)
+constexpr int kSMaxV = kSB * 4 * 13 - 3;    // 53245: 208 chunks of 64 float4 slots
+#ifndef NIS_SD
+#define NIS_SD 3
+#endif
+constexpr int kSD = NIS_SD;                 // loads in flight per lane ahead of the one in use
 constexpr int kSS = 4;                      // sample chunks per wave
 constexpr uint32_t kSTop = 44;              // sampled float4 maxima allowed above thc_w
 constexpr int kSE = 256;                    // listed float4s per wave
@@ -111,7 +115,9 @@ struct alignas(16) SCut {
     int32_t bp;       // b_p
     uint32_t nabove;  // candidates above b_p
     uint32_t reject;
-    uint32_t pad;
+    float M;          // row max logit
+    float R;          // ceil(M c)
+    uint32_t pad[3];
 };
 
 constexpr int kSC = 320;           // compact candidates per wave
@@ -130,7 +136,17 @@ struct WideShared {
     SMem mem[kSMem];               // members of b_p
     SRec rec[kSW];
     SCut cut;
+    uint64_t rng[4];               // the row's RNG state after its one draw
+    double u0;                     // the draw
     uint32_t nmem;
+    uint32_t cnt1;                 // waves done with their candidates
+    uint32_t cnt2;                 // waves done with their kept sums
+    // the waves' records reduced as they arrive (order-preserving keys)
+    uint32_t kmax;                 // max logit
+    uint32_t kxlo;                 // max listing threshold
+    uint32_t kthmin;               // min listing threshold of a wave with entries
+    uint32_t krwmin;               // min R_w of a wave with data
+    uint32_t nmax, ncmax;          // largest list / candidate counts
 };
 
 // Octave-relative fixed-point mass of a logit with t = x*c already rounded:
@@ -344,9 +360,12 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const int f_lo = mis ? 1 : 0;          // first float4 slot lying fully inside the row
     const int f_hi = (V + mis - 4) >> 2;   // last one
     const int nsl = (V + mis + 3) >> 2;    // slots touching the row
-    const int S = 64 * ((nsl + 64 * kSW - 1) / (64 * kSW));  // slots per wave
-    const int Kw = min(max((nsl - w * S + 63) >> 6, 0), S >> 6);
-    const int slot0 = w * S + l;
+    // wave w owns slots [wbase, wbase + 64 Kw): the same number of chunks
+    // for every wave but the last ones
+    const int cpw = (((nsl + 63) >> 6) + kSW - 1) / kSW;  // chunks per wave
+    const int wbase = 64 * cpw * w;
+    const int Kw = min(max((nsl - wbase + 63) >> 6, 0), cpw);
+    const int slot0 = wbase + l;
     NIS_STS(0);
 
     // the (at most 3 + 3) elements of partial head / tail slots, by one
@@ -359,11 +378,35 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const i4v rsrc = {(int32_t)(uint32_t)bptr, (int32_t)(uint32_t)((bptr >> 32) & 0xFFFFu),
                       16 * (f_hi + 1), 0x00020000};
     f4v xv[kSN];
+    // Chunk 0 first; then the LDS state every wave shares (its histogram
+    // slice and the counters) is cleared and one barrier orders that before
+    // any use.  The barrier sits before the other loads: a barrier after a
+    // wave's whole batch of loads would wait until the CU has issued them
+    // all, which it does only as the row's data arrives.
+    xv[0] = nis_buffer_load_f4(rsrc, (Kw > 0) ? 16 * max(slot0, f_lo) : 0x7FFFFFF0, 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    *reinterpret_cast<u4v*>(&sh.hist[w * (kSHB / kSW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
+    if (l < 32 / kSW) sh.oct[w * (32 / kSW) + l] = 0ull;
+    if (w == 0 && l == 0) {
+        sh.nmem = 0u;
+        sh.cnt1 = 0u;
+        sh.cnt2 = 0u;
+        sh.kmax = 0u;
+        sh.kxlo = 0u;
+        sh.kthmin = 0xFFFFFFFFu;
+        sh.krwmin = 0xFFFFFFFFu;
+        sh.nmax = 0u;
+        sh.ncmax = 0u;
+    }
+    lds_barrier();
+#define NIS_SLOAD(k)                                                                          \
+    do {                                                                                      \
+        const int f_ = slot0 + (k) * 64;                                                      \
+        xv[k] = nis_buffer_load_f4(rsrc, ((k) < Kw) ? 16 * max(f_, f_lo) : 0x7FFFFFF0, 0, 2); \
+    } while (0)
 #pragma unroll
-    for (int k = 0; k < kSN; ++k) {
-        const int f = slot0 + k * 64;
-        const int off = (k < Kw) ? 16 * max(f, f_lo) : 0x7FFFFFF0;
-        xv[k] = nis_buffer_load_f4(rsrc, off, 0, 2);
+    for (int k = 1; k < kSD && k < kSN; ++k) {
+        NIS_SLOAD(k);
         __builtin_amdgcn_sched_barrier(0);  // chunk order = issue order
     }
     // the row's RNG state (sampler.rs:209 draws from it once), wave 0 only
@@ -378,18 +421,17 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     if (w >= kSW / 4) __builtin_amdgcn_s_setprio(1);
     if (w >= kSW / 2) __builtin_amdgcn_s_setprio(2);
     if (w >= 3 * kSW / 4) __builtin_amdgcn_s_setprio(3);
-    // No workgroup barrier before the stream ends: each wave clears only its
-    // own sample histogram.
+    // each wave's sample histogram is its own
     uint32_t* const whist = &sh.cf[w][0];
     *reinterpret_cast<u4v*>(&whist[4 * l]) = u4v{0u, 0u, 0u, 0u};
 
-    const bool edge_wave = (w * S < f_lo) || (w * S + 64 * Kw - 1 > f_hi);
+    const bool edge_wave = (wbase < f_lo) || (wbase + 64 * Kw - 1 > f_hi);
     // (used only by edge waves; the broadcasts wait for the first load only)
     const float h0 = bcast_f32(hv, 0), h1 = bcast_f32(hv, 1), h2 = bcast_f32(hv, 2);
     const float t0 = bcast_f32(hv, 3), t1 = bcast_f32(hv, 4), t2 = bcast_f32(hv, 5);
 #define NIS_SFIX(k)                                                                           \
     do {                                                                                      \
-        const int fb0 = w * S + (k) * 64;                                                     \
+        const int fb0 = wbase + (k) * 64;                                                     \
         if (fb0 < f_lo || fb0 + 63 > f_hi)                                                    \
             xv[k] = fix_slot(xv[k], slot0 + (k) * 64, f_lo, f_hi, mis, V, h0, h1, h2, t0, t1, t2); \
     } while (0)
@@ -415,18 +457,21 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     float cz = c, Rz = Rw;
     asm volatile("" : "+v"(cz), "+v"(Rz));
     const uint32_t ent0 = lds_addr(&sh.ent[w][0]), pos0 = lds_addr(&sh.epos[w][0]);
-    float thc = INFINITY;  // listing threshold (x*c units, a multiple of 1/8)
+    float thc = INFINITY;  // this wave's sample threshold (x*c units, a multiple of 1/8)
+    float thl = INFINITY;  // its listing threshold: thc raised to the waves' running max
     uint32_t nw = 0;
     float mcs[kSS];
 #define NIS_SLIST(k, mc)                                                                    \
     {                                                                                       \
-        const uint64_t mk = __ballot((mc) >= thc);                                          \
+        const uint64_t mk = __ballot((mc) >= thl);                                          \
         const uint32_t slot = min(nw + lane_rank(mk), (uint32_t)kSE - 1);                   \
         lds_put_x4_u16(mk, ent0 + 16 * slot, xv[k], pos0 + 2 * slot, (uint32_t)((k) * 64 + l)); \
         nw += (uint32_t)__popcll(mk);                                                       \
     }
 #define NIS_SSTREAM(FIX)                                                                     \
     _Pragma("unroll") for (int k = 0; k < kSN; ++k) {                                        \
+        if (k + kSD < kSN) NIS_SLOAD(k + kSD);                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
         if (k >= Kw && k >= kSS) continue;                                                   \
         if (k > 0) {                                                                         \
             if (k >= Kw) xv[k] = ninf4;                                                      \
@@ -456,6 +501,11 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                                  (uint32_t)(c2 <= kSTop) + (uint32_t)(c3 <= kSTop);          \
             const int bw = (int)wsum_u32(nok) - 1; /* last bin whose cumulative count fits */ \
             thc = (bw < 0 || Kw == 0) ? INFINITY : RwH - (float)(bw + 1) * 0.125f;           \
+            /* x_lo = max_w thc_w bounds the complete range, so nothing below the */         \
+            /* running max of the thresholds published so far is ever needed */            \
+            if (Kw > 0 && l == 0) atomicMax(&sh.kxlo, key32(thc));                           \
+            lds_wave_fence();                                                                \
+            thl = fmaxf(thc, unkey32(sh.kxlo));                                              \
             _Pragma("unroll") for (int j = 0; j < kSS; ++j) NIS_SLIST(j, mcs[j])             \
             NIS_STS(6);                                                                      \
         }                                                                                    \
@@ -468,13 +518,21 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     }
 #undef NIS_SSTREAM
 #undef NIS_SLIST
+#undef NIS_SLOAD
 #undef NIS_SFIX
 
     // ---- stream end: compact this wave's candidates ----------------------
     NIS_STS(1);
+#ifdef NIS_EXPERIMENT_STREAM_ONLY
+    lds_barrier();
+    NIS_STS(2);
+    return NIS_REJECT_CAPACITY;
+#endif
     __builtin_amdgcn_s_setprio(0);
     mx = wmax_f32(mx);
     z = wsum_f64(z);
+    NIS_STS(4);
+    thl = fmaxf(thl, unkey32(sh.kxlo));  // the thresholds published meanwhile
     const uint32_t ne = min(nw, (uint32_t)kSE);
     const int sg = (int)((ne + 63u) >> 6);  // lane l reads entries [l sg, l sg + sg)
     // every element of the lane's entries at or above thc is a candidate;
@@ -495,29 +553,35 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             if (j < (int)ne) ex[i] = v;
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) cb |= (elem(ex[i], q) * c >= thc) ? (1u << (4 * i + q)) : 0u;
+        for (int q = 0; q < 4; ++q) cb |= (elem(ex[i], q) * c >= thl) ? (1u << (4 * i + q)) : 0u;
     }
     const uint32_t ccnt = (uint32_t)__popc(cb);
     const uint32_t cincl = wscan_u32(ccnt);
     const uint32_t nc = (uint32_t)__builtin_amdgcn_readlane((int)cincl, 63);
     const uint32_t cbase = cincl - ccnt;
     {
+        // non-candidates store to the lane's own slot of the (now dead) entry
+        // list, so every position is a plain store: no branches, no exec masks
+        typedef __attribute__((address_space(3))) uint32_t* lu32p;
         const uint32_t cx0 = lds_addr(&sh.cx[w][0]), ci0 = lds_addr(&sh.ci[w][0]);
+        const uint32_t junk = lds_addr(&sh.ent[w][l]);
 #pragma unroll
         for (int i = 0; i < kSSeg; ++i) {
             if (i < sg) {
-                const uint32_t idx0 = (uint32_t)(4 * (w * S + (int)ep[i]) - mis);
+                const uint32_t idx0 = (uint32_t)(4 * (wbase + (int)ep[i]) - mis);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int bit = 4 * i + q;
+                    const bool cq = (cb >> bit) & 1u;
                     const uint32_t slot = min(cbase + (uint32_t)__popc(cb & ((1u << bit) - 1u)),
                                               (uint32_t)kSC - 1);
-                    lds_put2_u32_m(__ballot((cb >> bit) & 1u), cx0 + 4 * slot,
-                                   __float_as_uint(elem(ex[i], q)), ci0 + 4 * slot, idx0 + (uint32_t)q);
+                    *(lu32p)(size_t)(cq ? cx0 + 4 * slot : junk) = __float_as_uint(elem(ex[i], q));
+                    *(lu32p)(size_t)(cq ? ci0 + 4 * slot : junk + 4) = idx0 + (uint32_t)q;
                 }
             }
         }
     }
+    NIS_STS(7);
     {
         const uint64_t zb = (uint64_t)__double_as_longlong(z);
         const uint32_t ra = lds_addr(&sh.rec[w]);
@@ -525,74 +589,83 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                                      __float_as_uint(Rw)});
         lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, nc, 0u});
     }
-    // this wave's slices of the shared histograms, its kept total (and the
-    // member count) are cleared before B1; they are added to only after it
-    *reinterpret_cast<u4v*>(&sh.hist[w * (kSHB / kSW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
-    if (l < 32 / kSW) sh.oct[w * (32 / kSW) + l] = 0ull;
-    if (w == 0 && l == 0) sh.nmem = 0u;
+    // this wave's candidates into the shared histograms (all of them: the
+    // search reads only the buckets at or above blo, which are complete);
+    // lane l takes candidates [5 l, 5 l + 5) and keeps their logit, index,
+    // fm, bucket and mass in its own frame (2^(R_w - 40) units; exact
+    // integers wherever they are summed later, since R_w <= R and kept
+    // elements lie within 16 octaves of R) for the steps after the search
+    const uint32_t ncl = min(nc, (uint32_t)kSC);
+    uint32_t vx[kSCL], vf[kSCL], vi[kSCL];
+    int vb[kSCL];
+    double vm[kSCL];
+    {
+        const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
+#pragma unroll
+        for (int i = 0; i < kSCL; ++i) {
+            const int j = kSCL * l + i;
+            const bool v = j < (int)ncl;
+            vx[i] = __float_as_uint(sh.cx[w][j]);
+            vi[i] = sh.ci[w][j];
+            const float x = __uint_as_float(vx[i]);
+            const float t = x * c;
+            const float o = floorf(t);
+            vf[i] = s_fm(x, c, t);
+            vb[i] = s_bucket(t);
+            vm[i] = ldexp((double)vf[i], (int)o - (int)Rw + 16);
+            if (v) sh.cf[w][j] = vf[i];
+            lds_add2_u64_m(__ballot(v), hist0 + 8 * ((uint32_t)vb[i] & (kSHB - 1)),
+                           oct0 + 8 * ((uint32_t)(int)o & 31u), (1ull << 48) | (uint64_t)vf[i]);
+        }
+    }
     // the row's one draw (sampler.rs:209), made by wave 0 off the critical path
-    double u0 = 0.0;
-    uint64_t st[4];
     if (w == 0) {
+        uint64_t st[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
-        u0 = rng_next_f64(st);
-    }
-
-    // ---- B1: records and compact lists complete ---------------------------
-    NIS_STS(2);
-    lds_barrier();
-    NIS_STS(3);
-    const int li = min(l, kSW - 1);
-    const bool rv = l < kSW;
-    const u4v ra = *reinterpret_cast<const u4v*>(&sh.rec[li]);
-    const u4v rb = *reinterpret_cast<const u4v*>(reinterpret_cast<const char*>(&sh.rec[li]) + 16);
-    const float rmx = __uint_as_float(ra.z), rthc = __uint_as_float(rb.x);
-    const uint32_t rn = rb.y, rnc = rb.z;
-    const float M = r16_max(rv ? rmx : -INFINITY);
-    const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
-    const int Ri = (int)R;
-    const float xlo = r16_max(rv ? rthc : -INFINITY);
-    const bool addok = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * c) < 1e6f) & (xlo < INFINITY) &
-                       (xlo <= M * c);
-    const int blo = addok ? (int)(xlo * (float)kSRes) : 0;  // xlo is a multiple of 1/8
-    const int bM = addok ? s_bucket(M * c) : 0;
-    const uint32_t ncl = min(nc, (uint32_t)kSC);
-    // this wave's candidates in the complete range into the shared histograms
-    // (their fm kept for later)
-    if (addok) {
-        const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
-#pragma unroll
-        for (int r0 = 0; r0 < kSC; r0 += 64) {
-            if (r0 < (int)ncl) {
-                const int j = r0 + l;
-                const bool v = j < (int)ncl;
-                const int jc = min(j, kSC - 1);
-                const float x = sh.cx[w][jc];
-                const float t = x * c;
-                const float o = floorf(t);
-                const uint32_t fm = s_fm(x, c, t);
-                const int b = s_bucket(t);
-                sh.cf[w][jc] = fm;
-                lds_add2_u64_m(__ballot(v & (b >= blo)), hist0 + 8 * ((uint32_t)b & (kSHB - 1)),
-                               oct0 + 8 * ((uint32_t)(int)o & 31u), (1ull << 48) | (uint64_t)fm);
-            }
+        const double u0 = rng_next_f64(st);
+        if (l == 0) {
+            sh.u0 = u0;
+            sh.rng[0] = st[0];
+            sh.rng[1] = st[1];
+            sh.rng[2] = st[2];
+            sh.rng[3] = st[3];
         }
     }
-    // ---- B1.5: histograms complete ----------------------------------------
-    lds_barrier();
+    if (l == 0) {
+        const float thr = Kw > 0 ? thc : -INFINITY;
+        atomicMax(&sh.kmax, key32(mx));
+        if (nw > 0u) atomicMin(&sh.kthmin, key32(thr));
+        if (mx > -INFINITY) atomicMin(&sh.krwmin, key32(Rw));
+        atomicMax(&sh.nmax, nw);
+        atomicMax(&sh.ncmax, nc);
+    }
+    NIS_STS(2);
 
-    if (w == 0) {
-        // ---- the cutoff search (wave 0; the others wait at B2) ------------
+    // ---- the last wave to finish its candidates runs the cutoff search ----
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    uint32_t done1 = 0u;
+    if (l == 0) done1 = atomicAdd(&sh.cnt1, 1u);
+    done1 = bcast_u32(done1, 0);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    const int li = min(l, kSW - 1);
+    const bool rv = l < kSW;
+    if (done1 == (uint32_t)(kSW - 1)) {
+        NIS_STS(3);
         __builtin_amdgcn_s_setprio(3);
-        const double rz = __longlong_as_double((long long)(((uint64_t)ra.y << 32) | ra.x));
+        const u4v ra = *reinterpret_cast<const u4v*>(&sh.rec[li]);
         const float rrw = __uint_as_float(ra.w);
+        const double rz = __longlong_as_double((long long)(((uint64_t)ra.y << 32) | ra.x));
+        const float M = unkey32(sh.kmax);
+        const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
+        const int Ri = (int)R;
+        const float xlo = unkey32(sh.kxlo);
+        const float thmin = unkey32(sh.kthmin);
+        const uint32_t nmax = sh.nmax, ncmax = sh.ncmax;
         const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
-        const float thmin = -r16_max((rv && rn > 0u) ? -rthc : -INFINITY);
-        const uint32_t nmax = r16_maxu(rv ? rn : 0u), ncmax = r16_maxu(rv ? rnc : 0u);
         // a wave whose reference sits far below the row max may have overflowed
-        const bool range_ok = r16_max((rv && rmx > -INFINITY) ? fmaf(M, c, -rrw) : -INFINITY) <= 120.0f;
+        const bool range_ok = fmaf(M, c, -unkey32(sh.krwmin)) <= 120.0f;
         const double pz = (double)p * ZR * kS40;
         NIS_STS1(8);
         SCut cut;
@@ -602,18 +675,28 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         cut.zr = ZR;
         cut.bp = 0;
         cut.nabove = 0u;
+        cut.M = M;
+        cut.R = R;
+        const bool fin = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * c) < 1e6f);
+        const int blo = (fin & (xlo < INFINITY)) ? (int)(xlo * (float)kSRes) : 0;  // xlo: a multiple of 1/8
+        const int bM = fin ? s_bucket(M * c) : 0;
         const int oM = bM >> kSLog, olo = blo >> kSLog;
-        if (!(M > -INFINITY) || !(M < INFINITY) || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok ||
-            !(fabsf(M * c) < 1e6f)) {
+        if (!fin || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok) {
             cut.reject = NIS_REJECT_NONFINITE;
-        } else if (!addok || nmax > (uint32_t)kSE || ncmax > (uint32_t)kSC ||
+        } else if (!(xlo < INFINITY) || !(xlo <= M * c) || nmax > (uint32_t)kSE || ncmax > (uint32_t)kSC ||
                    !(bM - (int)(thmin * (float)kSRes) < kSHB - kSRes) || oM - olo > 30) {
             cut.reject = NIS_REJECT_CAPACITY;
         } else {
+            // octave olo holds candidates below blo too: its complete part from
+            // its buckets at or above blo
+            const int bl = kSRes * olo + l;
+            const unsigned long long lv =
+                (bl >= blo && bl <= bM) ? sh.hist[(uint32_t)bl & (kSHB - 1)] : 0ull;
+            const unsigned long long lsum = bcast_u64(wscan_u64(lv), 63);
             // level 1: octave oM - l for l <= oM - olo
             const int o = oM - l;
             const bool oin = l <= oM - olo;
-            const unsigned long long ov = oin ? sh.oct[(uint32_t)o & 31u] : 0ull;
+            const unsigned long long ov = !oin ? 0ull : (o == olo ? lsum : sh.oct[(uint32_t)o & 31u]);
             const uint32_t on = (uint32_t)(ov >> 48);
             const double om = s_m40(ov & 0xFFFFFFFFFFFFull, o, Ri);
             const double oincl = wscan_f64(om);
@@ -677,36 +760,37 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             }
         }
         NIS_STS1(10);
+        NIS_STS1(0);
         if (l == 0) sh.cut = cut;
         __builtin_amdgcn_s_setprio(0);
     }
     // ---- B2: the cutoff bucket is known ------------------------------------
-    if (w == 0) NIS_STS1(0);
     lds_barrier();
     if (w == 0) NIS_STS1(1);
     const SCut cut = sh.cut;
     if (cut.reject != NIS_REJECT_NONE) return cut.reject;
     const int bp = cut.bp;
+    const float M = cut.M, R = cut.R;
+    const int Ri = (int)R;
     {
         // this wave's kept mass above b_p per lane segment of its compact
-        // list (lane l: candidates [4 l, 4 l + 4)), and its members of b_p
-        uint32_t vx[kSCL], vf[kSCL], vi[kSCL];
+        // list (lane l: candidates [5 l, 5 l + 5)), and its members of b_p
+        if (Rw > R) {  // (no finite reference in the first chunk)
 #pragma unroll
-        for (int i = 0; i < kSCL; ++i) {
-            vx[i] = __float_as_uint(sh.cx[w][kSCL * l + i]);
-            vf[i] = sh.cf[w][kSCL * l + i];
-            vi[i] = sh.ci[w][kSCL * l + i];
+            for (int i = 0; i < kSCL; ++i)
+                vm[i] = ldexp((double)vf[i], (int)floorf(__uint_as_float(vx[i]) * c) - Ri + 16);
+        } else {
+            const double scl = ldexp(1.0, (int)Rw - Ri);  // exact power of two
+#pragma unroll
+            for (int i = 0; i < kSCL; ++i) vm[i] *= scl;
         }
         double ssum = 0.0;
         uint32_t mb = 0u;
 #pragma unroll
         for (int i = 0; i < kSCL; ++i) {
-            const float x = __uint_as_float(vx[i]);
-            const float t = x * c;
-            const int b = s_bucket(t);
             const bool v = kSCL * l + i < (int)ncl;
-            ssum += (v & (b > bp)) ? s_m40(vf[i], (int)floorf(t), Ri) : 0.0;
-            mb |= (v & (b == bp)) ? (1u << i) : 0u;
+            ssum += (v & (vb[i] > bp)) ? vm[i] : 0.0;
+            mb |= (v & (vb[i] == bp)) ? (1u << i) : 0u;
         }
         sh.seg[w][l] = ssum;
         const double tsum = wsum_f64(ssum);
@@ -727,14 +811,17 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         }
         if (l == 0) sh.tw[w] = tsum;
     }
-    // ---- B3: per-wave sums and members listed ------------------------------
-    if (w == 1) NIS_STS1(2);
-    lds_barrier();
-    if (w != 0) return NIS_REJECT_NONE;
+    // ---- the last wave to finish its sums ranks the members and walks -------
+    NIS_STS(6);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    uint32_t done2 = 0u;
+    if (l == 0) done2 = atomicAdd(&sh.cnt2, 1u);
+    done2 = bcast_u32(done2, 0);
+    if (done2 != (uint32_t)(kSW - 1)) return NIS_REJECT_NONE;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     NIS_STS1(3);
     __builtin_amdgcn_s_setprio(3);
 
-    // ---- wave 0: rank the members, then the walk -----------------------------
     const double pz = cut.pz, gp = cut.gp;
     const int n = (int)min(sh.nmem, (uint32_t)kSMem);
     const bool valid = l < n;
@@ -759,11 +846,22 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const uint32_t nkept = (uint32_t)__popcll(keptm);
     // the last kept member (the smallest key); elements of b_p at or above it are kept
     unsigned long long Kcut = kept ? Km : ~0ull;
-#pragma unroll
-    for (int o2 = 32; o2 > 0; o2 >>= 1) {
-        const unsigned long long y = ((unsigned long long)(uint32_t)__shfl_xor((int)(uint32_t)(Kcut >> 32), o2) << 32) |
-                                     (uint32_t)__shfl_xor((int)(uint32_t)Kcut, o2);
-        Kcut = y < Kcut ? y : Kcut;
+    {
+#define NIS_MIN64(C, MSK)                                                                              \
+        {                                                                                              \
+            const uint32_t lo_ = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)Kcut, C, MSK, 0xF, false);         \
+            const uint32_t hi_ = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)(Kcut >> 32), C, MSK, 0xF, false); \
+            const unsigned long long y_ = ((unsigned long long)hi_ << 32) | lo_;                      \
+            Kcut = y_ < Kcut ? y_ : Kcut;                                                              \
+        }
+        NIS_MIN64(0x111, 0xF)
+        NIS_MIN64(0x112, 0xF)
+        NIS_MIN64(0x114, 0xF)
+        NIS_MIN64(0x118, 0xF)
+        NIS_MIN64(0x142, 0xA)
+        NIS_MIN64(0x143, 0xC)
+#undef NIS_MIN64
+        Kcut = bcast_u64(Kcut, 63);
     }
     // the kept members join their wave's and their segment's kept mass
     {
@@ -774,7 +872,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const double T = rv ? sh.tw[li] : 0.0;
     const double Tincl = wscan_f64(T);
     const double zk = bcast_f64(Tincl, 63);
-    const double u = u0;
+    const double u = sh.u0;
     const double r = u * zk;
     const uint64_t hw = __ballot(rv & (T > 0.0) & (Tincl >= r));
     const int ws = hw ? (__ffsll((long long)hw) - 1) : 0;
@@ -788,7 +886,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const int ls = hs ? (__ffsll((long long)hs) - 1) : 0;
     const double runl = bcast_f64(runw + Sincl - Sl, ls);
     // that segment's candidates, one per lane
-    const uint32_t ncs = min(bcast_u32(rnc, ws), (uint32_t)kSC);
+    const uint32_t ncs = min(sh.rec[ws].nc, (uint32_t)kSC);
     const int je = kSCL * ls + l;
     const int jec = min(je, kSC - 1);
     const float xe = sh.cx[ws][jec];
@@ -816,13 +914,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                          cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
     }
     NIS_STS1(7);
-    if (l == 0) {
-        uint64_t* sp = a.rng + 4 * (int64_t)row;
-        sp[0] = st[0];
-        sp[1] = st[1];
-        sp[2] = st[2];
-        sp[3] = st[3];
-    }
+    if (l < 4) a.rng[4 * (int64_t)row + l] = sh.rng[l];
     return NIS_REJECT_NONE;
 }
 
