@@ -70,25 +70,43 @@ constexpr int kSLog = 6;                    // log2(kSRes)
 constexpr int kSHB = 32 * kSRes;            // bucket ring: 32 octaves
 constexpr int kSPer = kSHB / 64;            // search rounds (64 buckets each, at most)
 constexpr int kSMem = 64;                   // members of the cutoff bucket
+constexpr uint32_t kSNone = 0x80000000u;    // packed bucket of no candidate (below any b_p)
 constexpr double kS40 = 1099511627776.0;    // 2^40
 
-// Optional per-wave phase timestamps (profiling builds only; compiled out
-// unless NIS_PHASE_TIMING is defined): slot 256 * row + 8 * wave + i for the
-// per-wave phases, 256 * row + 128 + j for the single-wave ones.
+// Optional phase timestamps (profiling builds only; compiled out unless
+// NIS_PHASE_TIMING is defined).  Each wave keeps the low 32 bits of the
+// 100 MHz clock in registers and writes them out when it leaves: slot
+// 256 * row + 8 * wave + i for its own phases, 256 * row + 128 + j for the
+// phases of the single-wave steps it ran.
 #ifdef NIS_PHASE_TIMING
 __device__ unsigned long long nis_sparse_ts[2048 * 256];
-#define NIS_TSLOT(s)                                                                        \
+#define NIS_TDECL                \
+    uint32_t nis_tw_[8] = {};    \
+    uint32_t nis_ts_[16] = {};
+#define NIS_STS(i) (nis_tw_[i] = (uint32_t)wall_clock64())
+#define NIS_STS1(j) (nis_ts_[j] = (uint32_t)wall_clock64())
+#define NIS_TFLUSH()                                                                        \
     do {                                                                                    \
-        if (lane_id() == 0 && blockIdx.x < 2048)                                            \
-            nis_sparse_ts[blockIdx.x * 256 + (s)] = wall_clock64();                         \
+        if (lane_id() == 0 && blockIdx.x < 2048) {                                          \
+            unsigned long long* ts_ = &nis_sparse_ts[blockIdx.x * 256];                    \
+            _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) if (nis_tw_[i_])              \
+                ts_[8 * wave_id() + i_] = nis_tw_[i_];                                      \
+            _Pragma("unroll") for (int j_ = 0; j_ < 16; ++j_) if (nis_ts_[j_])             \
+                ts_[128 + j_] = nis_ts_[j_];                                                \
+        }                                                                                   \
     } while (0)
 #else
-#define NIS_TSLOT(s) \
+#define NIS_TDECL
+#define NIS_STS(i) \
+    do {           \
+    } while (0)
+#define NIS_STS1(j) \
+    do {            \
+    } while (0)
+#define NIS_TFLUSH() \
     do {             \
     } while (0)
 #endif
-#define NIS_STS(i) NIS_TSLOT(8 * wave_id() + (i))
-#define NIS_STS1(j) NIS_TSLOT(128 + (j))
 
 // Stream-end record of one wave (32 bytes, written by its lane 0).
 struct alignas(16) SRec {
@@ -97,15 +115,14 @@ struct alignas(16) SRec {
     float rw;     // R_w
     float thc;    // listing threshold in units of x*c (-inf: the wave holds no data)
     uint32_t n;   // float4s listed (may exceed kSE: overflow)
-    uint32_t nc;  // candidates in the compact list (may exceed kSC: overflow)
-    uint32_t pad;
+    uint32_t pad[2];
 };
 // A member of the cutoff bucket.
 struct alignas(16) SMem {
     float x;
     uint32_t idx;  // row index
     uint32_t fm;   // octave-relative fixed-point mass
-    uint32_t loc;  // owner wave << 16 | lane segment of its compact list
+    uint32_t loc;  // owner wave << 16 | lane segment of its entry list
 };
 // Result of the cutoff search (written by wave 0 between barriers).
 struct alignas(16) SCut {
@@ -120,18 +137,13 @@ struct alignas(16) SCut {
     uint32_t pad[3];
 };
 
-constexpr int kSC = 320;           // compact candidates per wave
-constexpr int kSCL = kSC / 64;     // ... per lane segment
-
 struct WideShared {
     f4v ent[kSW][kSE];             // listed float4s, index order per wave
     uint16_t epos[kSW][kSE];       //   their chunk * 64 + lane
-    float cx[kSW][kSC];            // compact candidates, index order: logit
-    uint32_t ci[kSW][kSC];         //   row index
-    uint32_t cf[kSW][kSC];         //   fm; a wave's sample histogram during its stream
+    uint32_t whist[kSW][256];      // each wave's sample histogram (1/8-octave bins)
     unsigned long long hist[kSHB]; // [b & (kSHB-1)]: count << 48 | sum of fm, buckets >= blo
     unsigned long long oct[32];    // the same per octave
-    double seg[kSW][64];           // kept mass above b_p per compact-list lane segment
+    double seg[kSW][64];           // kept mass above b_p per lane segment of the entry lists
     double tw[kSW];                // per-wave kept mass (2^(R-40) units, integers)
     SMem mem[kSMem];               // members of b_p
     SRec rec[kSW];
@@ -146,7 +158,7 @@ struct WideShared {
     uint32_t kxlo;                 // max listing threshold
     uint32_t kthmin;               // min listing threshold of a wave with entries
     uint32_t krwmin;               // min R_w of a wave with data
-    uint32_t nmax, ncmax;          // largest list / candidate counts
+    uint32_t nmax;                 // largest list
 };
 
 // Octave-relative fixed-point mass of a logit with t = x*c already rounded:
@@ -366,6 +378,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const int wbase = 64 * cpw * w;
     const int Kw = min(max((nsl - wbase + 63) >> 6, 0), cpw);
     const int slot0 = wbase + l;
+    NIS_TDECL
     NIS_STS(0);
 
     // the (at most 3 + 3) elements of partial head / tail slots, by one
@@ -396,7 +409,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         sh.kthmin = 0xFFFFFFFFu;
         sh.krwmin = 0xFFFFFFFFu;
         sh.nmax = 0u;
-        sh.ncmax = 0u;
     }
     lds_barrier();
 #define NIS_SLOAD(k)                                                                          \
@@ -422,7 +434,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     if (w >= kSW / 2) __builtin_amdgcn_s_setprio(2);
     if (w >= 3 * kSW / 4) __builtin_amdgcn_s_setprio(3);
     // each wave's sample histogram is its own
-    uint32_t* const whist = &sh.cf[w][0];
+    uint32_t* const whist = &sh.whist[w][0];
     *reinterpret_cast<u4v*>(&whist[4 * l]) = u4v{0u, 0u, 0u, 0u};
 
     const bool edge_wave = (wbase < f_lo) || (wbase + 64 * Kw - 1 > f_hi);
@@ -526,57 +538,61 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
 #ifdef NIS_EXPERIMENT_STREAM_ONLY
     lds_barrier();
     NIS_STS(2);
+    NIS_TFLUSH();
     return NIS_REJECT_CAPACITY;
 #endif
     __builtin_amdgcn_s_setprio(0);
     mx = wmax_f32(mx);
     z = wsum_f64(z);
     NIS_STS(4);
-    thl = fmaxf(thl, unkey32(sh.kxlo));  // the thresholds published meanwhile
+    // every element of the wave's entries at or above thl (raised to the
+    // thresholds published meanwhile) is a candidate; lane l holds entries
+    // [l sg, l sg + sg).  The candidates join the shared histograms (bucket:
+    // count << 48 | fm, and octave) entry by entry, one candidate per lane per
+    // round: a lane's entry holds few of them, and each round costs the LDS
+    // two instructions.  Each round's bucket (with the element's place) and
+    // fm stay in registers for the kept sums after the search.
+    thl = fmaxf(thl, unkey32(sh.kxlo));
     const uint32_t ne = min(nw, (uint32_t)kSE);
-    const int sg = (int)((ne + 63u) >> 6);  // lane l reads entries [l sg, l sg + sg)
-    // every element of the lane's entries at or above thc is a candidate;
-    // one scan of the per-lane counts places them all, in index order
-    // (branch-free: the stores of each position run under its ballot)
-    f4v ex[kSSeg];
-    uint32_t ep[kSSeg];
-    uint32_t cb = 0;  // bit 4i + q: element q of entry i
-#pragma unroll
-    for (int i = 0; i < kSSeg; ++i) {
-        ex[i] = ninf4;
-        ep[i] = 0u;
-        if (i < sg) {
-            const int j = l * sg + i;
-            const int jc = min(j, kSE - 1);
-            const f4v v = sh.ent[w][jc];
-            ep[i] = sh.epos[w][jc];
-            if (j < (int)ne) ex[i] = v;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) cb |= (elem(ex[i], q) * c >= thl) ? (1u << (4 * i + q)) : 0u;
-    }
-    const uint32_t ccnt = (uint32_t)__popc(cb);
-    const uint32_t cincl = wscan_u32(ccnt);
-    const uint32_t nc = (uint32_t)__builtin_amdgcn_readlane((int)cincl, 63);
-    const uint32_t cbase = cincl - ccnt;
+    const int sg = (int)((ne + 63u) >> 6);
+    uint32_t cbk[kSSeg][4];  // bucket << 4 | (4 i + q); kSNone: no candidate
+    uint32_t cfm[kSSeg][4];  // its fm
+    int nr[kSSeg];           // rounds per entry (wave-uniform)
     {
-        // non-candidates store to the lane's own slot of the (now dead) entry
-        // list, so every position is a plain store: no branches, no exec masks
-        typedef __attribute__((address_space(3))) uint32_t* lu32p;
-        const uint32_t cx0 = lds_addr(&sh.cx[w][0]), ci0 = lds_addr(&sh.ci[w][0]);
-        const uint32_t junk = lds_addr(&sh.ent[w][l]);
+        const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
 #pragma unroll
         for (int i = 0; i < kSSeg; ++i) {
-            if (i < sg) {
-                const uint32_t idx0 = (uint32_t)(4 * (wbase + (int)ep[i]) - mis);
+            nr[i] = 0;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int bit = 4 * i + q;
-                    const bool cq = (cb >> bit) & 1u;
-                    const uint32_t slot = min(cbase + (uint32_t)__popc(cb & ((1u << bit) - 1u)),
-                                              (uint32_t)kSC - 1);
-                    *(lu32p)(size_t)(cq ? cx0 + 4 * slot : junk) = __float_as_uint(elem(ex[i], q));
-                    *(lu32p)(size_t)(cq ? ci0 + 4 * slot : junk + 4) = idx0 + (uint32_t)q;
+            for (int r = 0; r < 4; ++r) {
+                cbk[i][r] = kSNone;
+                cfm[i][r] = 0u;
+            }
+            if (i < sg) {
+                const int j = l * sg + i;
+                f4v v = sh.ent[w][min(j, kSE - 1)];
+                if (j >= (int)ne) v = ninf4;
+                uint32_t cm = 0u;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cm |= (elem(v, q) * c >= thl) ? (1u << q) : 0u;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint64_t am = __ballot(cm != 0u);
+                    if (!am) break;
+                    nr[i] = r + 1;
+                    const uint32_t q = (uint32_t)__builtin_ctz(cm | 16u);
+                    cm &= cm - 1u;
+                    const float lo = (q & 1u) ? v.y : v.x;
+                    const float hi = (q & 1u) ? v.w : v.z;
+                    float xq = (q & 2u) ? hi : lo;
+                    asm volatile("" : "+v"(xq));
+                    const float tq = xq * c;
+                    const int b = s_bucket(tq);
+                    const uint32_t fm = s_fm(xq, c, tq);
+                    lds_add2_u64_m(am, hist0 + 8 * ((uint32_t)b & (uint32_t)(kSHB - 1)),
+                                   oct0 + 8 * ((uint32_t)(b >> kSLog) & 31u), (1ull << 48) | (uint64_t)fm);
+                    cbk[i][r] = (q < 4u) ? (((uint32_t)b << 4) | (uint32_t)(4 * i) | q) : kSNone;
+                    cfm[i][r] = fm;
                 }
             }
         }
@@ -587,36 +603,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const uint32_t ra = lds_addr(&sh.rec[w]);
         lds_put_b128_m(1ull, ra, u4v{(uint32_t)zb, (uint32_t)(zb >> 32), __float_as_uint(mx),
                                      __float_as_uint(Rw)});
-        lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, nc, 0u});
-    }
-    // this wave's candidates into the shared histograms (all of them: the
-    // search reads only the buckets at or above blo, which are complete);
-    // lane l takes candidates [5 l, 5 l + 5) and keeps their logit, index,
-    // fm, bucket and mass in its own frame (2^(R_w - 40) units; exact
-    // integers wherever they are summed later, since R_w <= R and kept
-    // elements lie within 16 octaves of R) for the steps after the search
-    const uint32_t ncl = min(nc, (uint32_t)kSC);
-    uint32_t vx[kSCL], vf[kSCL], vi[kSCL];
-    int vb[kSCL];
-    double vm[kSCL];
-    {
-        const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
-#pragma unroll
-        for (int i = 0; i < kSCL; ++i) {
-            const int j = kSCL * l + i;
-            const bool v = j < (int)ncl;
-            vx[i] = __float_as_uint(sh.cx[w][j]);
-            vi[i] = sh.ci[w][j];
-            const float x = __uint_as_float(vx[i]);
-            const float t = x * c;
-            const float o = floorf(t);
-            vf[i] = s_fm(x, c, t);
-            vb[i] = s_bucket(t);
-            vm[i] = ldexp((double)vf[i], (int)o - (int)Rw + 16);
-            if (v) sh.cf[w][j] = vf[i];
-            lds_add2_u64_m(__ballot(v), hist0 + 8 * ((uint32_t)vb[i] & (kSHB - 1)),
-                           oct0 + 8 * ((uint32_t)(int)o & 31u), (1ull << 48) | (uint64_t)vf[i]);
-        }
+        lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, 0u, 0u});
     }
     // the row's one draw (sampler.rs:209), made by wave 0 off the critical path
     if (w == 0) {
@@ -639,7 +626,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         if (nw > 0u) atomicMin(&sh.kthmin, key32(thr));
         if (mx > -INFINITY) atomicMin(&sh.krwmin, key32(Rw));
         atomicMax(&sh.nmax, nw);
-        atomicMax(&sh.ncmax, nc);
     }
     NIS_STS(2);
 
@@ -662,7 +648,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const int Ri = (int)R;
         const float xlo = unkey32(sh.kxlo);
         const float thmin = unkey32(sh.kthmin);
-        const uint32_t nmax = sh.nmax, ncmax = sh.ncmax;
+        const uint32_t nmax = sh.nmax;
         const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
         // a wave whose reference sits far below the row max may have overflowed
         const bool range_ok = fmaf(M, c, -unkey32(sh.krwmin)) <= 120.0f;
@@ -683,7 +669,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const int oM = bM >> kSLog, olo = blo >> kSLog;
         if (!fin || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok) {
             cut.reject = NIS_REJECT_NONFINITE;
-        } else if (!(xlo < INFINITY) || !(xlo <= M * c) || nmax > (uint32_t)kSE || ncmax > (uint32_t)kSC ||
+        } else if (!(xlo < INFINITY) || !(xlo <= M * c) || nmax > (uint32_t)kSE ||
                    !(bM - (int)(thmin * (float)kSRes) < kSHB - kSRes) || oM - olo > 30) {
             cut.reject = NIS_REJECT_CAPACITY;
         } else {
@@ -768,29 +754,31 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     lds_barrier();
     if (w == 0) NIS_STS1(1);
     const SCut cut = sh.cut;
-    if (cut.reject != NIS_REJECT_NONE) return cut.reject;
+    if (cut.reject != NIS_REJECT_NONE) {
+        NIS_TFLUSH();
+        return cut.reject;
+    }
     const int bp = cut.bp;
     const float M = cut.M, R = cut.R;
     const int Ri = (int)R;
     {
-        // this wave's kept mass above b_p per lane segment of its compact
-        // list (lane l: candidates [5 l, 5 l + 5)), and its members of b_p
-        if (Rw > R) {  // (no finite reference in the first chunk)
-#pragma unroll
-            for (int i = 0; i < kSCL; ++i)
-                vm[i] = ldexp((double)vf[i], (int)floorf(__uint_as_float(vx[i]) * c) - Ri + 16);
-        } else {
-            const double scl = ldexp(1.0, (int)Rw - Ri);  // exact power of two
-#pragma unroll
-            for (int i = 0; i < kSCL; ++i) vm[i] *= scl;
-        }
+        // this wave's kept mass above b_p per lane segment of its entry list
+        // (lane l: entries [l sg, l sg + sg)), and its members of b_p; every
+        // element of bucket >= b_p >= blo is listed, and its mass (octave
+        // >= R - 16) is an exact integer in 2^(R - 40) units
         double ssum = 0.0;
-        uint32_t mb = 0u;
+        uint32_t mb = 0u;  // bit 4 i + q: element q of entry i is a member
 #pragma unroll
-        for (int i = 0; i < kSCL; ++i) {
-            const bool v = kSCL * l + i < (int)ncl;
-            ssum += (v & (vb[i] > bp)) ? vm[i] : 0.0;
-            mb |= (v & (vb[i] == bp)) ? (1u << i) : 0u;
+        for (int i = 0; i < kSSeg; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (r < nr[i]) {
+                    const int b = (int)cbk[i][r] >> 4;
+                    const double m = ldexp((double)cfm[i][r], (b >> kSLog) - Ri + 16);
+                    ssum += (b > bp) ? m : 0.0;
+                    mb |= (b == bp) ? (1u << (cbk[i][r] & 15u)) : 0u;
+                }
+            }
         }
         sh.seg[w][l] = ssum;
         const double tsum = wsum_f64(ssum);
@@ -800,13 +788,16 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         if (mtot) {
             uint32_t base = 0u;
             if (l == 0) base = atomicAdd(&sh.nmem, mtot);
-            base = bcast_u32(base, 0) + mincl - mcnt;
-            const uint32_t mem0 = lds_addr(&sh.mem[0]);
-#pragma unroll
-            for (int i = 0; i < kSCL; ++i) {
-                const uint32_t slot = min(base + (uint32_t)__popc(mb & ((1u << i) - 1u)), (uint32_t)kSMem - 1);
-                lds_put_b128_m(__ballot((mb >> i) & 1u), mem0 + 16 * slot,
-                               u4v{vx[i], vi[i], vf[i], ((uint32_t)w << 16) | (uint32_t)l});
+            uint32_t slot = bcast_u32(base, 0) + mincl - mcnt;
+            while (mb) {  // (members are few: at most kSMem per row)
+                const int bit = __ffs(mb) - 1;
+                mb &= mb - 1u;
+                const int e = l * sg + (bit >> 2), q = bit & 3;
+                const float x = reinterpret_cast<const float*>(&sh.ent[w][e])[q];
+                const uint32_t idx = (uint32_t)(4 * (wbase + (int)sh.epos[w][e]) - mis + q);
+                sh.mem[min(slot, (uint32_t)kSMem - 1)] =
+                    SMem{x, idx, s_fm(x, c, x * c), ((uint32_t)w << 16) | (uint32_t)l};
+                ++slot;
             }
         }
         if (l == 0) sh.tw[w] = tsum;
@@ -817,7 +808,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     uint32_t done2 = 0u;
     if (l == 0) done2 = atomicAdd(&sh.cnt2, 1u);
     done2 = bcast_u32(done2, 0);
-    if (done2 != (uint32_t)(kSW - 1)) return NIS_REJECT_NONE;
+    if (done2 != (uint32_t)(kSW - 1)) {
+        NIS_TFLUSH();
+        return NIS_REJECT_NONE;
+    }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     NIS_STS1(3);
     __builtin_amdgcn_s_setprio(3);
@@ -885,18 +879,19 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const uint64_t hs = __ballot((Sl > 0.0) & (runw + Sincl >= r));
     const int ls = hs ? (__ffsll((long long)hs) - 1) : 0;
     const double runl = bcast_f64(runw + Sincl - Sl, ls);
-    // that segment's candidates, one per lane
-    const uint32_t ncs = min(sh.rec[ws].nc, (uint32_t)kSC);
-    const int je = kSCL * ls + l;
-    const int jec = min(je, kSC - 1);
-    const float xe = sh.cx[ws][jec];
-    const uint32_t fme = sh.cf[ws][jec];
-    const uint32_t ide = sh.ci[ws][jec];
+    // that segment's elements in index order, one per lane (lane j: element
+    // j % 4 of the segment's entry j / 4)
+    const uint32_t nes = min(sh.rec[ws].n, (uint32_t)kSE);
+    const int sgs = (int)((nes + 63u) >> 6);
+    const int je = ls * sgs + (l >> 2);
+    const int jec = min(je, kSE - 1);
+    const float xe = reinterpret_cast<const float*>(&sh.ent[ws][jec])[l & 3];
+    const uint32_t ide = (uint32_t)(4 * (64 * cpw * ws + (int)sh.epos[ws][jec]) - mis + (l & 3));
     const float te = xe * c;
     const int be = s_bucket(te);
     const unsigned long long Ke = ((unsigned long long)key32(xe) << 32) | (uint32_t)~ide;
-    const bool kje = (l < kSCL) & (je < (int)ncs) & ((be > bp) | ((be == bp) & (Ke >= Kcut)));
-    const double ee = kje ? s_m40(fme, (int)floorf(te), Ri) : 0.0;
+    const bool kje = (l < 4 * sgs) & (je < (int)nes) & ((be > bp) | ((be == bp) & (Ke >= Kcut)));
+    const double ee = kje ? s_m40(s_fm(xe, c, te), (int)floorf(te), Ri) : 0.0;
     NIS_STS1(6);
     const double pe_incl = rscan_f64(ee);
     const uint64_t he = __ballot(kje & (runl + pe_incl >= r));
@@ -915,6 +910,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     }
     NIS_STS1(7);
     if (l < 4) a.rng[4 * (int64_t)row + l] = sh.rng[l];
+    NIS_TFLUSH();
     return NIS_REJECT_NONE;
 }
 
