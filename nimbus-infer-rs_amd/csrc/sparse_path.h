@@ -71,6 +71,7 @@ constexpr int kSHB = 32 * kSRes;            // bucket ring: 32 octaves
 constexpr int kSPer = kSHB / 64;            // search rounds (64 buckets each, at most)
 constexpr int kSMem = 64;                   // members of the cutoff bucket
 constexpr uint32_t kSNone = 0x80000000u;    // packed bucket of no candidate (below any b_p)
+constexpr int kSRounds = 4 * kSSeg;         // candidates per lane (at most)
 constexpr double kS40 = 1099511627776.0;    // 2^40
 
 // Optional phase timestamps (profiling builds only; compiled out unless
@@ -548,53 +549,52 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     // every element of the wave's entries at or above thl (raised to the
     // thresholds published meanwhile) is a candidate; lane l holds entries
     // [l sg, l sg + sg).  The candidates join the shared histograms (bucket:
-    // count << 48 | fm, and octave) entry by entry, one candidate per lane per
-    // round: a lane's entry holds few of them, and each round costs the LDS
-    // two instructions.  Each round's bucket (with the element's place) and
-    // fm stay in registers for the kept sums after the search.
+    // count << 48 | fm, and octave) one candidate per lane per round (a lane
+    // holds few of them), the round's element read back from the list by its
+    // LDS address.  Each round's bucket (with the element's place) and fm
+    // stay in registers for the kept sums after the search.
     thl = fmaxf(thl, unkey32(sh.kxlo));
     const uint32_t ne = min(nw, (uint32_t)kSE);
     const int sg = (int)((ne + 63u) >> 6);
-    uint32_t cbk[kSSeg][4];  // bucket << 4 | (4 i + q); kSNone: no candidate
-    uint32_t cfm[kSSeg][4];  // its fm
-    int nr[kSSeg];           // rounds per entry (wave-uniform)
+    const int e0 = l * sg;  // the lane's first entry
+    uint32_t cm = 0u;       // bit 4 i + q: element q of entry e0 + i is a candidate
+#pragma unroll
+    for (int i = 0; i < kSSeg; ++i) {
+        if (i < sg) {
+            const int j = e0 + i;
+            f4v v = sh.ent[w][min(j, kSE - 1)];
+            if (j >= (int)ne) v = ninf4;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) cm |= (elem(v, q) * c >= thl) ? (1u << (4 * i + q)) : 0u;
+        }
+    }
+    uint32_t cbk[kSRounds];  // bucket << 4 | (4 i + q); kSNone: no candidate
+    uint32_t cfm[kSRounds];  // its fm
+    int nrd = 0;             // rounds (wave-uniform)
     {
         const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
+        const float* const el = reinterpret_cast<const float*>(&sh.ent[w][0]) + 4 * e0;
 #pragma unroll
-        for (int i = 0; i < kSSeg; ++i) {
-            nr[i] = 0;
+        for (int r = 0; r < kSRounds; ++r) {
+            cbk[r] = kSNone;
+            cfm[r] = 0u;
+        }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                cbk[i][r] = kSNone;
-                cfm[i][r] = 0u;
-            }
-            if (i < sg) {
-                const int j = l * sg + i;
-                f4v v = sh.ent[w][min(j, kSE - 1)];
-                if (j >= (int)ne) v = ninf4;
-                uint32_t cm = 0u;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) cm |= (elem(v, q) * c >= thl) ? (1u << q) : 0u;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint64_t am = __ballot(cm != 0u);
-                    if (!am) break;
-                    nr[i] = r + 1;
-                    const uint32_t q = (uint32_t)__builtin_ctz(cm | 16u);
-                    cm &= cm - 1u;
-                    const float lo = (q & 1u) ? v.y : v.x;
-                    const float hi = (q & 1u) ? v.w : v.z;
-                    float xq = (q & 2u) ? hi : lo;
-                    asm volatile("" : "+v"(xq));
-                    const float tq = xq * c;
-                    const int b = s_bucket(tq);
-                    const uint32_t fm = s_fm(xq, c, tq);
-                    lds_add2_u64_m(am, hist0 + 8 * ((uint32_t)b & (uint32_t)(kSHB - 1)),
-                                   oct0 + 8 * ((uint32_t)(b >> kSLog) & 31u), (1ull << 48) | (uint64_t)fm);
-                    cbk[i][r] = (q < 4u) ? (((uint32_t)b << 4) | (uint32_t)(4 * i) | q) : kSNone;
-                    cfm[i][r] = fm;
-                }
-            }
+        for (int r = 0; r < kSRounds; ++r) {
+            const uint64_t am = __ballot(cm != 0u);
+            if (!am) break;
+            nrd = r + 1;
+            const uint32_t bit = min((uint32_t)__builtin_ctz(cm | 0x10000u), 15u);
+            const bool has = cm != 0u;
+            cm &= cm - 1u;
+            const float xq = el[bit];
+            const float tq = xq * c;
+            const int b = s_bucket(tq);
+            const uint32_t fm = s_fm(xq, c, tq);
+            lds_add2_u64_m(am, hist0 + 8 * ((uint32_t)b & (uint32_t)(kSHB - 1)),
+                           oct0 + 8 * ((uint32_t)(b >> kSLog) & 31u), (1ull << 48) | (uint64_t)fm);
+            cbk[r] = has ? (((uint32_t)b << 4) | bit) : kSNone;
+            cfm[r] = fm;
         }
     }
     NIS_STS(7);
@@ -769,15 +769,12 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         double ssum = 0.0;
         uint32_t mb = 0u;  // bit 4 i + q: element q of entry i is a member
 #pragma unroll
-        for (int i = 0; i < kSSeg; ++i) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (r < nr[i]) {
-                    const int b = (int)cbk[i][r] >> 4;
-                    const double m = ldexp((double)cfm[i][r], (b >> kSLog) - Ri + 16);
-                    ssum += (b > bp) ? m : 0.0;
-                    mb |= (b == bp) ? (1u << (cbk[i][r] & 15u)) : 0u;
-                }
+        for (int r = 0; r < kSRounds; ++r) {
+            if (r < nrd) {
+                const int b = (int)cbk[r] >> 4;
+                const double m = ldexp((double)cfm[r], (b >> kSLog) - Ri + 16);
+                ssum += (b > bp) ? m : 0.0;
+                mb |= (b == bp) ? (1u << (cbk[r] & 15u)) : 0u;
             }
         }
         sh.seg[w][l] = ssum;
