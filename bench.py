@@ -32,7 +32,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "sampled rows/s + HBM GB/s (% peak), B=256 x V=50257 fp32, T=0.8 top-p=0.9"
-KERNEL_NAME = "sample_rows"
+KERNEL_NAME = "sample_rows_sparse_kernel"
 
 
 def read_traffic(workload):

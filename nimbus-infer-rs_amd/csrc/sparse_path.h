@@ -2,32 +2,31 @@
 // (16 wave64s, four per SIMD), for rows whose nucleus holds a small share of
 // the vocabulary (V <= 53245, 0 < top_p < 1, T > 0, no penalty, no top-k).
 //
-// Stream.  Every lane issues its 13 nontemporal 16-byte buffer loads up
-// front (chunk k / lane l of wave w holds float4 slot base_w + 64k + l, so each
-// wave owns a contiguous index range).  As the chunks land each wave adds the
-// masses 2^(x c - R_w) to Z in f64 (c = log2(e)/T, R_w an integer reference
-// from the wave's first chunk), keeps its max, and appends every float4
-// holding an element at or above its listing threshold thc_w to its LDS
-// list (index order, one ballot per chunk).  thc_w comes from the wave's
-// first four chunks: the lower edge of the 1/8-octave bins of x c holding at
-// most 44 of their 256 float4 maxima.  Four waves share a SIMD, so one
-// wave's dependent chain overlaps the others' and the stream ends close to
-// the last load.
+// Stream.  Chunk k / lane l of wave w holds float4 slot base_w + 64k + l, so
+// each wave owns a contiguous index range of up to 13 chunks.  Every lane
+// keeps three nontemporal 16-byte buffer loads in flight ahead of the chunk
+// it works on, so each wave's data arrives spread over the whole stream and
+// the waves finish together.  As the chunks land each wave adds the masses
+// 2^(x c - R_w) to Z in f64 (c = log2(e)/T, R_w an integer reference from
+// the wave's first chunk), keeps its max, and appends every float4 holding
+// an element at or above its listing threshold to its LDS list (index order,
+// one ballot per chunk).  The threshold thc_w comes from the wave's first
+// four chunks: the lower edge of the 1/8-octave bins of x c holding at most
+// 44 of their 256 float4 maxima, raised to the running max of the thresholds
+// the other waves have published.
 //
 // Cutoff (src/sampler.rs:118-160) without a sort.  The reference keeps
 // sorted position pos iff D(pos) = cum_excl(pos) - q(pos) <= p*Z; D is
 // non-decreasing in pos, so the kept set is a prefix of the stable order.
-// Each wave adds its candidates to its own histogram on an absolute grid of
-// 1/64 octave of x*c (bucket floor(64 * x*c), monotone in x), each bucket
-// holding its count and the exact sum of its members' masses in fixed point
-// relative to the bucket's octave; the search adds the sixteen histograms.
-// Private histograms need no cross-wave ordering before the stream-end
-// barrier: a barrier any earlier would wait until every wave has issued all
-// of its loads, which the CU allows only as the row's data arrives.  Every
+// After its stream each wave adds its candidates (the listed elements at or
+// above its threshold) to one shared histogram on an absolute grid of 1/64
+// octave of x*c (bucket floor(64 * x*c), monotone in x) and to a histogram of
+// whole octaves; each bucket holds its count and the exact sum of its
+// members' masses in fixed point relative to the bucket's octave.  Every
 // element at or above x_lo = max_w thc_w is listed by its wave, so buckets
-// from blo = 16 x_lo up are complete.  With G(b) the
-// mass of the buckets above b and m_up(b) an upper bound of any mass in b,
-// b_p is the deepest non-empty bucket with G(b) - m_up(b) <= p Z:
+// from blo = 64 x_lo up are complete.  With G(b) the mass of the buckets
+// above b and m_up(b) an upper bound of any mass in b, b_p is the deepest
+// non-empty bucket with G(b) - m_up(b) <= p Z:
 //   - every bucket below it fails, so its first element and everything after
 //     it in sorted order is removed;
 //   - every element of the buckets above b_p is kept (the last element y of
@@ -42,12 +41,13 @@
 // agree to the last bit and the inverse-CDF walk (sampler.rs:209-216)
 // always finds its crossing.
 //
-// Three barriers follow the stream: after the histograms (wave 0 then finds
-// b_p), after the search (every wave then lists its members of b_p and sums
-// its buckets above b_p), and after that scan (wave 0 ranks the members and
-// walks waves -> the chosen wave's list segments -> elements).  Any step that cannot
-// prove its result returns a reject code before the last barrier; the caller
-// then runs the general path on the row.
+// Hand-offs after the stream: the last wave to finish its histogram adds
+// (an LDS counter) finds b_p; one barrier publishes it; every wave then sums
+// its kept mass above b_p per lane segment of its list and lists its members
+// of b_p; the last wave to finish that (a second counter) ranks the members
+// and walks waves -> the chosen wave's list segments -> elements.  Any step
+// that cannot prove its result returns a reject code before the barrier; the
+// caller then runs the general path on the row.
 #pragma once
 #include "fast_path.h"
 
