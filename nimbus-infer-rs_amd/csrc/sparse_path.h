@@ -649,6 +649,19 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const float xlo = unkey32(sh.kxlo);
         const float thmin = unkey32(sh.kthmin);
         const uint32_t nmax = sh.nmax;
+        const bool fin = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * c) < 1e6f);
+        const bool xfin = fin & (xlo < INFINITY) & (xlo <= M * c);
+        const int blo = xfin ? (int)(xlo * (float)kSRes) : 0;  // xlo: a multiple of 1/8
+        const int bM = xfin ? s_bucket(M * c) : 0;
+        const int oM = bM >> kSLog, olo = blo >> kSLog;
+        // the level-1 reads go out before anything waits on them: octave
+        // oM - l for l <= oM - olo, and octave olo's buckets at or above blo
+        // (it holds candidates below blo too; its complete part is their sum)
+        const int bl = kSRes * olo + l;
+        const unsigned long long lv = (bl >= blo && bl <= bM) ? sh.hist[(uint32_t)bl & (kSHB - 1)] : 0ull;
+        const int o = oM - l;
+        const bool oin = l <= oM - olo;
+        const unsigned long long ovr = (oin && o != olo) ? sh.oct[(uint32_t)o & 31u] : 0ull;
         const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
         // a wave whose reference sits far below the row max may have overflowed
         const bool range_ok = fmaf(M, c, -unkey32(sh.krwmin)) <= 120.0f;
@@ -663,33 +676,24 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         cut.nabove = 0u;
         cut.M = M;
         cut.R = R;
-        const bool fin = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * c) < 1e6f);
-        const int blo = (fin & (xlo < INFINITY)) ? (int)(xlo * (float)kSRes) : 0;  // xlo: a multiple of 1/8
-        const int bM = fin ? s_bucket(M * c) : 0;
-        const int oM = bM >> kSLog, olo = blo >> kSLog;
         if (!fin || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok) {
             cut.reject = NIS_REJECT_NONFINITE;
-        } else if (!(xlo < INFINITY) || !(xlo <= M * c) || nmax > (uint32_t)kSE ||
+        } else if (!xfin || nmax > (uint32_t)kSE ||
                    !(bM - (int)(thmin * (float)kSRes) < kSHB - kSRes) || oM - olo > 30) {
             cut.reject = NIS_REJECT_CAPACITY;
         } else {
-            // octave olo holds candidates below blo too: its complete part from
-            // its buckets at or above blo
-            const int bl = kSRes * olo + l;
-            const unsigned long long lv =
-                (bl >= blo && bl <= bM) ? sh.hist[(uint32_t)bl & (kSHB - 1)] : 0ull;
+            // level 1.  Octave olo is the deepest lane, so the octaves' prefix
+            // sums do not need its complete part, which is summed alongside.
+            const uint32_t onr = (uint32_t)(ovr >> 48);
+            const double omr = s_m40(ovr & 0xFFFFFFFFFFFFull, o, Ri);
+            const double oincl = wscan_f64(omr);
+            const double Go = oincl - omr;  // mass of the octaves above
+            const uint32_t ocincl = wscan_u32(onr);
+            const uint32_t Co = ocincl - onr;
             const unsigned long long lsum = bcast_u64(wscan_u64(lv), 63);
-            // level 1: octave oM - l for l <= oM - olo
-            const int o = oM - l;
-            const bool oin = l <= oM - olo;
-            const unsigned long long ov = !oin ? 0ull : (o == olo ? lsum : sh.oct[(uint32_t)o & 31u]);
-            const uint32_t on = (uint32_t)(ov >> 48);
-            const double om = s_m40(ov & 0xFFFFFFFFFFFFull, o, Ri);
-            const double oincl = wscan_f64(om);
-            const double Go = oincl - om;  // mass of the octaves above
-            const uint32_t ocincl = wscan_u32(on);
-            const uint32_t Co = ocincl - on;
-            const double gtot = bcast_f64(oincl, 63);  // everything >= blo
+            const double omlo = s_m40(lsum & 0xFFFFFFFFFFFFull, olo, Ri);
+            const uint32_t on = (o == olo) ? (uint32_t)(lsum >> 48) : onr;
+            const double gtot = bcast_f64(oincl, 63) + omlo;  // everything >= blo
             const uint64_t P = __ballot(oin & (on != 0u) & (Go - ldexp(1.0001, o + 1 - Ri + 40) <= pz));
             const uint64_t NEo = __ballot(oin & (on != 0u));
             // everything below blo is removed: G(blo - 1) - m_up(blo - 1) > p Z
@@ -766,17 +770,20 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         // (lane l: entries [l sg, l sg + sg)), and its members of b_p; every
         // element of bucket >= b_p >= blo is listed, and its mass (octave
         // >= R - 16) is an exact integer in 2^(R - 40) units
-        double ssum = 0.0;
+        // (in 64-bit integers: a kept mass is fm << (octave - R + 16), a shift
+        // of 0..16)
+        unsigned long long isum = 0ull;
         uint32_t mb = 0u;  // bit 4 i + q: element q of entry i is a member
 #pragma unroll
         for (int r = 0; r < kSRounds; ++r) {
             if (r < nrd) {
                 const int b = (int)cbk[r] >> 4;
-                const double m = ldexp((double)cfm[r], (b >> kSLog) - Ri + 16);
-                ssum += (b > bp) ? m : 0.0;
+                const uint32_t fk = (b > bp) ? cfm[r] : 0u;
+                isum += (unsigned long long)fk << ((uint32_t)((b >> kSLog) - Ri + 16) & 63u);
                 mb |= (b == bp) ? (1u << (cbk[r] & 15u)) : 0u;
             }
         }
+        const double ssum = (double)isum;
         sh.seg[w][l] = ssum;
         const double tsum = wsum_f64(ssum);
         const uint32_t mcnt = (uint32_t)__popc(mb);
