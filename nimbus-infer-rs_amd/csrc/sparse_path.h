@@ -697,7 +697,8 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const uint64_t P = __ballot(oin & (on != 0u) & (Go - ldexp(1.0001, o + 1 - Ri + 40) <= pz));
             const uint64_t NEo = __ballot(oin & (on != 0u));
             // everything below blo is removed: G(blo - 1) - m_up(blo - 1) > p Z
-            const bool lo_ok = gtot - s_mup(blo - 1, Ri) > pz;
+            // (and every sum of kept masses stays an exact f64 integer: below 2^52)
+            const bool lo_ok = (gtot - s_mup(blo - 1, Ri) > pz) & (gtot < 4503599627370496.0);
             if (!P || !lo_ok) {
                 cut.reject = NIS_REJECT_WINDOW;
             } else {

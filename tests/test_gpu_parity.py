@@ -213,9 +213,10 @@ def test_padded_and_misaligned_rows(sampler, ld_extra):
 
 @pytest.mark.parametrize("V", [256, 300, 1000, 2053, 4100, 16383, 16389, 30001, 53245])
 def test_register_layout_sizes(sampler, V):
-    # the register-resident path splits a row's float4 slots evenly over its
-    # eight waves in whole 64-slot chunks: sizes with fewer chunks than the
-    # sample, waves holding nothing, partial last chunks, and the largest V
+    # both row kernels split a row's float4 slots over their waves (16 for the
+    # sparse kernel, 8 for the other) in whole 64-slot chunks: sizes with
+    # fewer chunks than the sample, waves holding nothing, partial last
+    # chunks, and the largest V
     rnd = np.random.Generator(np.random.PCG64(V))
     B = 48
     x = rnd.standard_normal((B, V), dtype=np.float32) * np.float32(3.0)
