@@ -149,7 +149,6 @@ struct WideShared {
     SMem mem[kSMem];               // members of b_p
     SRec rec[kSW];
     SCut cut;
-    uint64_t rng[4];               // the row's RNG state after its one draw
     double u0;                     // the draw
     uint32_t nmem;
     uint32_t cnt1;                 // waves done with their candidates
@@ -605,20 +604,17 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                                      __float_as_uint(Rw)});
         lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, 0u, 0u});
     }
-    // the row's one draw (sampler.rs:209), made by wave 0 off the critical path
+    // the row's one draw (sampler.rs:209), made by wave 0 off the critical
+    // path; wave 0 stores the advanced state once the row cannot be declined
+    uint64_t rst = 0;  // wave 0, lane j < 4: word j of the advanced state
     if (w == 0) {
         uint64_t st[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
         const double u0 = rng_next_f64(st);
-        if (l == 0) {
-            sh.u0 = u0;
-            sh.rng[0] = st[0];
-            sh.rng[1] = st[1];
-            sh.rng[2] = st[2];
-            sh.rng[3] = st[3];
-        }
+        if (l == 0) sh.u0 = u0;
+        rst = (l == 0) ? st[0] : (l == 1) ? st[1] : (l == 2) ? st[2] : st[3];
     }
     if (l == 0) {
         const float thr = Kw > 0 ? thc : -INFINITY;
@@ -763,6 +759,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         NIS_TFLUSH();
         return cut.reject;
     }
+    if (w == 0 && l < 4) a.rng[4 * (int64_t)row + l] = rst;
     const int bp = cut.bp;
     const float M = cut.M, R = cut.R;
     const int Ri = (int)R;
@@ -869,8 +866,8 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     }
     lds_wave_fence();
     const double T = rv ? sh.tw[li] : 0.0;
-    const double Tincl = wscan_f64(T);
-    const double zk = bcast_f64(Tincl, 63);
+    const double Tincl = rscan_f64(T);  // (lanes 0..15 hold the waves)
+    const double zk = bcast_f64(Tincl, 15);
     const double u = sh.u0;
     const double r = u * zk;
     const uint64_t hw = __ballot(rv & (T > 0.0) & (Tincl >= r));
@@ -902,19 +899,17 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const uint64_t he = __ballot(kje & (runl + pe_incl >= r));
     const int le = he ? (__ffsll((long long)he) - 1) : 0;
     if (l == le) {
-        uint32_t tok = ide;
-        double prob = ee / zk;
-        if (u == 0.0) {  // r == 0 stops the reference's walk at index 0
-            tok = 0u;
-            prob = 0.0;
+        const uint32_t tok = (u == 0.0) ? 0u : ide;  // r == 0 stops the reference's walk at index 0
+        a.tokens[row] = tok;
+        if (a.stats) {
+            const double prob = (u == 0.0) ? 0.0 : ee / zk;
+            // 2^(R - M c): units of 2^R -> units of the max element's mass
+            const double rho = (double)__builtin_amdgcn_exp2f(-fmaf(M, c, -R));
+            write_row_result(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zk / kS40 * rho,
+                             cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
         }
-        // 2^(R - M c): units of 2^R -> units of the max element's mass
-        const double rho = (double)__builtin_amdgcn_exp2f(-fmaf(M, c, -R));
-        write_row_result(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zk / kS40 * rho,
-                         cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
     }
     NIS_STS1(7);
-    if (l < 4) a.rng[4 * (int64_t)row + l] = sh.rng[l];
     NIS_TFLUSH();
     return NIS_REJECT_NONE;
 }
