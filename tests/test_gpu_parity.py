@@ -231,6 +231,23 @@ def test_register_layout_sizes(sampler, V):
            label=f"layout-V{V}-greedy")
 
 
+@pytest.mark.parametrize("sigma", [0.5, 2.0, 6.0])
+def test_sparse_kernel_distribution_sweep(sampler, sigma):
+    # the sparse top-p kernel over logit scales, temperatures and top-p
+    # values around the headline's: nuclei from a handful of tokens to a
+    # large share of the vocabulary (the wide ones leave for the general
+    # path; every row must match either way), plus rows with a planted
+    # dominant token and rows whose draw is u = 0 territory (seed sweep)
+    rnd = np.random.Generator(np.random.PCG64(int(sigma * 10)))
+    B, V = 32, 32000
+    x = (rnd.standard_normal((B, V), dtype=np.float32) * np.float32(sigma))
+    x[::5, rnd.integers(0, V)] += np.float32(12.0)
+    for T in (0.5, 1.0, 1.7):
+        for p in (0.3, 0.8, 0.95):
+            _check(sampler, x, V, _params(temperature=T, top_p=p), list(range(100, 100 + B)),
+                   label=f"sweep-s{sigma}-T{T}-p{p}")
+
+
 def test_penalty_and_top_k_full_vocab(sampler):
     rnd = np.random.Generator(np.random.PCG64(77))
     B, V = 48, 50257
