@@ -175,7 +175,11 @@ __device__ __forceinline__ double s_m40(unsigned long long fm, int o, int R) {
     return sh >= 0 ? v : floor(v);
 }
 // Bucket of t = x*c on the absolute grid: floor(64 t), monotone in x.
-__device__ __forceinline__ int s_bucket(float t) { return (int)floorf(t * (float)kSRes); }
+__device__ __forceinline__ int s_bucket(float t) {
+    int b;
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(b) : "v"(t * (float)kSRes));  // floor, then convert
+    return b;
+}
 // Upper bound of the 2^(R - 40)-unit mass of any element in bucket b (its
 // upper edge, inflated for the roundings of x*c and exp2).
 __device__ __forceinline__ double s_mup(int b, int R) {
@@ -583,7 +587,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const uint64_t am = __ballot(cm != 0u);
             if (!am) break;
             nrd = r + 1;
-            const uint32_t bit = min((uint32_t)__builtin_ctz(cm | 0x10000u), 15u);
+            const uint32_t bit = (uint32_t)__builtin_ctz(cm | 0x8000u);  // 15 for no candidate
             const bool has = cm != 0u;
             cm &= cm - 1u;
             const float xq = el[bit];
@@ -830,35 +834,22 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const unsigned long long Km = valid ? (((unsigned long long)key32(xm) << 32) | (uint32_t)~im) : 0ull;
     NIS_STS1(11);
     double pre = 0.0;
+    uint32_t rk = 0u;  // members ahead of this one
 #pragma unroll 4
     for (int j = 0; j < n; ++j) {
         const unsigned long long Kj = bcast_u64(Km, j);
         const double ej = bcast_f64(em, j);
         pre += (Kj > Km) ? ej : 0.0;
+        rk += (Kj > Km) ? 1u : 0u;
     }
     NIS_STS1(12);
     const bool kept = valid & (gp + pre - em <= pz);  // sampler.rs:150
     const uint64_t keptm = __ballot(kept);
     const uint32_t nkept = (uint32_t)__popcll(keptm);
-    // the last kept member (the smallest key); elements of b_p at or above it are kept
-    unsigned long long Kcut = kept ? Km : ~0ull;
-    {
-#define NIS_MIN64(C, MSK)                                                                              \
-        {                                                                                              \
-            const uint32_t lo_ = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)Kcut, C, MSK, 0xF, false);         \
-            const uint32_t hi_ = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)(Kcut >> 32), C, MSK, 0xF, false); \
-            const unsigned long long y_ = ((unsigned long long)hi_ << 32) | lo_;                      \
-            Kcut = y_ < Kcut ? y_ : Kcut;                                                              \
-        }
-        NIS_MIN64(0x111, 0xF)
-        NIS_MIN64(0x112, 0xF)
-        NIS_MIN64(0x114, 0xF)
-        NIS_MIN64(0x118, 0xF)
-        NIS_MIN64(0x142, 0xA)
-        NIS_MIN64(0x143, 0xC)
-#undef NIS_MIN64
-        Kcut = bcast_u64(Kcut, 63);
-    }
+    // the last kept member (the smallest key; the kept ones are the nkept
+    // largest, the keys being distinct); elements of b_p at or above it are kept
+    const uint64_t lastm = __ballot(valid & (rk + 1u == nkept));
+    const unsigned long long Kcut = lastm ? bcast_u64(Km, __ffsll((long long)lastm) - 1) : ~0ull;
     // the kept members join their wave's and their segment's kept mass
     {
         const int mw = min((int)(mr.w >> 16), kSW - 1), ms = (int)(mr.w & 63u);
