@@ -139,8 +139,8 @@ struct alignas(16) SCut {
 };
 
 struct WideShared {
-    f4v ent[kSW][kSE];             // listed float4s, index order per wave
-    uint16_t epos[kSW][kSE];       //   their chunk * 64 + lane
+    f4v ent[kSW][kSE + 64];        // listed float4s, index order per wave (+ one chunk of slack)
+    uint16_t epos[kSW][kSE + 64];  //   their chunk * 64 + lane
     uint32_t whist[kSW][256];      // each wave's sample histogram (1/8-octave bins)
     unsigned long long hist[kSHB]; // [b & (kSHB-1)]: count << 48 | sum of fm, buckets >= blo
     unsigned long long oct[32];    // the same per octave
@@ -415,10 +415,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         sh.nmax = 0u;
     }
     lds_barrier();
+    const int voff = 16 * slot0;  // (chunks past the first never hold slot 0)
 #define NIS_SLOAD(k)                                                                          \
     do {                                                                                      \
-        const int f_ = slot0 + (k) * 64;                                                      \
-        xv[k] = nis_buffer_load_f4(rsrc, ((k) < Kw) ? 16 * max(f_, f_lo) : 0x7FFFFFF0, 0, 2); \
+        xv[k] = nis_buffer_load_f4(rsrc, ((k) < Kw) ? voff + 1024 * (k) : 0x7FFFFFF0, 0, 2);  \
     } while (0)
 #pragma unroll
     for (int k = 1; k < kSD && k < kSN; ++k) {
@@ -475,12 +475,16 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const uint32_t ent0 = lds_addr(&sh.ent[w][0]), pos0 = lds_addr(&sh.epos[w][0]);
     float thc = INFINITY;  // this wave's sample threshold (x*c units, a multiple of 1/8)
     float thl = INFINITY;  // its listing threshold: thc raised to the waves' running max
+    float thx = INFINITY;  // the same in logit units, rounded down
     uint32_t nw = 0;
     float mcs[kSS];
-#define NIS_SLIST(k, mc)                                                                    \
+    // (a chunk's entries go from slot min(nw, kSE) on: at most 64 of them land
+    // in the list's slack, and a list past kSE entries declines the row)
+#define NIS_SLIST(k, cond)                                                                  \
     {                                                                                       \
-        const uint64_t mk = __ballot((mc) >= thl);                                          \
-        const uint32_t slot = min(nw + lane_rank(mk), (uint32_t)kSE - 1);                   \
+        const uint64_t mk = __ballot(cond);                                                 \
+        const uint32_t slot = __builtin_amdgcn_mbcnt_hi(                                    \
+            (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, min(nw, (uint32_t)kSE))); \
         lds_put_x4_u16(mk, ent0 + 16 * slot, xv[k], pos0 + 2 * slot, (uint32_t)((k) * 64 + l)); \
         nw += (uint32_t)__popcll(mk);                                                       \
     }
@@ -501,8 +505,8 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         z += (double)((e0 + e1) + (e2 + e3));                                                \
         const float m4 = s_max4(x);                                                          \
         mx = s_max(mx, m4);                                                                  \
-        const float mc = m4 * c;                                                             \
         if (k < kSS) {                                                                       \
+            const float mc = m4 * c;                                                         \
             mcs[k] = mc;                                                                     \
             const float tb = floorf((RwH - mc) * 8.0f); /* -inf -> +inf */                   \
             atomicAdd(&whist[(uint32_t)fminf(fmaxf(tb, 0.0f), 255.0f)], 1u);                 \
@@ -522,10 +526,12 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             if (Kw > 0 && l == 0) atomicMax(&sh.kxlo, key32(thc));                           \
             lds_wave_fence();                                                                \
             thl = fmaxf(thc, unkey32(sh.kxlo));                                              \
-            _Pragma("unroll") for (int j = 0; j < kSS; ++j) NIS_SLIST(j, mcs[j])             \
+            /* thl in logit units, rounded down: x >= thx whenever x * c >= thl */           \
+            thx = thl < INFINITY ? thl / c - fabsf(thl / c) * 1.0e-6f - 1.0e-30f : INFINITY; \
+            _Pragma("unroll") for (int j = 0; j < kSS; ++j) NIS_SLIST(j, mcs[j] >= thl)      \
             NIS_STS(6);                                                                      \
         }                                                                                    \
-        if (k >= kSS) NIS_SLIST(k, mc)                                                       \
+        if (k >= kSS) NIS_SLIST(k, m4 >= thx)                                                \
     }
     if (edge_wave) {
         NIS_SSTREAM(true)
