@@ -48,6 +48,66 @@ def read_traffic(workload):
     return None
 
 
+def bench_decode(args, w, sampler, params, bufs, states, tokens):
+    """Decode steps (engine.rs:279-287 on the device): one nis_decode_step per
+    rotated batch, sequences never finishing (budget and history capacity
+    above the steps of a replay, which starts by clearing lengths and flags)."""
+    import torch
+    B, V = w.B, w.V
+    dev = tokens.device
+    cap = 64
+    gen_ids = torch.zeros((B, cap), dtype=torch.int32, device=dev)
+    gen_len = torch.zeros(B, dtype=torch.int32, device=dev)
+    max_new = torch.full((B,), cap, dtype=torch.int32, device=dev)
+    done = torch.zeros(B, dtype=torch.uint8, device=dev)
+    G = len(bufs)
+
+    def block():
+        gen_len.zero_()
+        done.zero_()
+        for i in range(G):
+            sampler.decode_step(bufs[i], params, states, gen_ids, gen_len, max_new, done,
+                                tokens=tokens)
+
+    for _ in range(max(1, args.warmup // G)):
+        block()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap_stream = torch.cuda.Stream()
+    cap_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap_stream):
+        with torch.cuda.graph(graph, stream=cap_stream):
+            block()
+    torch.cuda.current_stream().wait_stream(cap_stream)
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    K = max(G, (args.steps // G) * G)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(K // G):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / K
+    assert int(gen_len[0].item()) == G and int(done.sum().item()) == 0
+    alg_bytes = B * (4 * V + 68) + B * (4 + 4 + 1)  # logits, RNG, token + history, length, flag
+    print(json.dumps({
+        "metric": f"decode steps: tokens/s, B={B} sequences x V={V} fp32, "
+                  f"T={w.temperature} top-p={w.top_p}",
+        "value": B / (us * 1e-6), "unit": "tokens/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "us_per_step": us, "higher_is_better": True,
+        "data": "synthetic logits of the workload, 8 rotated batches resident in HBM",
+        "config": {"workload": args.workload, "B": B, "V": V, "history_cap": cap,
+                   "launch": f"hipGraph replay of {G} nis_decode_step calls after clearing "
+                             "the lengths and flags"},
+        "roofline": {"bound": "hbm", "achieved": alg_bytes / (us * 1e-6) / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -58,6 +118,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="oracle worker threads (0: NIMBUS_THREADS, else min(16, cores))")
+    ap.add_argument("--decode", action="store_true",
+                    help="time nis_decode_step (sample + on-device history / stop / budget "
+                         "update) on the workload instead, and print that line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 4 plain device copies of MIB MiB (reads MIB, writes MIB) "
                          "to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -99,6 +162,10 @@ def main():
     states = torch.from_numpy(ns.rng_states(w.seeds).view(np.int64)).to(dev)
     tokens = torch.empty(B, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
+    if args.decode:
+        bench_decode(args, w, sampler, params, bufs, states, tokens)
+        sampler.close()
+        return
 
     # parity of one batch against the oracle (state copy so the timed run is unaffected)
     parity = None

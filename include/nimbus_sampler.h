@@ -125,6 +125,27 @@ int nis_sample_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B,
                      const uint32_t* d_gen_ids, const int64_t* d_gen_offsets,
                      uint32_t* d_tokens, nis_row_stats* d_stats);
 
+/* One step of a device-resident batched decode loop: the decode loop of
+ * Engine::generate_ids (engine.rs:279-287) for B sequences at once, with the
+ * model step left to the caller.  For every sequence b with d_done[b] == 0:
+ *   token = sample(logits row b, params, history b, rng b)   (engine.rs:280)
+ *   history b gets the token                                  (engine.rs:281)
+ *   done when the token is one of the n_stop ids d_stop_ids, or the sequence
+ *   has produced d_max_new[b] tokens                          (engine.rs:285)
+ * History b is d_gen_ids[b*gen_cap .. b*gen_cap + d_gen_len[b]) and doubles
+ * as the repetition-penalty list (the reference penalizes `generated`, not
+ * the prompt); a full history (gen_len == gen_cap) also ends the sequence.
+ * Sequences already done are skipped: no token written, RNG not advanced.
+ * The caller starts with gen_len = 0 and done[b] = (max_new[b] <= 0), where
+ * max_new[b] = min(max_new_tokens, max_seq_len - prompt length)
+ * (engine.rs:265-266).  Same logits / params / RNG / stats contract as
+ * nis_sample_batch.  Asynchronous on the context stream. */
+int nis_decode_step(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                    const nis_params* params, uint64_t* d_rng_state, uint32_t* d_gen_ids,
+                    int64_t gen_cap, int32_t* d_gen_len, const int32_t* d_max_new,
+                    const uint32_t* d_stop_ids, int32_t n_stop, uint8_t* d_done,
+                    uint32_t* d_tokens, nis_row_stats* d_stats);
+
 /* Batched greedy: first index of the row maximum (sampler.rs:172-181);
  * same as nis_sample_batch with temperature 0 and no penalty. */
 int nis_argmax_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,

@@ -73,6 +73,50 @@ int check_batch_args(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B,
     return NIS_OK;
 }
 
+nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_params* params,
+                      uint64_t* d_rng_state, uint32_t* d_tokens, nis_row_stats* d_stats) {
+    nis::RowArgs a;
+    a.logits = d_logits;
+    a.ld = ld;
+    a.V = V;
+    a.temperature = params->temperature;
+    a.top_p = params->top_p;
+    a.penalty = params->repetition_penalty;
+    a.top_k = params->top_k;
+    a.rng = d_rng_state;
+    a.gen_ids = nullptr;
+    a.gen_off = nullptr;
+    a.gen_len = nullptr;
+    a.gen_cap = 0;
+    a.done = nullptr;
+    a.gen_out = nullptr;
+    a.max_new = nullptr;
+    a.stop = nullptr;
+    a.n_stop = 0;
+    a.tokens = d_tokens;
+    a.stats = d_stats;
+    return a;
+}
+
+// Rows whose nucleus is likely a small share of the vocabulary (top-p well
+// below 1, no top-k, no penalty history) go to the 1024-lane sparse kernel;
+// everything else (greedy, top-p off or near 1, top-k, penalty, V outside its
+// range) to the 512-lane register-resident / general one.  Either kernel
+// computes every row exactly; this only picks the faster.
+int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
+    const bool sparse = a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f &&
+                        a.top_p > 0.0f && a.top_p <= 0.98f && (a.top_k == 0 || a.top_k >= (uint64_t)a.V) &&
+                        (a.penalty == 1.0f || a.gen_ids == nullptr);
+    if (sparse)
+        hipLaunchKernelGGL(nis::sample_rows_sparse_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
+                           ctx->stream, a);
+    else
+        hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
+                           ctx->stream, a);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "sample kernel launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -164,36 +208,38 @@ int nis_sample_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B,
     if (rc != NIS_OK) return rc;
     DeviceGuard g(ctx->device);
     if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
-    nis::RowArgs a;
-    a.logits = d_logits;
-    a.ld = ld;
-    a.V = V;
-    a.temperature = params->temperature;
-    a.top_p = params->top_p;
-    a.penalty = params->repetition_penalty;
-    a.top_k = params->top_k;
-    a.rng = d_rng_state;
+    nis::RowArgs a = row_args(d_logits, ld, V, params, d_rng_state, d_tokens, d_stats);
     a.gen_ids = d_gen_ids;
     a.gen_off = d_gen_offsets;
-    a.tokens = d_tokens;
-    a.stats = d_stats;
-    // Rows whose nucleus is likely a small share of the vocabulary (top-p
-    // well below 1, no top-k, no penalty lists) go to the 1024-lane sparse
-    // kernel; everything else (greedy, top-p off or near 1, top-k, penalty,
-    // V outside its range) to the 512-lane register-resident / general one.
-    // Either kernel computes every row exactly; this only picks the faster.
-    const bool sparse = V >= 256 && V <= nis::kSMaxV && params->temperature > 0.0f &&
-                        params->top_p > 0.0f && params->top_p <= 0.98f &&
-                        (params->top_k == 0 || params->top_k >= (uint64_t)V) &&
-                        (params->repetition_penalty == 1.0f || d_gen_ids == nullptr);
-    if (sparse)
-        hipLaunchKernelGGL(nis::sample_rows_sparse_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
-                           ctx->stream, a);
-    else
-        hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
-                           ctx->stream, a);
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "sample kernel launch");
+    return launch_rows(ctx, a, B);
+}
+
+int nis_decode_step(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                    const nis_params* params, uint64_t* d_rng_state, uint32_t* d_gen_ids,
+                    int64_t gen_cap, int32_t* d_gen_len, const int32_t* d_max_new,
+                    const uint32_t* d_stop_ids, int32_t n_stop, uint8_t* d_done,
+                    uint32_t* d_tokens, nis_row_stats* d_stats) {
+    int rc = check_batch_args(ctx, d_logits, ld, B, V, params, d_rng_state, nullptr, nullptr,
+                              d_tokens);
+    if (rc != NIS_OK) return rc;
+    if (!d_gen_ids || !d_gen_len || !d_max_new || !d_done)
+        return fail(ctx, NIS_EINVAL, "gen_ids, gen_len, max_new and done are required");
+    if (gen_cap <= 0) return fail(ctx, NIS_EINVAL, "gen_cap must be positive");
+    if (gen_cap > ((int64_t)1 << 31) - 1) return fail(ctx, NIS_ERANGE, "gen_cap exceeds INT32_MAX");
+    if (n_stop < 0 || (n_stop > 0 && !d_stop_ids))
+        return fail(ctx, NIS_EINVAL, "n_stop must be >= 0 with stop ids when positive");
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+    nis::RowArgs a = row_args(d_logits, ld, V, params, d_rng_state, d_tokens, d_stats);
+    a.gen_ids = d_gen_ids;
+    a.gen_len = d_gen_len;
+    a.gen_cap = gen_cap;
+    a.done = d_done;
+    a.gen_out = d_gen_ids;
+    a.max_new = d_max_new;
+    a.stop = d_stop_ids;
+    a.n_stop = n_stop;
+    return launch_rows(ctx, a, B);  // the row kernels append, stop and count in place
 }
 
 int nis_argmax_batch(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,

@@ -455,8 +455,8 @@ __device__ __forceinline__ void hist_list(FastShared& sh, int o, uint32_t n, flo
 
 __device__ __forceinline__ bool fast_eligible(const RowArgs a, int row) {
     if (a.V < 256 || a.V > kFastMaxV) return false;
-    if (a.penalty != 1.0f && a.gen_ids != nullptr && a.gen_off != nullptr &&
-        a.gen_off[row + 1] > a.gen_off[row])
+    int64_t g0 = 0, g1 = 0;
+    if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0)
         return false;
     if (a.temperature <= 0.0f) return true;
     if (a.top_k > 0 && a.top_k < (uint64_t)a.V) return false;

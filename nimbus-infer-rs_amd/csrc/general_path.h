@@ -44,10 +44,34 @@ struct RowArgs {
     uint64_t top_k;
     uint64_t* rng;
     const uint32_t* gen_ids;
-    const int64_t* gen_off;
+    const int64_t* gen_off;     // CSR history: row b's ids are gen_ids[gen_off[b] .. gen_off[b+1])
+    int32_t* gen_len;           // or, when set, row b's are gen_ids[b cap .. b cap + gen_len[b])
+    int64_t gen_cap;
+    // decode step (all NULL otherwise): rows with done[b] != 0 are skipped; a
+    // row's token joins its history, and a stop id or the budget max_new[b]
+    // ends the row
+    uint8_t* done;
+    uint32_t* gen_out;          // the same history, written
+    const int32_t* max_new;
+    const uint32_t* stop;
+    int32_t n_stop;
     uint32_t* tokens;
     nis_row_stats* stats;
 };
+
+// Row b's repetition-penalty history [g0, g1) in gen_ids; false without one.
+__device__ __forceinline__ bool gen_range(const RowArgs& a, int row, int64_t& g0, int64_t& g1) {
+    if (a.gen_ids == nullptr) return false;
+    if (a.gen_len != nullptr) {
+        g0 = (int64_t)row * a.gen_cap;
+        g1 = g0 + min((int64_t)max(a.gen_len[row], 0), a.gen_cap);
+        return true;
+    }
+    if (a.gen_off == nullptr) return false;
+    g0 = a.gen_off[row];
+    g1 = a.gen_off[row + 1];
+    return true;
+}
 
 constexpr int kGU = 16;                          // loads per lane per block of a pass
 constexpr int kGChunk = 512;                     // walk chunk: 8 rows of 64 elements
@@ -83,12 +107,27 @@ struct GeneralShared {
     int64_t bi[4];
 };
 
-__device__ __forceinline__ void write_row_result(const RowArgs a, int row, uint32_t token,
-                                                 uint32_t path, double max_w, double z_kept,
-                                                 double z_all, double u, double prob,
-                                                 uint64_t kept, uint32_t kernel,
-                                                 uint32_t reject = NIS_REJECT_NONE) {
+// The row's token (one lane per row).  In a decode step it also joins the
+// row's history, which ends the row on a stop id, on its budget or when full
+// (engine.rs:281-287); the penalty read that history before this point.
+__device__ __forceinline__ void emit_token(const RowArgs& a, int row, uint32_t token) {
     a.tokens[row] = token;
+    if (a.max_new != nullptr) {
+        int64_t n = max(a.gen_len[row], 0);
+        if (n < a.gen_cap) a.gen_out[(int64_t)row * a.gen_cap + n] = token;
+        n = min(n + 1, a.gen_cap);
+        a.gen_len[row] = (int32_t)n;
+        bool hit = false;
+        for (int s = 0; s < a.n_stop; ++s) hit |= a.stop[s] == token;
+        if (hit || n >= (int64_t)a.max_new[row] || n >= a.gen_cap) a.done[row] = 1u;
+    }
+}
+
+__device__ __forceinline__ void write_row_stats(const RowArgs a, int row, uint32_t token,
+                                                uint32_t path, double max_w, double z_kept,
+                                                double z_all, double u, double prob,
+                                                uint64_t kept, uint32_t kernel,
+                                                uint32_t reject = NIS_REJECT_NONE) {
     if (a.stats) {
         nis_row_stats s;
         s.max_w = max_w;
@@ -103,6 +142,15 @@ __device__ __forceinline__ void write_row_result(const RowArgs a, int row, uint3
         s.reject = reject;
         a.stats[row] = s;
     }
+}
+
+__device__ __forceinline__ void write_row_result(const RowArgs a, int row, uint32_t token,
+                                                 uint32_t path, double max_w, double z_kept,
+                                                 double z_all, double u, double prob,
+                                                 uint64_t kept, uint32_t kernel,
+                                                 uint32_t reject = NIS_REJECT_NONE) {
+    emit_token(a, row, token);
+    write_row_stats(a, row, token, path, max_w, z_kept, z_all, u, prob, kept, kernel, reject);
 }
 
 // Digit range of a most-significant-digit radix walk: bits above `hi_shift+8`
@@ -218,8 +266,8 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
 
     // ---- repetition penalty set (sampler.rs:83-101) --------------------
     bool pen = false;
-    if (a.penalty != 1.0f && a.gen_ids != nullptr && a.gen_off != nullptr) {
-        const int64_t g0 = a.gen_off[row], g1 = a.gen_off[row + 1];
+    int64_t g0 = 0, g1 = 0;
+    if (a.penalty != 1.0f && gen_range(a, row, g0, g1)) {
         if (SIMPLE && g1 > g0) return false;
         if (!SIMPLE && g1 > g0) {
             pen = true;

@@ -12,6 +12,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(RowArgs a) {
         FastShared f;
     } sh;
     const int row = (int)blockIdx.x;
+    if (a.done != nullptr && a.done[row]) return;  // a finished sequence (decode step)
     // every argument the fast path reads before its first load, fetched in
     // one batch of scalar loads instead of a chain of them behind the
     // eligibility tests
@@ -36,6 +37,7 @@ __global__ __launch_bounds__(kSB) void sample_rows_sparse_kernel(RowArgs a) {
         WideShared s;
     } sh;
     const int row = (int)blockIdx.x;
+    if (a.done != nullptr && a.done[row]) return;  // a finished sequence (decode step)
     asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
                  "s"(a.penalty), "s"(a.top_k), "s"(a.gen_ids), "s"(a.gen_off));
     uint32_t reject = NIS_REJECT_SHAPE;

@@ -358,8 +358,8 @@ __device__ __forceinline__ bool sparse_eligible(const RowArgs a, int row) {
     if (a.V < 256 || a.V > kSMaxV) return false;
     if (!(a.temperature > 0.0f) || !(a.top_p > 0.0f) || !(a.top_p < 1.0f)) return false;
     if (a.top_k > 0 && a.top_k < (uint64_t)a.V) return false;
-    if (a.penalty != 1.0f && a.gen_ids != nullptr && a.gen_off != nullptr &&
-        a.gen_off[row + 1] > a.gen_off[row])
+    int64_t g0 = 0, g1 = 0;
+    if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0)
         return false;
     return true;
 }
@@ -897,13 +897,13 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const int le = he ? (__ffsll((long long)he) - 1) : 0;
     if (l == le) {
         const uint32_t tok = (u == 0.0) ? 0u : ide;  // r == 0 stops the reference's walk at index 0
-        a.tokens[row] = tok;
+        emit_token(a, row, tok);
         if (a.stats) {
             const double prob = (u == 0.0) ? 0.0 : ee / zk;
             // 2^(R - M c): units of 2^R -> units of the max element's mass
             const double rho = (double)__builtin_amdgcn_exp2f(-fmaf(M, c, -R));
-            write_row_result(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zk / kS40 * rho,
-                             cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
+            write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zk / kS40 * rho,
+                            cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
         }
     }
     NIS_STS1(7);

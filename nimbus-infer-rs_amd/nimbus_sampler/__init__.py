@@ -34,7 +34,7 @@ EXPORTED_SYMBOLS = (
     "nis_ctx_create", "nis_ctx_destroy", "nis_ctx_set_stream", "nis_ctx_get_stream",
     "nis_last_error", "nis_status_string", "nis_rng_seed", "nis_rng_next_u64",
     "nis_rng_next_f64", "nis_rng_seed_batch", "nis_sample_batch", "nis_argmax_batch",
-    "nis_apply_repetition_penalty", "nis_sample_one", "nis_sync",
+    "nis_apply_repetition_penalty", "nis_sample_one", "nis_sync", "nis_decode_step",
 )
 
 
@@ -89,6 +89,9 @@ def load_library(path: str = LIB_PATH):
     L.nis_sample_batch.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                    ctypes.POINTER(NisParams), vp, vp, vp, vp, vp]
     L.nis_argmax_batch.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64, vp]
+    L.nis_decode_step.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                                  ctypes.POINTER(NisParams), vp, vp, ctypes.c_int64, vp, vp, vp,
+                                  ctypes.c_int32, vp, vp, vp]
     L.nis_apply_repetition_penalty.argtypes = [vp, vp, ctypes.c_int64, vp, ctypes.c_int64,
                                                ctypes.c_float]
     L.nis_sample_one.argtypes = [vp, vp, ctypes.c_int64, ctypes.POINTER(NisParams), vp,
@@ -215,6 +218,35 @@ class Sampler:
             ctypes.c_void_p(gen_ids.data_ptr()) if gen_ids is not None else None,
             ctypes.c_void_p(gen_offsets.data_ptr()) if gen_offsets is not None else None,
             ctypes.c_void_p(tokens.data_ptr()),
+            ctypes.c_void_p(stats.data_ptr()) if stats is not None else None)
+        _check(self._L, self._ctx, rc)
+        return tokens
+
+    def decode_step(self, logits, params: SamplingParams, rng_states, gen_ids, gen_len, max_new,
+                    done, stop_ids=None, V: Optional[int] = None, tokens=None, stats=None):
+        """One step of a batched decode loop (engine.rs:279-287) on device tensors.
+
+        gen_ids: int32 [B, cap] histories (also the penalty lists), gen_len:
+        int32 [B], max_new: int32 [B], done: uint8 [B], stop_ids: int32 [n]
+        (optional).  Sequences not yet done sample a token, append it and may
+        finish; done ones are skipped.  Returns the tokens tensor."""
+        import torch
+        assert logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1
+        assert gen_ids.dim() == 2 and gen_ids.stride(1) == 1
+        B = logits.shape[0]
+        V = logits.shape[1] if V is None else V
+        if tokens is None:
+            tokens = torch.empty(B, dtype=torch.int32, device=logits.device)
+        self._bind_stream()
+        p = params.to_c() if isinstance(params, SamplingParams) else params
+        n_stop = 0 if stop_ids is None else int(stop_ids.numel())
+        rc = self._L.nis_decode_step(
+            self._ctx, ctypes.c_void_p(logits.data_ptr()), logits.stride(0), B, V, ctypes.byref(p),
+            ctypes.c_void_p(rng_states.data_ptr()) if rng_states is not None else None,
+            ctypes.c_void_p(gen_ids.data_ptr()), gen_ids.stride(0),
+            ctypes.c_void_p(gen_len.data_ptr()), ctypes.c_void_p(max_new.data_ptr()),
+            ctypes.c_void_p(stop_ids.data_ptr()) if n_stop else None, n_stop,
+            ctypes.c_void_p(done.data_ptr()), ctypes.c_void_p(tokens.data_ptr()),
             ctypes.c_void_p(stats.data_ptr()) if stats is not None else None)
         _check(self._L, self._ctx, rc)
         return tokens

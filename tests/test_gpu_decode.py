@@ -1,0 +1,128 @@
+"""GPU parity of nis_decode_step: the batched decode loop of
+Engine::generate_ids (engine.rs:279-287) with the model step replaced by
+seeded synthetic logits, against the same loop over the CPU oracle's sample().
+
+Each sequence keeps its history on the device (it is also the penalty list,
+as `generated` is in the reference), stops on a stop id or on its budget,
+and is skipped once done (no token, RNG not advanced).
+"""
+import numpy as np
+import pytest
+
+from parity_util import BOUNDARY
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    import nimbus_sampler as ns
+    s = ns.Sampler(0)
+    yield s
+    s.close()
+
+
+def _run(sampler, B, V, steps, cap, params_kw, seed):
+    import torch
+    import nimbus_sampler as ns
+    from oracle import oracle
+
+    rnd = np.random.Generator(np.random.PCG64(seed))
+    seeds = list(range(500, 500 + B))
+    max_new = rnd.integers(0, steps + 1, size=B).astype(np.int32)
+    max_new[:3] = [0, 1, steps]
+    stop = rnd.choice(V, size=3, replace=False).astype(np.uint32)
+    logits = (rnd.standard_normal((steps, B, V), dtype=np.float32) * np.float32(2.0))
+    # plant a stop id on top of some rows at some steps, so sequences stop early
+    for s in range(steps):
+        rows = rnd.choice(B, size=B // 6, replace=False)
+        logits[s, rows, stop[s % 3]] += np.float32(14.0)
+
+    dev = torch.device("cuda:0")
+    params = ns.SamplingParams(**params_kw)
+    states = torch.from_numpy(ns.rng_states(seeds).view(np.int64)).to(dev)
+    gen_ids = torch.zeros((B, cap), dtype=torch.int32, device=dev)
+    gen_len = torch.zeros(B, dtype=torch.int32, device=dev)
+    maxn = torch.from_numpy(max_new).to(dev)
+    done = torch.from_numpy((max_new <= 0).astype(np.uint8)).to(dev)
+    stop_d = torch.from_numpy(stop.view(np.int32)).to(dev)
+    tokens = torch.full((B,), -1, dtype=torch.int32, device=dev)
+    gpu_tokens = []
+    for s in range(steps):
+        tokens.fill_(-1)
+        x = torch.from_numpy(np.ascontiguousarray(logits[s])).to(dev)
+        sampler.decode_step(x, params, states, gen_ids, gen_len, maxn, done, stop_d, tokens=tokens)
+        gpu_tokens.append(tokens.cpu().numpy().view(np.uint32).copy())
+    torch.cuda.synchronize()
+    g_len = gen_len.cpu().numpy()
+    g_ids = gen_ids.cpu().numpy().view(np.uint32)
+    g_done = done.cpu().numpy()
+    g_states = states.cpu().numpy().view(np.uint64)
+
+    p = oracle.make_params(params.temperature, params.top_p, params.top_k,
+                           params.repetition_penalty)
+    diverged = 0
+    for b in range(B):
+        rng = oracle.Rng(seeds[b])
+        generated = []
+        fin = max_new[b] <= 0
+        ok = True
+        for s in range(steps):
+            if fin:
+                assert gpu_tokens[s][b] == 0xFFFFFFFF, (b, s, "done row got a token")
+                continue
+            tok, st = oracle.sample(logits[s, b], p, generated, rng)
+            if gpu_tokens[s][b] != tok:
+                # allowed only on the oracle's own top-p / CDF boundary; the
+                # histories differ from there on, so the row is not compared further
+                assert params.temperature > 0.0 and \
+                    min(st["topp_margin"], st["cdf_margin"]) <= BOUNDARY, \
+                    (b, s, gpu_tokens[s][b], tok)
+                ok = False
+                diverged += 1
+                break
+            generated.append(tok)
+            fin = tok in set(stop.tolist()) or len(generated) >= max_new[b] or len(generated) >= cap
+        if not ok:
+            continue
+        assert g_len[b] == len(generated), (b, g_len[b], len(generated))
+        assert list(g_ids[b, :g_len[b]]) == generated, b
+        assert bool(g_done[b]) == fin, (b, g_done[b], fin)
+        assert np.array_equal(g_states[b], np.array(rng.words(), dtype=np.uint64)), b
+    return diverged, int(g_done.sum()), int((g_len > 0).sum())
+
+
+@pytest.mark.parametrize("V,kw", [
+    (4096, dict(temperature=0.9, top_p=0.9, repetition_penalty=1.3)),
+    (4096, dict(temperature=0.7, top_k=40, repetition_penalty=0.8)),
+    (50257, dict(temperature=0.8, top_p=0.9)),
+    (50257, dict(temperature=0.0, repetition_penalty=1.2)),
+])
+def test_decode_steps_match_oracle_loop(sampler, V, kw):
+    diverged, n_done, n_started = _run(sampler, B=24, V=V, steps=7, cap=8, params_kw=kw,
+                                       seed=V + int(10 * kw["temperature"]))
+    print(f"[decode] V={V} {kw} diverged_at_boundary={diverged} done={n_done} "
+          f"started={n_started}", flush=True)
+    assert diverged <= 1
+    assert n_done > 0 and n_started > 0
+
+
+def test_decode_step_rejects_bad_arguments(sampler):
+    import ctypes
+    import torch
+    import nimbus_sampler as ns
+    dev = torch.device("cuda:0")
+    x = torch.zeros((2, 300), dtype=torch.float32, device=dev)
+    st = torch.zeros((2, 4), dtype=torch.int64, device=dev)
+    ids = torch.zeros((2, 4), dtype=torch.int32, device=dev)
+    n = torch.zeros(2, dtype=torch.int32, device=dev)
+    d = torch.zeros(2, dtype=torch.uint8, device=dev)
+    p = ns.SamplingParams().to_c()
+    L = ns.load_library()
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    base = [sampler._ctx, ptr(x), 300, 2, 300, ctypes.byref(p), ptr(st), ptr(ids)]
+    # gen_cap 0, a missing length array, a negative stop count
+    assert L.nis_decode_step(*base, 0, ptr(n), ptr(n), None, 0, ptr(d), ptr(n), None) == ns.NIS_EINVAL
+    assert L.nis_decode_step(*base, 4, None, ptr(n), None, 0, ptr(d), ptr(n), None) == ns.NIS_EINVAL
+    assert L.nis_decode_step(*base, 4, ptr(n), ptr(n), None, -1, ptr(d), ptr(n), None) == ns.NIS_EINVAL
+    assert L.nis_decode_step(*base, 4, ptr(n), ptr(n), None, 2, ptr(d), ptr(n), None) == ns.NIS_EINVAL
