@@ -121,6 +121,17 @@ class Sampler {
                                d_tokens, d_stats),
               "sample_batch");
     }
+    // One step of a batched decode loop (engine.rs:279-287): see nis_decode_step.
+    void decode_step(const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     const SamplingParams& params, uint64_t* d_rng_state, uint32_t* d_gen_ids,
+                     int64_t gen_cap, int32_t* d_gen_len, const int32_t* d_max_new,
+                     const uint32_t* d_stop_ids, int32_t n_stop, uint8_t* d_done,
+                     uint32_t* d_tokens, nis_row_stats* d_stats = nullptr) {
+        const nis_params p = params.to_c();
+        check(nis_decode_step(ctx_, d_logits, ld, B, V, &p, d_rng_state, d_gen_ids, gen_cap,
+                              d_gen_len, d_max_new, d_stop_ids, n_stop, d_done, d_tokens, d_stats),
+              "decode_step");
+    }
     void argmax_batch(const float* d_logits, int64_t ld, int32_t B, int64_t V, uint32_t* d_tokens) {
         check(nis_argmax_batch(ctx_, d_logits, ld, B, V, d_tokens), "argmax_batch");
     }
