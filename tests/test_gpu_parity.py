@@ -248,6 +248,23 @@ def test_sparse_kernel_distribution_sweep(sampler, sigma):
                    label=f"sweep-s{sigma}-T{T}-p{p}")
 
 
+def test_sparse_kernel_bucket_edges_and_wide_ties(sampler):
+    # headline-like logits rounded to a 1/32 lattice with T = log2(e)/2, so
+    # x*c sits on (or a hair off) the sparse kernel's 1/64-octave bucket
+    # edges and each occupied bucket near the cutoff is a tie group of ~10
+    # tokens spread over the waves: bucket assignment must agree between the
+    # histogram, the kept sums and the walk, and the cutoff bucket's members
+    # are ranked by index across waves
+    rnd = np.random.Generator(np.random.PCG64(64))
+    B, V = 32, 50257
+    x = (np.round(rnd.standard_normal((B, V)) * 3.0 * 32.0) / 32.0).astype(np.float32)
+    T = float(np.float32(1.4426950408889634 / 2.0))
+    for p in (0.5, 0.9):
+        rep = _check(sampler, x, V, _params(temperature=T, top_p=p), list(range(B)),
+                     label=f"edges-p{p}")
+        assert rep["sparse_rows"] >= B // 2, rep
+
+
 def test_penalty_and_top_k_full_vocab(sampler):
     rnd = np.random.Generator(np.random.PCG64(77))
     B, V = 48, 50257
