@@ -57,10 +57,7 @@ constexpr int kSB = 1024;                   // lanes per workgroup
 constexpr int kSW = kSB / 64;               // waves per workgroup
 constexpr int kSN = 13;                     // float4 chunks per lane (at most)
 constexpr int kSMaxV = kSB * 4 * 13 - 3;    // 53245: 208 chunks of 64 float4 slots
-#ifndef NIS_SD
-#define NIS_SD 3
-#endif
-constexpr int kSD = NIS_SD;                 // loads in flight per lane ahead of the one in use
+constexpr int kSD = 3;                      // loads in flight per lane ahead of the one in use
 constexpr int kSS = 4;                      // sample chunks per wave
 constexpr uint32_t kSTop = 44;              // sampled float4 maxima allowed above thc_w
 constexpr int kSE = 256;                    // listed float4s per wave
@@ -545,12 +542,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
 
     // ---- stream end: compact this wave's candidates ----------------------
     NIS_STS(1);
-#ifdef NIS_EXPERIMENT_STREAM_ONLY
-    lds_barrier();
-    NIS_STS(2);
-    NIS_TFLUSH();
-    return NIS_REJECT_CAPACITY;
-#endif
     __builtin_amdgcn_s_setprio(0);
     mx = wmax_f32(mx);
     z = wsum_f64(z);
