@@ -187,10 +187,6 @@ __device__ unsigned long long nis_phase_ts[8192 * 16];
     } while (0)
 #endif
 
-#ifndef NIS_SETPRIO
-#define NIS_SETPRIO() __builtin_amdgcn_s_setprio(2)
-#endif
-
 // Workgroup barrier that orders LDS only, so global loads still in flight
 // are not drained by it.
 __device__ __forceinline__ void lds_barrier() {
@@ -616,7 +612,7 @@ __device__ __forceinline__ uint32_t fast_row(const RowArgs a, const int row, Fas
     // at a raised priority, ahead of the first half's work on the same
     // SIMDs once its data arrives.
     if (w >= kWaves / 2) {
-        NIS_SETPRIO();
+        __builtin_amdgcn_s_setprio(2);
     } else {
         for (int i = tid; i < kHB + 64; i += kBlock / 2) sh.s.hist[i] = 0ull;
         if (tid < 32 + 64) sh.s.chist[tid] = 0ull;
