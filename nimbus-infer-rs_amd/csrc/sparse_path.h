@@ -540,7 +540,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
 #undef NIS_SLOAD
 #undef NIS_SFIX
 
-    // ---- stream end: compact this wave's candidates ----------------------
+    // ---- stream end: this wave's candidates into the histograms ----------
     NIS_STS(1);
     __builtin_amdgcn_s_setprio(0);
     mx = wmax_f32(mx);
