@@ -80,6 +80,8 @@ def test_status_strings_and_null_context():
     p = ns.SamplingParams().to_c()
     assert L.nis_sample_batch(None, None, 1, 1, 1, ctypes.byref(p), None, None, None, None,
                               None) == ns.NIS_EINVAL
+    assert L.nis_decode_step(None, None, 1, 1, 1, ctypes.byref(p), None, None, 1, None, None,
+                             None, 0, None, None, None) == ns.NIS_EINVAL
     assert L.nis_sync(None) == ns.NIS_EINVAL
     assert L.nis_ctx_create(0, None) == ns.NIS_EINVAL
 
