@@ -126,3 +126,61 @@ def test_decode_step_rejects_bad_arguments(sampler):
     assert L.nis_decode_step(*base, 4, None, ptr(n), None, 0, ptr(d), ptr(n), None) == ns.NIS_EINVAL
     assert L.nis_decode_step(*base, 4, ptr(n), ptr(n), None, -1, ptr(d), ptr(n), None) == ns.NIS_EINVAL
     assert L.nis_decode_step(*base, 4, ptr(n), ptr(n), None, 2, ptr(d), ptr(n), None) == ns.NIS_EINVAL
+
+
+def test_graph_replays_match_eager_calls(sampler):
+    # sample_batch and decode_step captured in a HIP graph: every replay, with
+    # eager work and synchronizations between replays, matches the eager call
+    # sequence (tokens, RNG states, histories, lengths, flags)
+    import torch
+    import nimbus_sampler as ns
+    from nimbus_sampler import workloads
+    dev = torch.device("cuda:0")
+    w = workloads.WORKLOADS["headline"]
+    B, V, cap = 64, w.V, 8
+    x = torch.from_numpy(w.make(w.B)[:B].copy()).to(dev)
+    params = ns.SamplingParams(temperature=w.temperature, top_p=w.top_p)
+    seeds = list(range(B))
+
+    def fresh():
+        return dict(st=torch.from_numpy(ns.rng_states(seeds).view(np.int64)).to(dev),
+                    ids=torch.zeros((B, cap), dtype=torch.int32, device=dev),
+                    n=torch.zeros(B, dtype=torch.int32, device=dev),
+                    mx=torch.full((B,), 5, dtype=torch.int32, device=dev),
+                    d=torch.zeros(B, dtype=torch.uint8, device=dev),
+                    tok=torch.zeros(B, dtype=torch.int32, device=dev),
+                    tok2=torch.zeros(B, dtype=torch.int32, device=dev))
+
+    def step(s):
+        sampler.sample_batch(x, params, s["st"], tokens=s["tok"])
+        sampler.decode_step(x, params, s["st"], s["ids"], s["n"], s["mx"], s["d"], tokens=s["tok2"])
+
+    def snap(s):
+        return [t.clone().cpu() for t in (s["tok"], s["tok2"], s["st"], s["ids"], s["n"], s["d"])]
+
+    eager = fresh()
+    ref = []
+    for _ in range(3):
+        step(eager)
+        torch.cuda.synchronize()
+        ref.append(snap(eager))
+    # each step advances the states, so a replay that re-ran stale work would differ
+    assert not torch.equal(ref[0][2], ref[1][2]) and not torch.equal(ref[1][2], ref[2][2])
+
+    g_state = fresh()
+    graph = torch.cuda.CUDAGraph()
+    cap_stream = torch.cuda.Stream()
+    cap_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap_stream):
+        with torch.cuda.graph(graph, stream=cap_stream):
+            step(g_state)
+    torch.cuda.current_stream().wait_stream(cap_stream)
+    torch.cuda.synchronize()
+    for k in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        got = snap(g_state)
+        for a, b in zip(got, ref[k]):
+            assert torch.equal(a, b), k
+        _ = (x * 2.0).sum().item()  # eager work between replays
+        torch.cuda.synchronize()
