@@ -39,6 +39,8 @@ extern "C" {
 /* Largest supported vocabulary (the penalty bitmap lives in LDS). */
 #define NIS_MAX_V (1 << 20)
 #define NIS_MAX_B (1 << 24)
+/* Largest hidden size accepted by nis_lm_head_logits. */
+#define NIS_MAX_H (1 << 20)
 
 /* Sampling knobs of SamplingParams (sampler.rs:7-15), same f32 types:
  * temperature (sampler.rs:9; greedy iff <= 0, sampler.rs:32-34), top_k
@@ -164,6 +166,33 @@ int nis_apply_repetition_penalty(nis_ctx* ctx, double* d_logits, int64_t V,
 int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_params* params,
                    const uint32_t* h_generated, int64_t n_generated, uint64_t state_inout[4],
                    uint32_t* token_out);
+
+/* LM-head weight formats (quant.rs:13-25): dense f32 rows; int8 codes stored
+ * as value + 128 in bytes; int4 codes stored as value + 8, two per byte, low
+ * nibble first over the global index row * H + k. */
+#define NIS_W_F32 0
+#define NIS_W_INT8 8
+#define NIS_W_INT4 4
+
+typedef struct nis_weights {
+    int32_t format;         /* NIS_W_F32, NIS_W_INT8 or NIS_W_INT4 */
+    int32_t group_size;     /* 0: one scale per row; else one per group_size input channels */
+    const void* d_data;     /* [V][H] f32 / u8, or ceil(V*H/2) packed bytes */
+    const float* d_scales;  /* [V] or [V][H/group_size]; unused for f32 */
+} nis_weights;
+
+/* The logits producer before sampling: d_logits[b*ld + v] = dot(d_hidden[b*ldh ..], W[v])
+ * for B last-hidden rows, i.e. Model::logits_last (model.rs:317-325) through
+ * Mat::gemv_into (model.rs:65-86) on a dense row (simd.rs:22) or
+ * QuantMatrix::dot_rows_into (quant.rs:121-161): a per-row scale multiplies
+ * the row's dot product, group scales each group's.  Sums are f32 in the
+ * library's own order (the reference's is its SIMD lane order): each logit is
+ * within the f32 error bound of a length-H sum of its exact value.  int4
+ * needs an even H and group size (the reference's reader assumes even nibble
+ * offsets).  Asynchronous on the context stream; the output feeds
+ * nis_sample_batch / nis_decode_step on the same stream. */
+int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t B, int32_t H,
+                       const nis_weights* w, int64_t V, float* d_logits, int64_t ld);
 
 /* Wait for all work queued on the context stream. */
 int nis_sync(nis_ctx* ctx);

@@ -11,6 +11,7 @@
 #include <string>
 
 #include "kernels.h"
+#include "lm_head.h"
 #include "nimbus_sampler.h"
 #include "rng.h"
 
@@ -115,6 +116,23 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
                            ctx->stream, a);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "sample kernel launch");
+}
+
+template <int FMT, bool VEC, bool GROUPED>
+void launch_lm_head_t(const nis::LmHeadArgs& a, int nb, dim3 grid, dim3 block, hipStream_t st) {
+    if (nb == 4)
+        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 4>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 1>), grid, block, 0, st, a);
+}
+
+template <int FMT>
+void launch_lm_head_f(const nis::LmHeadArgs& a, bool vec, bool grouped, int nb, dim3 grid,
+                      dim3 block, hipStream_t st) {
+    if (vec && grouped) launch_lm_head_t<FMT, true, true>(a, nb, grid, block, st);
+    else if (vec) launch_lm_head_t<FMT, true, false>(a, nb, grid, block, st);
+    else if (grouped) launch_lm_head_t<FMT, false, true>(a, nb, grid, block, st);
+    else launch_lm_head_t<FMT, false, false>(a, nb, grid, block, st);
 }
 
 }  // namespace
@@ -269,6 +287,67 @@ int nis_apply_repetition_penalty(nis_ctx* ctx, double* d_logits, int64_t V,
                        d_logits, V, d_generated, n_generated, (double)penalty);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "penalty kernel launch");
+}
+
+int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t B, int32_t H,
+                       const nis_weights* w, int64_t V, float* d_logits, int64_t ld) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_hidden || !w || !d_logits || !w->d_data) return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (B <= 0 || H <= 0 || V <= 0) return fail(ctx, NIS_EINVAL, "B, H and V must be positive");
+    if (ldh < H || ld < V) return fail(ctx, NIS_EINVAL, "ldh must be >= H and ld >= V");
+    if (B > NIS_MAX_B || V > NIS_MAX_V || H > NIS_MAX_H) return fail(ctx, NIS_ERANGE, "B, H or V too large");
+    const int fmt = w->format;
+    if (fmt != NIS_W_F32 && fmt != NIS_W_INT8 && fmt != NIS_W_INT4)
+        return fail(ctx, NIS_EINVAL, "unknown weight format");
+    const int32_t g = w->group_size;
+    if (fmt == NIS_W_F32) {
+        if (g != 0) return fail(ctx, NIS_EINVAL, "f32 weights take no group size");
+    } else {
+        if (!w->d_scales) return fail(ctx, NIS_EINVAL, "quantized weights need scales");
+        if (g < 0 || (g > 0 && H % g != 0)) return fail(ctx, NIS_EINVAL, "group size must divide H");
+        // the reference's int4 row / group reader starts at a low nibble
+        // (quant.rs:130-133, 150-152), which is its packing only at even offsets
+        if (fmt == NIS_W_INT4 && (H % 2 != 0 || g % 2 != 0))
+            return fail(ctx, NIS_EINVAL, "int4 weights need an even H and group size");
+    }
+    if (((uintptr_t)d_hidden & 3u) || ((uintptr_t)d_logits & 3u) || ((uintptr_t)w->d_scales & 3u) ||
+        (fmt == NIS_W_F32 && ((uintptr_t)w->d_data & 3u)))
+        return fail(ctx, NIS_EALIGN, "hidden, logits, scales and f32 weights must be 4-byte aligned");
+    DeviceGuard dg(ctx->device);
+    if (dg.status != hipSuccess) return hip_fail(ctx, dg.status, "hipSetDevice");
+
+    nis::LmHeadArgs a;
+    a.x = d_hidden;
+    a.ldx = ldh;
+    a.B = B;
+    a.H = H;
+    a.w = w->d_data;
+    a.scales = w->d_scales;
+    a.group = g > 0 ? g : H;
+    a.groups = H / a.group;
+    a.gmagic = (uint32_t)((((uint64_t)1 << 32) + (uint64_t)a.group - 1) / (uint64_t)a.group);
+    a.V = V;
+    a.out = d_logits;
+    a.ld = ld;
+    const bool grouped = fmt != NIS_W_F32 && a.groups > 1;
+    const uintptr_t wp = (uintptr_t)w->d_data;
+    const bool vec = H % 4 == 0 && ldh % 4 == 0 && ((uintptr_t)d_hidden & 15u) == 0 &&
+                     (!grouped || a.group % 4 == 0) &&
+                     ((fmt == NIS_W_F32 && (wp & 15u) == 0) || (fmt == NIS_W_INT8 && (wp & 3u) == 0) ||
+                      (fmt == NIS_W_INT4 && (wp & 1u) == 0));
+    // a wave: 64 vocab rows x 16*nb hidden rows; workgroups of 1 wave for
+    // small batches (spread over every CU), else 4 waves split along b first
+    const int nb = B > 16 ? 4 : 1;
+    const int64_t nbt = ((int64_t)B + 16 * nb - 1) / (16 * nb);
+    a.wb = nb == 1 ? 1 : (nbt >= 4 ? 4 : (nbt >= 2 ? 2 : 1));
+    a.wv = nb == 1 ? 1 : 4 / a.wb;
+    dim3 grid((unsigned)((nbt + a.wb - 1) / a.wb), (unsigned)((V + 64 * a.wv - 1) / (64 * a.wv)));
+    dim3 block((unsigned)(64 * a.wv * a.wb));
+    if (fmt == NIS_W_F32) launch_lm_head_f<nis::kLhF32>(a, vec, false, nb, grid, block, ctx->stream);
+    else if (fmt == NIS_W_INT8) launch_lm_head_f<nis::kLhInt8>(a, vec, grouped, nb, grid, block, ctx->stream);
+    else launch_lm_head_f<nis::kLhInt4>(a, vec, grouped, nb, grid, block, ctx->stream);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "lm_head kernel launch");
 }
 
 int nis_sync(nis_ctx* ctx) {

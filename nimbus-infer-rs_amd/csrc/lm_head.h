@@ -1,0 +1,228 @@
+// lm_head.h — the LM-head producer: logits[b][v] = dot(hidden[b], W[v]) for
+// B last-hidden rows, on the matrix cores.
+//
+// Reference: Model::logits_last (src/model.rs:317-325) calls Mat::gemv_into
+// (src/model.rs:65-86) on the LM head or the tied embedding; a dense row is
+// simd::dot_f32 (src/simd.rs:22), a quantized one QuantMatrix::dot_rows_into
+// (src/quant.rs:121-161): int8 biased bytes or int4 biased nibbles (low nibble
+// first over the global index row*H + k), one f32 scale per row applied to the
+// row's dot product, or one per group of input channels applied to each
+// group's partial dot product.
+//
+// Layout and tiling (gfx950):
+//   - v_mfma_f32_16x16x4_f32, A = 16 hidden rows (b), B = 16 weight rows (v):
+//     lane l holds row l%16 at reduction index l/16 of each operand, and
+//     D[b = 4*(l/16) + r][v = l%16] in accumulator r.  The reduction index is
+//     permuted so that a lane's four successive MFMAs use four consecutive h:
+//     each operand is one 16-byte load per lane per four MFMAs.
+//   - A wave owns 64 vocab rows x 16*NB hidden rows (4 x NB accumulator tiles)
+//     and walks h in chunks of 32 (two runs of 4 per lane, so one weight row's
+//     128-byte line is read by one instruction pair), with the next chunk's
+//     loads issued before the current chunk's MFMAs.
+//   - Quantized codes stay packed until the MFMAs of their chunk: int8 runs
+//     are one u32, int4 runs one u16; (code - bias) is exact in f32.  A
+//     per-row scale multiplies the finished dot product, as in the
+//     reference; a group scale multiplies each weight (same real value, one
+//     more rounding per term, inside the f32 error bound of the sum).
+//   - Stores: accumulator r of a tile is 4 hidden rows x 16 consecutive
+//     vocab entries, 64 contiguous bytes per row.
+// No LDS, no barriers: waves outside the problem return at once; every load
+// index is clamped into the operands and every store is masked.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nis {
+
+typedef float lh_f4 __attribute__((ext_vector_type(4)));
+
+enum { kLhF32 = 0, kLhInt4 = 4, kLhInt8 = 8 };
+
+struct LmHeadArgs {
+    const float* x;        // hidden [B][ldx]
+    int64_t ldx;
+    int32_t B;
+    int32_t H;
+    const void* w;         // weights, row v of H entries (f32, u8 or packed u4)
+    const float* scales;   // [V][groups] (quantized only)
+    int32_t group;         // group length (H when one scale per row)
+    int32_t groups;        // H / group
+    uint32_t gmagic;       // ceil(2^32 / group)
+    int32_t wv;            // waves of a workgroup along v (wv * wb waves)
+    int32_t wb;            // waves of a workgroup along b
+    int64_t V;
+    float* out;            // logits [B][ld]
+    int64_t ld;
+};
+
+// floor(h / group) for 0 <= h < 2^31: the product with ceil(2^32/group) is
+// exact or one too high.
+__device__ __forceinline__ int lh_group_of(const LmHeadArgs& a, int h) {
+    int q = (int)__umulhi((uint32_t)h, a.gmagic);
+    return q * a.group > h ? q - 1 : q;
+}
+
+__device__ __forceinline__ float lh_code(const LmHeadArgs& a, int64_t idx, int fmt) {
+    const uint8_t* q = (const uint8_t*)a.w;
+    if (fmt == kLhInt8) return (float)((int)q[idx] - 128);
+    uint8_t byte = q[idx >> 1];
+    return (float)((int)((idx & 1) ? (byte >> 4) : (byte & 15)) - 8);
+}
+
+// Hidden run h..h+3 of row `row` (zero past H).
+template <bool VEC>
+__device__ __forceinline__ lh_f4 lh_load_x(const LmHeadArgs& a, int64_t row, int h) {
+    lh_f4 r = {0.f, 0.f, 0.f, 0.f};
+    const float* p = a.x + row * a.ldx;
+    if (VEC) {
+        if (h < a.H) r = *(const lh_f4*)(p + h);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (h + e < a.H) r[e] = p[h + e];
+    }
+    return r;
+}
+
+// A weight run in flight: the raw 16 bytes / u32 / u16 and, for group scales,
+// the run's scale (a run never straddles a group when VEC holds).
+struct LhRun {
+    lh_f4 f;
+    uint32_t c;
+    float s;
+};
+
+template <int FMT, bool VEC, bool GROUPED>
+__device__ __forceinline__ LhRun lh_load_w(const LmHeadArgs& a, int64_t v, int h) {
+    LhRun r;
+    r.f = lh_f4{0.f, 0.f, 0.f, 0.f};
+    r.c = FMT == kLhInt8 ? 0x80808080u : 0x8888u;  // codes of 0.0 past H
+    r.s = 0.f;
+    const int64_t base = v * (int64_t)a.H;
+    if (VEC) {
+        if (h < a.H) {
+            if (FMT == kLhF32) {
+                r.f = *(const lh_f4*)((const float*)a.w + base + h);
+            } else if (FMT == kLhInt8) {
+                r.c = *(const uint32_t*)((const uint8_t*)a.w + base + h);
+            } else {
+                r.c = *(const uint16_t*)((const uint8_t*)a.w + ((base + h) >> 1));
+            }
+            if (GROUPED) r.s = a.scales[v * a.groups + lh_group_of(a, h)];
+        }
+    } else {
+        // any H, any group length: dequantized here, element by element
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (h + e >= a.H) continue;
+            if (FMT == kLhF32) {
+                r.f[e] = ((const float*)a.w)[base + h + e];
+            } else {
+                float c = lh_code(a, base + h + e, FMT);
+                r.f[e] = GROUPED ? c * a.scales[v * a.groups + lh_group_of(a, h + e)] : c;
+            }
+        }
+    }
+    return r;
+}
+
+template <int FMT, bool VEC, bool GROUPED>
+__device__ __forceinline__ lh_f4 lh_values(const LhRun& r) {
+    if (FMT == kLhF32 || !VEC) return r.f;
+    lh_f4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float c = FMT == kLhInt8 ? (float)((int)((r.c >> (8 * e)) & 255u) - 128)
+                                 : (float)((int)((r.c >> (4 * e)) & 15u) - 8);
+        w[e] = GROUPED ? c * r.s : c;
+    }
+    return w;
+}
+
+template <int FMT, bool VEC, bool GROUPED, int NB>
+__global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int64_t b0 = ((int64_t)blockIdx.x * a.wb + wave / a.wv) * (16 * NB);
+    const int64_t v0 = ((int64_t)blockIdx.y * a.wv + wave % a.wv) * 64;
+    if (b0 >= a.B || v0 >= a.V) return;
+
+    int64_t vrow[4], brow[NB];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vrow[j] = min(v0 + 16 * j + r16, a.V - 1);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) brow[i] = min(b0 + 16 * i + r16, (int64_t)a.B - 1);
+
+    lh_f4 acc[NB][4];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = lh_f4{0.f, 0.f, 0.f, 0.f};
+
+    lh_f4 xc[NB][2];
+    LhRun wc[4][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) xc[i][s] = lh_load_x<VEC>(a, brow[i], 16 * s + 4 * kq);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            wc[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], 16 * s + 4 * kq);
+    }
+    for (int h0 = 0; h0 < a.H; h0 += 32) {
+        lh_f4 xn[NB][2];
+        LhRun wn[4][2];
+        const int hn = h0 + 32;  // past H the loads return zeros / zero codes
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) xn[i][s] = lh_load_x<VEC>(a, brow[i], hn + 16 * s + 4 * kq);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wn[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hn + 16 * s + 4 * kq);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            lh_f4 wv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wv[j] = lh_values<FMT, VEC, GROUPED>(wc[j][s]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int i = 0; i < NB; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[i][s][c], wv[j][c],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) xc[i][s] = xn[i][s];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wc[j][s] = wn[j][s];
+        }
+    }
+
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t v = v0 + 16 * j + r16;
+        if (v >= a.V) continue;
+        const float sc = (FMT != kLhF32 && !GROUPED) ? a.scales[v] : 1.0f;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t b = b0 + 16 * i + 4 * kq + r;
+                if (b < a.B) {
+                    float y = acc[i][j][r];
+                    if (FMT != kLhF32 && !GROUPED) y *= sc;  // dot * scale (quant.rs:128)
+                    a.out[b * a.ld + v] = y;
+                }
+            }
+    }
+}
+
+}  // namespace nis

@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "nis_last_error", "nis_status_string", "nis_rng_seed", "nis_rng_next_u64",
     "nis_rng_next_f64", "nis_rng_seed_batch", "nis_sample_batch", "nis_argmax_batch",
     "nis_apply_repetition_penalty", "nis_sample_one", "nis_sync", "nis_decode_step",
+    "nis_lm_head_logits",
 )
 
 
@@ -42,6 +43,15 @@ class NisParams(ctypes.Structure):
     _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float),
                 ("repetition_penalty", ctypes.c_float), ("reserved", ctypes.c_uint32),
                 ("top_k", ctypes.c_uint64)]
+
+
+W_F32, W_INT8, W_INT4 = 0, 8, 4
+
+
+class NisWeights(ctypes.Structure):
+    """nis_weights: format, group size (0 = per row), data and scales pointers."""
+    _fields_ = [("format", ctypes.c_int32), ("group_size", ctypes.c_int32),
+                ("d_data", ctypes.c_void_p), ("d_scales", ctypes.c_void_p)]
 
 
 class SamplerError(RuntimeError):
@@ -92,6 +102,8 @@ def load_library(path: str = LIB_PATH):
     L.nis_decode_step.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                   ctypes.POINTER(NisParams), vp, vp, ctypes.c_int64, vp, vp, vp,
                                   ctypes.c_int32, vp, vp, vp]
+    L.nis_lm_head_logits.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                     ctypes.POINTER(NisWeights), ctypes.c_int64, vp, ctypes.c_int64]
     L.nis_apply_repetition_penalty.argtypes = [vp, vp, ctypes.c_int64, vp, ctypes.c_int64,
                                                ctypes.c_float]
     L.nis_sample_one.argtypes = [vp, vp, ctypes.c_int64, ctypes.POINTER(NisParams), vp,
@@ -250,6 +262,30 @@ class Sampler:
             ctypes.c_void_p(stats.data_ptr()) if stats is not None else None)
         _check(self._L, self._ctx, rc)
         return tokens
+
+    def lm_head_logits(self, hidden, fmt: int, data, V: int, scales=None, group_size: int = 0,
+                       out=None):
+        """Logits of B last-hidden rows (model.rs:317-325) on device tensors.
+
+        hidden: float32 [B, ldh] (unit column stride); data: the weights —
+        float32 [V, H] (W_F32), uint8 [V, H] biased codes (W_INT8) or uint8
+        [ceil(V*H/2)] packed nibbles (W_INT4); scales: float32 [V] or
+        [V, H/group_size].  out: optional float32 [B, ld >= V].  Returns out."""
+        import torch
+        assert hidden.dtype == torch.float32 and hidden.dim() == 2 and hidden.stride(1) == 1
+        B = hidden.shape[0]
+        H = hidden.shape[1]
+        if out is None:
+            out = torch.empty((B, V), dtype=torch.float32, device=hidden.device)
+        assert out.dtype == torch.float32 and out.stride(1) == 1
+        w = NisWeights(int(fmt), int(group_size), data.data_ptr(),
+                       scales.data_ptr() if scales is not None else None)
+        self._bind_stream()
+        rc = self._L.nis_lm_head_logits(self._ctx, ctypes.c_void_p(hidden.data_ptr()),
+                                        hidden.stride(0), B, H, ctypes.byref(w), V,
+                                        ctypes.c_void_p(out.data_ptr()), out.stride(0))
+        _check(self._L, self._ctx, rc)
+        return out
 
     def argmax_batch(self, logits, V: Optional[int] = None, tokens=None):
         import torch
