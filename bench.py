@@ -107,6 +107,95 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
                      "frac": alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS},
     }))
 
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def bench_lm_head(args):
+    """The logits producer (model.rs:317-325) on its own: B last-hidden rows
+    against a [V, H] head in the chosen weight format, K launches timed with
+    events on the stream the kernel runs on."""
+    import time
+    import numpy as np
+    import torch
+    import nimbus_sampler as ns
+    from nimbus_sampler import workloads
+
+    w = workloads.WORKLOADS[args.workload]
+    B, V, H = args.lm_b, w.V, args.lm_h
+    fmt = {"f32": ns.W_F32, "int8": ns.W_INT8, "int4": ns.W_INT4}[args.lm_head]
+    group = args.lm_group if fmt != ns.W_F32 else 0
+    dev = torch.device("cuda:0")
+    rnd = np.random.default_rng(0)
+    x = torch.from_numpy(rnd.standard_normal((B, H)).astype(np.float32)).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    groups = H // group if group else 1
+    if fmt == ns.W_F32:
+        data = torch.randn((V, H), generator=g, device=dev) * 0.05
+        wbytes = V * H * 4
+    else:
+        nbytes = V * H if fmt == ns.W_INT8 else (V * H + 1) // 2
+        data = torch.randint(0, 256, (nbytes,), generator=g, device=dev, dtype=torch.int32) \
+            .to(torch.uint8)
+        wbytes = nbytes + V * groups * 4
+    scales = torch.full((V * groups,), 0.01, dtype=torch.float32, device=dev) \
+        if fmt != ns.W_F32 else None
+    out = torch.empty((B, V), dtype=torch.float32, device=dev)
+    sampler = ns.Sampler(0)
+
+    def run():
+        sampler.lm_head_logits(x, fmt, data, V, scales=scales, group_size=group, out=out)
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    K = args.steps
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(K):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / K
+    flops = 2.0 * B * V * H
+    alg_bytes = wbytes + B * H * 4 + B * V * 4
+    t_mfma = flops / (MFMA_F32_PEAK_TFLOPS * 1e12)
+    t_hbm = alg_bytes / (HBM_PEAK_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        roof = {"bound": "mfma", "achieved": flops / (us * 1e-6) / 1e12,
+                "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": alg_bytes / (us * 1e-6) / 1e9,
+                "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["traffic"] = None
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the oracle's exact-sum restatement on a bounded sample of rows
+        from oracle import lm_head_oracle as lh
+        hd = data.cpu().numpy().reshape(-1)
+        sc = scales.cpu().numpy() if scales is not None else None
+        xs = x[:8].cpu().numpy()
+        t0 = time.perf_counter()
+        lh.lm_head_logits(xs, fmt, hd, sc, V, H, group or None)
+        dt = time.perf_counter() - t0
+        cpu = {"value": 8 / dt, "unit": "hidden rows/s", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": f"8 hidden rows, f64 numpy restatement (oracle)"}
+    print(json.dumps({
+        "metric": f"LM-head logits: hidden rows/s, B={B} x H={H} -> V={V}, {args.lm_head} weights"
+                  + (f" (groups of {group})" if group else ""),
+        "value": B / (us * 1e-6), "unit": "hidden rows/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic hidden rows and random weights, resident in HBM",
+        "config": {"workload": f"lm_head_{args.lm_head}", "B": B, "H": H, "V": V,
+                   "group_size": group, "alg_bytes": alg_bytes, "flops": flops},
+        "roofline": roof, "cpu_baseline": cpu,
+    }))
+    sampler.close()
+
 
 def main():
     ap = argparse.ArgumentParser()
@@ -121,6 +210,11 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="time nis_decode_step (sample + on-device history / stop / budget "
                          "update) on the workload instead, and print that line")
+    ap.add_argument("--lm-head", choices=("f32", "int8", "int4"), default=None,
+                    help="time the LM-head logits producer with these weights instead")
+    ap.add_argument("--lm-b", type=int, default=256, help="hidden rows for --lm-head")
+    ap.add_argument("--lm-h", type=int, default=768, help="hidden size for --lm-head")
+    ap.add_argument("--lm-group", type=int, default=0, help="group size for quantized --lm-head")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 4 plain device copies of MIB MiB (reads MIB, writes MIB) "
                          "to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -144,6 +238,10 @@ def main():
               "row sharding across GPUs is described in DESIGN.md). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.lm_head:
+        bench_lm_head(args)
+        return
 
     import numpy as np
     import torch

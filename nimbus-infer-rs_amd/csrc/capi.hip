@@ -135,6 +135,31 @@ void launch_lm_head_f(const nis::LmHeadArgs& a, bool vec, bool grouped, int nb, 
     else launch_lm_head_t<FMT, false, false>(a, nb, grid, block, st);
 }
 
+// The one-hidden-row GEMV (lm_head_row_kernel) when its shape holds: whole
+// 16-byte runs per row (H % R == 0), one scale per run, aligned operands and
+// at most KMAX runs per lane with 16 or 64 lanes per row.  Returns false to
+// leave the call to the matrix-core kernel.
+template <int FMT>
+bool launch_lm_head_row(const nis::LmHeadArgs& a, bool grouped, uintptr_t wp, hipStream_t st) {
+    constexpr int R = nis::LhRowCfg<FMT>::R;
+    constexpr int KMAX = nis::LhRowCfg<FMT>::KMAX;
+    if (a.H % R != 0 || (wp & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
+    if (grouped && a.group % R != 0) return false;
+    const int runs = a.H / R;
+    int log2L;
+    if ((runs + 15) / 16 <= KMAX) log2L = 4;
+    else if ((runs + 63) / 64 <= KMAX) log2L = 6;
+    else return false;
+    const int64_t rows_per_wave = (int64_t)(64 >> log2L) * nis::LhRowCfg<FMT>::ITER;
+    const int64_t waves = (a.V + rows_per_wave - 1) / rows_per_wave;
+    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if (grouped)
+        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, true>), grid, block, 0, st, a, log2L, runs);
+    else
+        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, false>), grid, block, 0, st, a, log2L, runs);
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -335,6 +360,14 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
                      (!grouped || a.group % 4 == 0) &&
                      ((fmt == NIS_W_F32 && (wp & 15u) == 0) || (fmt == NIS_W_INT8 && (wp & 3u) == 0) ||
                       (fmt == NIS_W_INT4 && (wp & 1u) == 0));
+    if (B == 1 && fmt == NIS_W_F32) {
+        if (launch_lm_head_row<nis::kLhF32>(a, false, wp, ctx->stream)) goto launched;
+    } else if (B == 1 && fmt == NIS_W_INT8) {
+        if (launch_lm_head_row<nis::kLhInt8>(a, grouped, wp, ctx->stream)) goto launched;
+    } else if (B == 1) {
+        if (launch_lm_head_row<nis::kLhInt4>(a, grouped, wp, ctx->stream)) goto launched;
+    }
+    {
     // a wave: 64 vocab rows x 16*nb hidden rows; workgroups of 1 wave for
     // small batches (spread over every CU), else 4 waves split along b first
     const int nb = B > 16 ? 4 : 1;
@@ -346,6 +379,8 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
     if (fmt == NIS_W_F32) launch_lm_head_f<nis::kLhF32>(a, vec, false, nb, grid, block, ctx->stream);
     else if (fmt == NIS_W_INT8) launch_lm_head_f<nis::kLhInt8>(a, vec, grouped, nb, grid, block, ctx->stream);
     else launch_lm_head_f<nis::kLhInt4>(a, vec, grouped, nb, grid, block, ctx->stream);
+    }
+launched:
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "lm_head kernel launch");
 }

@@ -225,4 +225,105 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
     }
 }
 
+// One hidden row (B = 1, the reference's own decode shape): matrix-core tiles
+// would pad it to 16 rows, so this is a VALU GEMV streaming the head once.
+// Each lane takes 16-byte weight runs (4 f32, 16 int8 or 32 int4 codes) at
+// fixed h positions j*R, j = li + k*L, of one weight row; L (16 or 64) lanes
+// share a row, 64/L rows per wave step, kLhIter steps per wave.  The lane's
+// hidden values for those positions stay in registers across the steps; the
+// runs of D steps are in flight while a step is summed; the L partial sums
+// of a row meet in an XOR butterfly (fixed order, deterministic).
+
+template <int FMT>
+struct LhRowCfg {
+    static constexpr int R = FMT == kLhF32 ? 4 : (FMT == kLhInt8 ? 16 : 32);  // h per run
+    static constexpr int KMAX = FMT == kLhInt4 ? 2 : 4;                        // runs per lane
+    // measured at H = 768, V = 50257: more steps per wave (fewer waves) or
+    // more steps in flight per wave were slower for every format
+    static constexpr int ITER = FMT == kLhInt4 ? 8 : 4;                        // wave steps
+    static constexpr int D = FMT == kLhInt8 ? 2 : ITER;                        // steps in flight
+};
+
+template <int FMT, bool GROUPED>
+__device__ __forceinline__ float lh_run_dot(const uint4& raw, const float* xr) {
+    constexpr int R = LhRowCfg<FMT>::R;
+    float part = 0.f;
+    const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int e = 0; e < R; ++e) {
+        float wv;
+        if (FMT == kLhF32) wv = __uint_as_float(wd[e]);
+        else if (FMT == kLhInt8) wv = (float)((int)((wd[e >> 2] >> (8 * (e & 3))) & 255u) - 128);
+        else wv = (float)((int)((wd[e >> 3] >> (4 * (e & 7))) & 15u) - 8);
+        part = fmaf(wv, xr[e], part);
+    }
+    return part;
+}
+
+template <int FMT, bool GROUPED>
+__global__ __launch_bounds__(256) void lm_head_row_kernel(LmHeadArgs a, int log2L, int runs) {
+    constexpr int R = LhRowCfg<FMT>::R;
+    constexpr int KMAX = LhRowCfg<FMT>::KMAX;
+    const int lane = threadIdx.x & 63;
+    const int L = 1 << log2L;
+    const int li = lane & (L - 1);
+    const int P = 64 >> log2L;
+    constexpr int ITER = LhRowCfg<FMT>::ITER;
+    const int64_t wave_row0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * P * ITER;
+    if (wave_row0 >= a.V) return;  // wave-uniform
+    const int gl = lane >> log2L;
+    const int64_t row_bytes = FMT == kLhF32 ? (int64_t)a.H * 4 : (FMT == kLhInt8 ? (int64_t)a.H : (int64_t)a.H / 2);
+
+    constexpr int D = LhRowCfg<FMT>::D;
+    uint4 ring[D][KMAX];
+    auto load_step = [&](int it, uint4* dst) {
+        const int64_t vl = min(wave_row0 + it * P + gl, a.V - 1);
+        const uint8_t* wrow = (const uint8_t*)a.w + vl * row_bytes;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+            const int j = li + k * L;
+            dst[k] = j < runs ? *(const uint4*)(wrow + (int64_t)j * 16) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+#pragma unroll
+    for (int it = 0; it < D; ++it) load_step(it, ring[it]);
+    float xr[KMAX][R];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        const int j = li + k * L;
+#pragma unroll
+        for (int q = 0; q < R / 4; ++q) {
+            lh_f4 xv = j < runs ? *(const lh_f4*)(a.x + (int64_t)j * R + 4 * q) : lh_f4{0.f, 0.f, 0.f, 0.f};
+            xr[k][4 * q] = xv[0];
+            xr[k][4 * q + 1] = xv[1];
+            xr[k][4 * q + 2] = xv[2];
+            xr[k][4 * q + 3] = xv[3];
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+        const int64_t v = wave_row0 + it * P + gl;
+        const int64_t vl = min(v, a.V - 1);
+        uint4 cur[KMAX];
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) cur[k] = ring[it % D][k];
+        if (it + D < ITER) load_step(it + D, ring[it % D]);
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+            const int j = li + k * L;
+            if (j < runs) {
+                const float part = lh_run_dot<FMT, GROUPED>(cur[k], xr[k]);
+                if (GROUPED) acc = fmaf(part, a.scales[vl * a.groups + lh_group_of(a, j * R)], acc);
+                else acc += part;
+            }
+        }
+        for (int off = L >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        if (li == 0 && v < a.V) {
+            if (FMT != kLhF32 && !GROUPED) acc *= a.scales[v];  // dot * scale (quant.rs:128)
+            a.out[v] = acc;
+        }
+    }
+}
+
 }  // namespace nis

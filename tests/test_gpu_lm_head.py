@@ -72,6 +72,17 @@ def _run(sampler, fmt, B, H, V, group=None, pad_h=0, pad_v=0, seed=0):
     (4, 64, 768, 2048, None, 0, 0),      # int4 per row
     (4, 2, 98, 77, 14, 0, 0),            # int4, H % 4 != 0: element path
     (4, 300, 256, 1500, 64, 0, 0),       # int4 grouped, more than one b tile along y
+    # one hidden row: the VALU GEMV (16 or 64 lanes per weight row) or, where
+    # its shape does not hold, the matrix-core kernel
+    (0, 1, 768, 50257, None, 0, 0),      # 64 lanes per row, 3 runs per lane
+    (8, 1, 768, 50257, None, 0, 0),      # 16 lanes per row
+    (8, 1, 768, 3001, 48, 0, 0),         # groups of 48 = 3 runs of 16
+    (4, 1, 768, 50257, 64, 0, 0),        # int4 groups of 64, 24 runs per row
+    (4, 1, 4096, 999, None, 0, 0),       # 64 lanes, 2 runs per lane
+    (0, 1, 1024, 777, None, 0, 0),       # 64 lanes, 4 runs per lane (the cap)
+    (0, 1, 4096, 300, None, 0, 0),       # over the cap: matrix-core kernel
+    (8, 1, 96, 130, 8, 0, 0),            # group 8 < run of 16: matrix-core kernel
+    (4, 1, 40, 65, None, 0, 0),          # H % 32 != 0: matrix-core kernel
 ])
 def test_lm_head_matches_exact_sum_within_f32_bound(sampler, fmt, B, H, V, group, pad_h, pad_v):
     worst = _run(sampler, fmt, B, H, V, group, pad_h, pad_v, seed=B + H + V)
