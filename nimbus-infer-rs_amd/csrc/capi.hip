@@ -12,6 +12,11 @@
 
 #include "kernels.h"
 #include "lm_head.h"
+
+// 16-row hidden tiles per matrix-core wave when B > 16 (4 or 2)
+#ifndef NIS_LH_NB
+#define NIS_LH_NB 4
+#endif
 #include "nimbus_sampler.h"
 #include "rng.h"
 
@@ -122,6 +127,8 @@ template <int FMT, bool VEC, bool GROUPED>
 void launch_lm_head_t(const nis::LmHeadArgs& a, int nb, dim3 grid, dim3 block, hipStream_t st) {
     if (nb == 4)
         hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 4>), grid, block, 0, st, a);
+    else if (nb == 2)
+        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 2>), grid, block, 0, st, a);
     else
         hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 1>), grid, block, 0, st, a);
 }
@@ -370,7 +377,7 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
     {
     // a wave: 64 vocab rows x 16*nb hidden rows; workgroups of 1 wave for
     // small batches (spread over every CU), else 4 waves split along b first
-    const int nb = B > 16 ? 4 : 1;
+    const int nb = B > 16 ? NIS_LH_NB : 1;
     const int64_t nbt = ((int64_t)B + 16 * nb - 1) / (16 * nb);
     a.wb = nb == 1 ? 1 : (nbt >= 4 ? 4 : (nbt >= 2 ? 2 : 1));
     a.wv = nb == 1 ? 1 : 4 / a.wb;
