@@ -50,6 +50,8 @@ def test_header_is_valid_c_with_expected_layouts(tmp_path):
         "_Static_assert(sizeof(nis_row_stats) == 64, \"nis_row_stats\");\n"
         "_Static_assert(offsetof(nis_row_stats, kept) == 40, \"kept\");\n"
         "_Static_assert(offsetof(nis_row_stats, path) == 48, \"path\");\n"
+        "_Static_assert(sizeof(nis_weights) == 24, \"nis_weights\");\n"
+        "_Static_assert(offsetof(nis_weights, d_data) == 8, \"d_data\");\n"
         "int main(void) { return 0; }\n")
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only",
                     "-I" + os.path.join(ROOT, "include"), str(src)], check=True)
@@ -57,6 +59,7 @@ def test_header_is_valid_c_with_expected_layouts(tmp_path):
     assert ctypes.sizeof(ns.NisParams) == 24
     assert ns.ROW_STATS_DTYPE.itemsize == 64
     assert ns.ROW_STATS_DTYPE.fields["kept"][1] == 40
+    assert ctypes.sizeof(ns.NisWeights) == 24 and ns.NisWeights.d_data.offset == 8
 
 
 def test_host_rng_matches_kats():
@@ -82,6 +85,8 @@ def test_status_strings_and_null_context():
                               None) == ns.NIS_EINVAL
     assert L.nis_decode_step(None, None, 1, 1, 1, ctypes.byref(p), None, None, 1, None, None,
                              None, 0, None, None, None) == ns.NIS_EINVAL
+    w = ns.NisWeights(ns.W_F32, 0, None, None)
+    assert L.nis_lm_head_logits(None, None, 1, 1, 1, ctypes.byref(w), 1, None, 1) == ns.NIS_EINVAL
     assert L.nis_sync(None) == ns.NIS_EINVAL
     assert L.nis_ctx_create(0, None) == ns.NIS_EINVAL
 
