@@ -121,6 +121,13 @@ class Sampler {
                                d_tokens, d_stats),
               "sample_batch");
     }
+    // Logits of B last-hidden rows (Model::logits_last, model.rs:317-325): see
+    // nis_lm_head_logits.  Asynchronous on the context stream.
+    void lm_head_logits(const float* d_hidden, int64_t ldh, int32_t B, int32_t H,
+                        const nis_weights& w, int64_t V, float* d_logits, int64_t ld) {
+        check(nis_lm_head_logits(ctx_, d_hidden, ldh, B, H, &w, V, d_logits, ld), "lm_head_logits");
+    }
+
     // One step of a batched decode loop (engine.rs:279-287): see nis_decode_step.
     void decode_step(const float* d_logits, int64_t ld, int32_t B, int64_t V,
                      const SamplingParams& params, uint64_t* d_rng_state, uint32_t* d_gen_ids,

@@ -132,6 +132,58 @@ static void sample_is_deterministic(nimbus::Sampler& s) {
     CHECK(b.state() == expect.state());
 }
 
+// simd.rs:183 dot_f32_matches_scalar and simd.rs:192 dot_i8_matches_reference,
+// through the LM-head producer (one weight row, one hidden row)
+static float lm_head_one(nimbus::Sampler& s, const std::vector<float>& x, const void* w,
+                         size_t wbytes, int32_t format) {
+    const int32_t H = (int32_t)x.size();
+    float *dx = nullptr, *ds = nullptr, *dout = nullptr;
+    void* dw = nullptr;
+    const float one = 1.0f;
+    CHECK(hipMalloc(&dx, x.size() * sizeof(float)) == hipSuccess);
+    CHECK(hipMalloc(&dw, wbytes) == hipSuccess);
+    CHECK(hipMalloc(&ds, sizeof one) == hipSuccess);
+    CHECK(hipMalloc(&dout, sizeof(float)) == hipSuccess);
+    CHECK(hipMemcpy(dx, x.data(), x.size() * sizeof(float), hipMemcpyHostToDevice) == hipSuccess);
+    CHECK(hipMemcpy(dw, w, wbytes, hipMemcpyHostToDevice) == hipSuccess);
+    CHECK(hipMemcpy(ds, &one, sizeof one, hipMemcpyHostToDevice) == hipSuccess);
+    nis_weights wt;
+    wt.format = format;
+    wt.group_size = 0;
+    wt.d_data = dw;
+    wt.d_scales = format == NIS_W_F32 ? nullptr : ds;
+    s.lm_head_logits(dx, H, 1, H, wt, 1, dout, 1);
+    s.sync();
+    float out = 0.0f;
+    CHECK(hipMemcpy(&out, dout, sizeof out, hipMemcpyDeviceToHost) == hipSuccess);
+    (void)hipFree(dx);
+    (void)hipFree(dw);
+    (void)hipFree(ds);
+    (void)hipFree(dout);
+    return out;
+}
+
+static void lm_head_matches_reference_dots(nimbus::Sampler& s) {
+    std::vector<float> a(257), b(257);
+    double exact = 0.0;
+    for (int i = 0; i < 257; ++i) {
+        a[i] = (float)i * 0.5f - 30.0f;
+        b[i] = 1.0f / ((float)i + 3.0f);
+        exact += (double)a[i] * (double)b[i];
+    }
+    CHECK(std::fabs(lm_head_one(s, a, b.data(), b.size() * sizeof(float), NIS_W_F32) - exact) < 1e-2);
+    std::vector<float> x(131);
+    std::vector<uint8_t> q(131);
+    exact = 0.0;
+    for (int i = 0; i < 131; ++i) {
+        x[i] = (float)i * 0.125f;
+        const int raw = (i * 7) % 255 - 128;
+        q[i] = (uint8_t)(raw + 128);
+        exact += (double)x[i] * raw;
+    }
+    CHECK(std::fabs(lm_head_one(s, x, q.data(), q.size(), NIS_W_INT8) - exact) < 1e-2);
+}
+
 static void errors_throw(nimbus::Sampler& s) {
     nimbus::SamplingParams p;
     nimbus::Rng rng(0);
@@ -156,6 +208,7 @@ int main(int argc, char** argv) {
         repetition_penalty(s);
         top_p_zero_keeps_argmax_only(s);
         sample_is_deterministic(s);
+        lm_head_matches_reference_dots(s);
         errors_throw(s);
     }
     std::printf("%s: %d failure(s)\n", gpu ? "gpu" : "cpu", g_failures);
