@@ -254,7 +254,12 @@ __device__ __forceinline__ float lh_run_dot(const uint4& raw, const float* xr) {
         float wv;
         if (FMT == kLhF32) wv = __uint_as_float(wd[e]);
         else if (FMT == kLhInt8) wv = (float)((int)((wd[e >> 2] >> (8 * (e & 3))) & 255u) - 128);
-        else wv = (float)((int)((wd[e >> 3] >> (4 * (e & 7))) & 15u) - 8);
+        else {
+            // nibble e of word e/8, taken from the even or odd nibbles spread
+            // one per byte, so the convert is a single byte-lane conversion
+            const uint32_t spread = (e & 1) ? ((wd[e >> 3] >> 4) & 0x0F0F0F0Fu) : (wd[e >> 3] & 0x0F0F0F0Fu);
+            wv = (float)((spread >> (8 * ((e & 7) >> 1))) & 255u) - 8.0f;
+        }
         part = fmaf(wv, xr[e], part);
     }
     return part;
