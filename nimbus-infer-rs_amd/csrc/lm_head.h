@@ -16,9 +16,9 @@
 //     permuted so that a lane's four successive MFMAs use four consecutive h:
 //     each operand is one 16-byte load per lane per four MFMAs.
 //   - A wave owns 64 vocab rows x 16*NB hidden rows (4 x NB accumulator tiles)
-//     and walks h in chunks of 32 (two runs of 4 per lane, so one weight row's
-//     128-byte line is read by one instruction pair), with the next chunk's
-//     loads issued before the current chunk's MFMAs.
+//     and walks h in chunks of 16 (f32) or 32 (packed codes: two runs of 4
+//     per lane), with the next chunk's loads issued before the current
+//     chunk's MFMAs.
 //   - Quantized codes stay packed until the MFMAs of their chunk: int8 runs
 //     are one u32, int4 runs one u16; (code - bias) is exact in f32.  A
 //     per-row scale multiplies the finished dot product, as in the
@@ -35,6 +35,7 @@
 namespace nis {
 
 typedef float lh_f4 __attribute__((ext_vector_type(4)));
+
 
 enum { kLhF32 = 0, kLhInt4 = 4, kLhInt8 = 8 };
 
@@ -141,6 +142,10 @@ __device__ __forceinline__ lh_f4 lh_values(const LhRun& r) {
 
 template <int FMT, bool VEC, bool GROUPED, int NB>
 __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
+    // runs of 4 h per lane per chunk: one for f32 (100 VGPRs, 3 waves per
+    // SIMD: 260 us at B = 256 against 281 with two), two for packed codes
+    // (their loads are narrower; one run was 4 % slower for int4)
+    constexpr int kLhRuns = FMT == kLhF32 ? 1 : 2;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r16 = lane & 15;
@@ -161,22 +166,22 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = lh_f4{0.f, 0.f, 0.f, 0.f};
 
-    lh_f4 xc[NB][2];
-    LhRun wc[4][2];
+    lh_f4 xc[NB][kLhRuns];
+    LhRun wc[4][kLhRuns];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < kLhRuns; ++s) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) xc[i][s] = lh_load_x<VEC>(a, brow[i], 16 * s + 4 * kq);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             wc[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], 16 * s + 4 * kq);
     }
-    for (int h0 = 0; h0 < a.H; h0 += 32) {
-        lh_f4 xn[NB][2];
-        LhRun wn[4][2];
-        const int hn = h0 + 32;  // past H the loads return zeros / zero codes
+    for (int h0 = 0; h0 < a.H; h0 += 16 * kLhRuns) {
+        lh_f4 xn[NB][kLhRuns];
+        LhRun wn[4][kLhRuns];
+        const int hn = h0 + 16 * kLhRuns;  // past H the loads return zeros / zero codes
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < kLhRuns; ++s) {
 #pragma unroll
             for (int i = 0; i < NB; ++i) xn[i][s] = lh_load_x<VEC>(a, brow[i], hn + 16 * s + 4 * kq);
 #pragma unroll
@@ -184,7 +189,7 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
                 wn[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hn + 16 * s + 4 * kq);
         }
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < kLhRuns; ++s) {
             lh_f4 wv[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) wv[j] = lh_values<FMT, VEC, GROUPED>(wc[j][s]);
@@ -198,7 +203,7 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
                                                                          acc[i][j], 0, 0, 0);
         }
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < kLhRuns; ++s) {
 #pragma unroll
             for (int i = 0; i < NB; ++i) xc[i][s] = xn[i][s];
 #pragma unroll
