@@ -140,3 +140,21 @@ def test_lm_head_feeds_sampler(sampler):
            st.cpu().numpy().view(np.uint64))
     rep = compare(gpu, run_oracle(host, V, params, seeds), greedy=False)
     print(f"[lm_head->sample] {rep}", flush=True)
+
+
+def test_bench_kernel_cli_checks_match_oracle():
+    # the reference's bench-kernel workload through the CLI: each y[0] check
+    # equals the exact dot of its format within the f32 bound (+ the JSON's
+    # 4-decimal rounding)
+    from nimbus_sampler import cli
+    from oracle import lm_head_oracle as lh
+    res = cli.bench_kernel(steps=2, warmup=1)
+    print(f"[bench-kernel] {res}", flush=True)
+    x, w_f32, w_i8, w_i4 = cli.reference_kernel_inputs()
+    ones = np.ones(1, np.float32)
+    for fmt, data, check in ((lh.FMT_F32, w_f32[:768], res["checks"][0]),
+                             (lh.FMT_INT8, w_i8[:768], res["checks"][1]),
+                             (lh.FMT_INT4, w_i4[:384], res["checks"][2])):
+        exact, absd = lh.lm_head_logits(x[None, :], fmt, data, ones, 1, 768)
+        assert abs(check - exact[0, 0]) <= lh.f32_bound(absd[0, 0], 768) + 5e-5, (fmt, check, exact)
+    assert all(res[f"{k}_gflops"] > 0 for k in ("f32", "int8", "int4"))
