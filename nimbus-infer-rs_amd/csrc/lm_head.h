@@ -48,7 +48,7 @@ struct LmHeadArgs {
     const float* scales;   // [V][groups] (quantized only)
     int32_t group;         // group length (H when one scale per row)
     int32_t groups;        // H / group
-    uint32_t gmagic;       // ceil(2^32 / group)
+    uint32_t gmagic;       // ceil(2^32 / group); 0 for group 1 (2^32 does not fit)
     int32_t wv;            // waves of a workgroup along v (wv * wb waves)
     int32_t wb;            // waves of a workgroup along b
     int64_t V;
@@ -57,8 +57,9 @@ struct LmHeadArgs {
 };
 
 // floor(h / group) for 0 <= h < 2^31: the product with ceil(2^32/group) is
-// exact or one too high.
+// exact or one too high.  Group 1 (magic 0) is h itself.
 __device__ __forceinline__ int lh_group_of(const LmHeadArgs& a, int h) {
+    if (a.gmagic == 0u) return h;
     int q = (int)__umulhi((uint32_t)h, a.gmagic);
     return q * a.group > h ? q - 1 : q;
 }

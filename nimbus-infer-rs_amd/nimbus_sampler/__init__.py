@@ -277,7 +277,33 @@ class Sampler:
         H = hidden.shape[1]
         if out is None:
             out = torch.empty((B, V), dtype=torch.float32, device=hidden.device)
-        assert out.dtype == torch.float32 and out.stride(1) == 1
+        # the C ABI sees bare pointers: every size it will read is checked here
+        if out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1 or \
+                out.shape[0] < B or out.shape[1] < V:
+            raise SamplerError(NIS_EINVAL, "out must be float32 [>= B, >= V] with unit column stride")
+        fmt, group_size = int(fmt), int(group_size)
+        if fmt == W_F32:
+            need, ddtype = V * H, torch.float32
+        elif fmt == W_INT8:
+            need, ddtype = V * H, torch.uint8
+        elif fmt == W_INT4:
+            need, ddtype = (V * H + 1) // 2, torch.uint8
+        else:
+            raise SamplerError(NIS_EINVAL, f"unknown weight format {fmt}")
+        if data.dtype != ddtype or not data.is_contiguous() or data.numel() < need:
+            raise SamplerError(NIS_EINVAL, f"weights must be contiguous {ddtype} with at least "
+                                           f"{need} elements (got {data.dtype}, {data.numel()})")
+        tensors = [hidden, data, out]
+        if fmt != W_F32:
+            groups = H // group_size if group_size > 0 and H % group_size == 0 else 1
+            if scales is None or scales.dtype != torch.float32 or not scales.is_contiguous() or \
+                    scales.numel() < V * groups:
+                raise SamplerError(NIS_EINVAL, f"scales must be contiguous float32 with at least "
+                                               f"{V * groups} elements")
+            tensors.append(scales)
+        dev = torch.device("cuda", self.device)
+        if any(t.device != dev for t in tensors):
+            raise SamplerError(NIS_EINVAL, f"hidden, weights, scales and out must be on {dev}")
         w = NisWeights(int(fmt), int(group_size), data.data_ptr(),
                        scales.data_ptr() if scales is not None else None)
         self._bind_stream()

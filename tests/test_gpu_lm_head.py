@@ -82,6 +82,8 @@ def _run(sampler, fmt, B, H, V, group=None, pad_h=0, pad_v=0, seed=0):
     (0, 1, 1024, 777, None, 0, 0),       # 64 lanes, 4 runs per lane (the cap)
     (0, 1, 4096, 300, None, 0, 0),       # over the cap: matrix-core kernel
     (8, 1, 96, 130, 8, 0, 0),            # group 8 < run of 16: matrix-core kernel
+    (8, 3, 40, 77, 1, 0, 0),             # int8, one scale per weight (group 1)
+    (8, 1, 40, 77, 1, 0, 0),             # the same through the one-row dispatch
     (4, 1, 40, 65, None, 0, 0),          # H % 32 != 0: matrix-core kernel
 ])
 def test_lm_head_matches_exact_sum_within_f32_bound(sampler, fmt, B, H, V, group, pad_h, pad_v):
