@@ -7,11 +7,15 @@ Bar (per row, from the oracle's own margins):
     top-p decision margin |cum_excl - q - p| or its CDF margin
     |r - prefix| / total is <= 1e-6 (such rows are counted, not failed);
   - kept-set size: equal unless the top-p margin is <= 1e-6;
-  - probability of the drawn token and the kept mass: within 1e-6 relative.
+  - probability of the drawn token and the kept mass: within 1e-6 relative;
+  - a sampled-id mismatch is allowed only where the oracle's margin is at
+    most 3e-7 (STRICT_BOUNDARY), three times the GPU's measured mass error
+    (~1e-7), although any row within 1e-6 is counted as a boundary row.
 """
 import numpy as np
 
 BOUNDARY = 1e-6
+STRICT_BOUNDARY = 3e-7
 PROB_RTOL = 1e-6
 
 
@@ -92,6 +96,11 @@ def compare(gpu, ref, greedy):
         rep["max_zkept_rel_err"] = float(rel_z.max())
         assert rel_p.max() <= PROB_RTOL, f"prob rel err {rel_p.max()}"
         assert rel_z.max() <= PROB_RTOL, f"z_kept rel err {rel_z.max()}"
+    margin = np.minimum(r_st["topp_margin"], r_st["cdf_margin"])
+    loose = np.nonzero(mism & (margin > STRICT_BOUNDARY))[0]
+    assert loose.size == 0, \
+        f"mismatch rows {loose[:10].tolist()} with oracle margins {margin[loose[:10]]} > {STRICT_BOUNDARY}"
+    rep["max_mismatch_margin"] = float(margin[mism].max()) if mism.any() else 0.0
     rep["sampled_mismatch"] = int(mism.sum())
     rep["topp_boundary_rows"] = int(topp_b.sum())
     rep["cdf_boundary_rows"] = int(cdf_b.sum())

@@ -41,7 +41,10 @@ def _run(sampler, B, V, steps, cap, params_kw, seed):
     dev = torch.device("cuda:0")
     params = ns.SamplingParams(**params_kw)
     states = torch.from_numpy(ns.rng_states(seeds).view(np.int64)).to(dev)
-    gen_ids = torch.zeros((B, cap), dtype=torch.int32, device=dev)
+    # one sentinel row past the B histories, and every unused slot, must stay untouched
+    SENT = 0x7F7F7F7F
+    gen_buf = torch.full((B + 1, cap), SENT, dtype=torch.int32, device=dev)
+    gen_ids = gen_buf[:B]
     gen_len = torch.zeros(B, dtype=torch.int32, device=dev)
     maxn = torch.from_numpy(max_new).to(dev)
     done = torch.from_numpy((max_new <= 0).astype(np.uint8)).to(dev)
@@ -55,7 +58,12 @@ def _run(sampler, B, V, steps, cap, params_kw, seed):
         gpu_tokens.append(tokens.cpu().numpy().view(np.uint32).copy())
     torch.cuda.synchronize()
     g_len = gen_len.cpu().numpy()
-    g_ids = gen_ids.cpu().numpy().view(np.uint32)
+    g_buf = gen_buf.cpu().numpy()
+    g_ids = g_buf[:B].view(np.uint32)
+    assert (g_buf[B] == SENT).all(), "history write past the last row"
+    for b in range(B):
+        assert (g_buf[b, g_len[b]:] == SENT).all(), (b, "history slot past gen_len written")
+    assert (g_len <= cap).all(), "history longer than its capacity"
     g_done = done.cpu().numpy()
     g_states = states.cpu().numpy().view(np.uint64)
 
@@ -89,22 +97,27 @@ def _run(sampler, B, V, steps, cap, params_kw, seed):
         assert list(g_ids[b, :g_len[b]]) == generated, b
         assert bool(g_done[b]) == fin, (b, g_done[b], fin)
         assert np.array_equal(g_states[b], np.array(rng.words(), dtype=np.uint64)), b
-    return diverged, int(g_done.sum()), int((g_len > 0).sum())
+    return diverged, int(g_done.sum()), int((g_len > 0).sum()), int((g_len == cap).sum())
 
 
-@pytest.mark.parametrize("V,kw", [
-    (4096, dict(temperature=0.9, top_p=0.9, repetition_penalty=1.3)),
-    (4096, dict(temperature=0.7, top_k=40, repetition_penalty=0.8)),
-    (50257, dict(temperature=0.8, top_p=0.9)),
-    (50257, dict(temperature=0.0, repetition_penalty=1.2)),
+@pytest.mark.parametrize("V,kw,cap", [
+    (4096, dict(temperature=0.9, top_p=0.9, repetition_penalty=1.3), 8),
+    (4096, dict(temperature=0.7, top_k=40, repetition_penalty=0.8), 8),
+    (50257, dict(temperature=0.8, top_p=0.9), 8),
+    (50257, dict(temperature=0.0, repetition_penalty=1.2), 8),
+    # histories smaller than the steps: a full history ends the sequence
+    (4096, dict(temperature=0.9, top_p=0.9, repetition_penalty=1.3), 3),
+    (50257, dict(temperature=0.8, top_p=0.9), 3),
 ])
-def test_decode_steps_match_oracle_loop(sampler, V, kw):
-    diverged, n_done, n_started = _run(sampler, B=24, V=V, steps=7, cap=8, params_kw=kw,
-                                       seed=V + int(10 * kw["temperature"]))
-    print(f"[decode] V={V} {kw} diverged_at_boundary={diverged} done={n_done} "
-          f"started={n_started}", flush=True)
+def test_decode_steps_match_oracle_loop(sampler, V, kw, cap):
+    diverged, n_done, n_started, n_full = _run(sampler, B=24, V=V, steps=7, cap=cap,
+                                               params_kw=kw, seed=V + int(10 * kw["temperature"]))
+    print(f"[decode] V={V} {kw} cap={cap} diverged_at_boundary={diverged} done={n_done} "
+          f"started={n_started} full={n_full}", flush=True)
     assert diverged <= 1
     assert n_done > 0 and n_started > 0
+    if cap < 7:
+        assert n_full > 0, "no history reached its capacity"
 
 
 def test_decode_step_rejects_bad_arguments(sampler):

@@ -1,0 +1,68 @@
+"""GPU parity where the drawn tokens lie far below the row maximum.
+
+One spike per row and every other logit 11-16 (scaled) nats below it, so the
+tail holds a large share of the mass and many rows draw a token 16-24 octaves
+below the maximum.  The mass 2^(t) of such a token must still match the
+oracle's exp(w - max) (sampler.rs:201-205) within 1e-6 relative: the
+probability of the drawn token and the kept mass are checked on every drawn
+row, at T = 1 and T = 0.3, with top-p off and at 0.99.
+"""
+import numpy as np
+import pytest
+
+from parity_util import compare, run_gpu, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    import nimbus_sampler as ns
+    s = ns.Sampler(0)
+    yield s
+    s.close()
+
+
+def deep_tail_rows(B, V, T, lo, hi, seed):
+    """Spike at a random index; others at spike - T * U[lo, hi) (scaled nats)."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    x = np.empty((B, V), dtype=np.float32)
+    for r in range(B):
+        spike = np.float32(g.uniform(-4.0, 12.0))
+        d = g.uniform(lo, hi, size=V) * T
+        x[r] = (np.float64(spike) - d).astype(np.float32)
+        x[r, int(g.integers(0, V))] = spike
+    return x
+
+
+def tail_depth_octaves(x, tokens, T):
+    """Octaves below the row max of each token (only rows where it was drawn)."""
+    m = x.max(axis=1).astype(np.float64)
+    t = x[np.arange(x.shape[0]), tokens].astype(np.float64)
+    return (m - t) / max(float(np.float32(T)), 1e-6) * np.log2(np.e)
+
+
+@pytest.mark.parametrize("V,T,top_p,lo,hi,B", [
+    (50257, 1.0, 1.0, 11.0, 13.0, 96),
+    (50257, 1.0, 0.99, 11.0, 13.0, 96),
+    (50257, 0.3, 1.0, 11.0, 13.0, 96),
+    (50257, 0.3, 0.99, 11.0, 16.0, 96),
+    (128256, 1.0, 1.0, 13.5, 14.5, 96),   # ~20 octaves deep, V of the Llama-3 vocabulary
+    (1 << 20, 1.0, 1.0, 15.5, 16.5, 128),  # 22-24 octaves deep at the largest V
+])
+def test_deep_tail_probabilities(sampler, V, T, top_p, lo, hi, B):
+    import nimbus_sampler as ns
+    x = deep_tail_rows(B, V, T, lo, hi, seed=V + int(100 * T) + int(100 * top_p))
+    params = ns.SamplingParams(temperature=T, top_p=top_p)
+    seeds = list(range(3000, 3000 + B))
+    print(f"[deep-tail] B={B} V={V} T={T} p={top_p} depth [{lo},{hi}) nats", flush=True)
+    gpu = run_gpu(sampler, x, V, params, seeds)
+    ref = run_oracle(x, V, params, seeds)
+    rep = compare(gpu, ref, greedy=False)
+    depth = tail_depth_octaves(x, ref[0], T)
+    drawn_deep = int((depth >= 16.0).sum())
+    rep["rows_drawing_16_octaves_deep"] = drawn_deep
+    rep["deepest_draw_octaves"] = float(depth.max())
+    print(f"[deep-tail] -> {rep}", flush=True)
+    # the workload must actually exercise the deep tail
+    assert drawn_deep >= 4, rep
