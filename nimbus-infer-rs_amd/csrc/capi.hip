@@ -104,21 +104,37 @@ nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_pa
     return a;
 }
 
-// Rows whose nucleus is likely a small share of the vocabulary (top-p well
-// below 1, no top-k, no penalty history) go to the 1024-lane sparse kernel;
-// everything else (greedy, top-p off or near 1, top-k, penalty, V outside its
-// range) to the 512-lane register-resident / general one.  Either kernel
-// computes every row exactly; this only picks the faster.
+// One kernel per launch, by the launch's parameters (every kernel computes
+// every row exactly; this only picks the faster):
+//   - greedy (T <= 0), 256 <= V <= 53245: the resident kernel's argmax;
+//   - top-p off (>= 1), no top-k: the resident kernel's all-kept walk;
+//   - 0 < top-p <= 0.98, no top-k: the 1024-lane sparse kernel (few kept
+//     tokens);
+//   - anything else (top-k, top-p in (0.98, 1), V outside those ranges): the
+//     512-lane register-resident / general kernel.
+// A row with a repetition-penalty history, or one a kernel cannot prove,
+// runs the general path inside whichever kernel was launched.
 int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
-    const bool sparse = a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f &&
-                        a.top_p > 0.0f && a.top_p <= 0.98f && (a.top_k == 0 || a.top_k >= (uint64_t)a.V) &&
-                        (a.penalty == 1.0f || a.gen_ids == nullptr);
-    if (sparse)
+#ifdef NIS_NO_RESIDENT
+    const bool res_shape = false;
+#else
+    const bool res_shape = a.V >= 256 && a.V <= nis::kRMaxV;
+#endif
+    const bool no_topk = a.top_k == 0 || a.top_k >= (uint64_t)a.V;
+    if (res_shape && a.temperature <= 0.0f) {
+        hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResGreedy>, dim3((unsigned)B),
+                           dim3(nis::kRB), 0, ctx->stream, a);
+    } else if (res_shape && a.temperature > 0.0f && no_topk && a.top_p >= 1.0f) {
+        hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResAll>, dim3((unsigned)B),
+                           dim3(nis::kRB), 0, ctx->stream, a);
+    } else if (a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f && a.top_p > 0.0f &&
+               a.top_p <= 0.98f && no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)) {
         hipLaunchKernelGGL(nis::sample_rows_sparse_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
                            ctx->stream, a);
-    else
+    } else {
         hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
                            ctx->stream, a);
+    }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "sample kernel launch");
 }
@@ -357,7 +373,9 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
     a.scales = w->d_scales;
     a.group = g > 0 ? g : H;
     a.groups = H / a.group;
-    a.gmagic = (uint32_t)((((uint64_t)1 << 32) + (uint64_t)a.group - 1) / (uint64_t)a.group);
+    // ceil(2^32 / group) fits 32 bits for group >= 2; group 1 is marked by 0
+    a.gmagic = a.group == 1 ? 0u
+                            : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)a.group - 1) / (uint64_t)a.group);
     a.V = V;
     a.out = d_logits;
     a.ld = ld;
@@ -458,6 +476,14 @@ int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_par
 #undef NIS_TRY
     return NIS_OK;
 }
+
+#ifdef NIS_RES_TIMING
+// Profiling builds only: copy the resident path's phase timestamps to the host.
+int nis_debug_res_ts(void* dst, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(nis::nis_res_ts), bytes, 0,
+                                    hipMemcpyDeviceToHost);
+}
+#endif
 
 #ifdef NIS_PHASE_TIMING
 // Profiling builds only: copy the sparse path's phase timestamps to the host.

@@ -1,6 +1,7 @@
 // kernels.h — __global__ entry points of the sampler library (gfx950).
 #pragma once
 #include "sparse_path.h"
+#include "resident_path.h"
 
 namespace nis {
 

@@ -140,7 +140,21 @@ def test_config_greedy(sampler, name):
     from nimbus_sampler import workloads
     w = workloads.WORKLOADS[name]
     x = w.make(w.B)
-    _check(sampler, x, w.V, _params(temperature=0.0), w.seeds, label=name + "-greedy")
+    rep = _check(sampler, x, w.V, _params(temperature=0.0), w.seeds, label=name + "-greedy")
+    # every row on the register-resident argmax (no general-path row)
+    assert rep["fast_rows"] == w.B and not rep["rejects"], rep
+
+
+@pytest.mark.parametrize("name", ["c1", "c3", "c5", "headline"])
+def test_config_top_p_off(sampler, name):
+    # the benchmark inputs with top-p off (every token kept, sampler.rs:119):
+    # every row on the register-resident walk, none handed to the general path
+    from nimbus_sampler import workloads
+    w = workloads.WORKLOADS[name]
+    x = w.make(w.B)
+    rep = _check(sampler, x, w.V, _params(temperature=w.temperature, top_p=1.0), w.seeds,
+                 label=name + "-p1")
+    assert rep["fast_rows"] == w.B and not rep["rejects"], rep
 
 
 def test_c4_llama_vocab_with_ties(sampler):
