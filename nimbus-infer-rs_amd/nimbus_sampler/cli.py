@@ -1,7 +1,20 @@
-"""Command-line surface of the GPU path, mirroring the reference's bench JSON.
+"""Command-line surface of the GPU path, mirroring the reference's CLI.
 
   python -m nimbus_sampler bench-kernel   # cmd_bench_kernel (main.rs:372-445) on the GPU
   python -m nimbus_sampler bench-sampler  # the same JSON shape for sample() over a batch
+  python -m nimbus_sampler generate ...   # cmd_generate's sampling flags (main.rs:136-189)
+                                          # driving the device decode loop
+
+generate takes the reference's options with their defaults and parsing
+(--max-new-tokens 64, --temperature 0 = greedy, --top-k 0, --top-p 1.0,
+--repetition-penalty 1.0, --seed unset = 0x5DEECE66D, --stream, --json;
+nimbus_sampler/flags.py).  The model is outside this build, so each step's
+logits come from the LM-head producer (nis_lm_head_logits) over a synthetic
+f32 head and synthetic hidden states (--hidden H, --data-seed); the decode
+step (nis_decode_step) samples on the device, and the ids are decoded on the
+host with a byte-level BPE vocabulary (--vocab vocab.json, streamed with
+--stream exactly as Engine::generate_stream does, engine.rs:296-316).
+--batch B runs B sequences at once, sequence b seeded with seed + b.
 
 bench-kernel builds the reference's synthetic 50257 x 768 head and hidden row
 (main.rs:375-384: x[i] = ((i % 97) - 48) / 48, weights from i * 2654435761)
@@ -101,7 +114,96 @@ def bench_sampler(steps=50, warmup=5, device=0, workload="headline"):
                     "bench.py rotates 8 batches for the HBM figure"}
 
 
+def generate(args, out=None, keep_logits=False):
+    """cmd_generate (main.rs:136-189) with the model step replaced by the
+    synthetic LM head: parse the reference's flags, run the device decode
+    loop, decode the ids on the host.  Returns a dict with the params, the
+    seed, each sequence's ids and text (and the per-step logits on request)."""
+    import time
+    import numpy as np
+    import torch
+    from . import Sampler, W_F32, Rng
+    from .flags import generate_params
+    from .stream import BatchStreams, TokenBytes
+    params, seed, flags = generate_params(list(args))
+    vocab_path = flags.get("vocab")
+    table = TokenBytes.from_file(vocab_path) if vocab_path else None
+    V = len(table) if table is not None else flags.usize_of("vocab-size", 50257)
+    H = flags.usize_of("hidden", 64)
+    B = max(flags.usize_of("batch", 1), 1)
+    dseed = flags.usize_of("data-seed", 0)
+    device = flags.usize_of("device", 0)
+    n_new = params.max_new_tokens
+    dev = torch.device("cuda", device)
+    rnd = np.random.Generator(np.random.PCG64(dseed))
+    # a head whose logits spread like a trained model's (std ~3)
+    w = (rnd.standard_normal((V, H)) * (3.0 / np.sqrt(H))).astype(np.float32)
+    wd = torch.from_numpy(w.reshape(-1)).to(dev)
+    s = Sampler(device)
+    cap = max(n_new, 1)
+    states = torch.from_numpy(np.array([Rng(seed + b).state() for b in range(B)],
+                                       dtype=np.uint64).view(np.int64)).to(dev)
+    gen_ids = torch.zeros((B, cap), dtype=torch.int32, device=dev)
+    gen_len = torch.zeros(B, dtype=torch.int32, device=dev)
+    max_new = torch.full((B,), n_new, dtype=torch.int32, device=dev)
+    done = torch.full((B,), 1 if n_new <= 0 else 0, dtype=torch.uint8, device=dev)
+    tokens = torch.zeros(B, dtype=torch.int32, device=dev)
+    logits = torch.empty((B, V), dtype=torch.float32, device=dev)
+    streams = BatchStreams(table, B) if table is not None else None
+    ids = [[] for _ in range(B)]
+    kept_logits = []
+    t0 = time.perf_counter()
+    for step in range(n_new):
+        live = done.cpu().numpy() == 0
+        if not live.any():
+            break
+        hid = torch.from_numpy(rnd.standard_normal((B, H)).astype(np.float32)).to(dev)
+        s.lm_head_logits(hid, W_F32, wd, V, out=logits)
+        if keep_logits:
+            kept_logits.append(logits.cpu().numpy().copy())
+        s.decode_step(logits, params, states, gen_ids, gen_len, max_new, done, tokens=tokens)
+        tok = tokens.cpu().numpy().view(np.uint32)
+        for b in range(B):
+            if live[b]:
+                ids[b].append(int(tok[b]))
+        if streams is not None:
+            deltas = streams.push_step(tok, live)
+            if flags.has("stream") and out is not None and deltas[0]:
+                out.write(deltas[0])
+                out.flush()
+    if streams is not None:
+        tail = streams.flush()
+        if flags.has("stream") and out is not None and tail[0]:
+            out.write(tail[0])
+    dt = time.perf_counter() - t0
+    s.close()
+    texts = streams.text if streams is not None else [str(x) for x in ids]
+    res = {"params": params, "seed": seed, "ids": ids, "texts": texts, "seconds": dt,
+           "flags": flags}
+    if keep_logits:
+        res["logits"] = kept_logits
+    return res
+
+
 def main(argv=None):
+    argv = sys.argv[1:] if argv is None else argv
+    if argv and argv[0] == "generate":
+        if "--help" in argv[1:] or "-h" in argv[1:]:
+            print(__doc__)
+            return 0
+        res = generate(argv[1:], out=sys.stdout)
+        flags = res["flags"]
+        n = len(res["ids"][0])
+        if flags.has("stream"):
+            print()
+        elif flags.has("json"):
+            print(json.dumps({"generated_ids": res["ids"][0], "text": res["texts"][0],
+                              "seed": res["seed"]}))
+        else:
+            print(res["texts"][0])
+        print(f"[{n} tokens in {res['seconds']:.2f}s = {n / max(res['seconds'], 1e-9):.1f} tok/s]",
+              file=sys.stderr)
+        return 0
     ap = argparse.ArgumentParser(prog="python -m nimbus_sampler")
     sub = ap.add_subparsers(dest="cmd", required=True)
     for name in ("bench-kernel", "bench-sampler"):
@@ -109,6 +211,8 @@ def main(argv=None):
         p.add_argument("--steps", type=int, default=50)
         p.add_argument("--warmup", type=int, default=5)
         p.add_argument("--device", type=int, default=0)
+    sub.add_parser("generate", help="sampling flags of the reference's generate, on the "
+                                    "device decode loop (see the module docstring)")
     args = ap.parse_args(argv)
     if args.cmd == "bench-kernel":
         print(json.dumps(bench_kernel(args.steps, args.warmup, args.device)))
