@@ -44,7 +44,8 @@ def parse_f32(text: str) -> np.float32:
     # the f32 neighbours of the f64 nearest, then the exact nearest of those
     fmax = np.finfo(np.float32).max
     f = np.float32(float(mag)) if mag <= fractions.Fraction(float(fmax)) else fmax
-    cands = {f, np.nextafter(f, np.float32(0)), np.nextafter(f, np.float32(np.inf))}
+    with np.errstate(over="ignore"):
+        cands = {f, np.nextafter(f, np.float32(0)), np.nextafter(f, np.float32(np.inf))}
     best = None
     for c in sorted(cands):
         if not np.isfinite(c):

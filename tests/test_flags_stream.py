@@ -149,7 +149,8 @@ def test_fixture_vocab_streams_reference_texts(text):
 
 def test_fixture_vocab_multi_byte_tokens():
     from nimbus_sampler.stream import IncrementalDecoder, TokenBytes
-    vocab = json.load(open(VOCAB, encoding="utf-8"))
+    with open(VOCAB, encoding="utf-8") as f:
+        vocab = json.load(f)
     table = TokenBytes(vocab)
     assert table.token_bytes(vocab["Ġnimbus"]) == b" nimbus"
     assert table.token_bytes(vocab["nimbus"]) == b"nimbus"
@@ -161,7 +162,8 @@ def test_fixture_vocab_multi_byte_tokens():
 def test_batch_streams_skip_finished_sequences():
     from nimbus_sampler.stream import BatchStreams, TokenBytes
     table = TokenBytes.from_file(VOCAB)
-    vocab = json.load(open(VOCAB, encoding="utf-8"))
+    with open(VOCAB, encoding="utf-8") as f:
+        vocab = json.load(f)
     bs = BatchStreams(table, 2)
     n = vocab["nimbus"]
     bs.push_step([n, n], [True, False])
