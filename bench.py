@@ -32,20 +32,97 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "sampled rows/s + HBM GB/s (% peak), B=256 x V=50257 fp32, T=0.8 top-p=0.9"
-KERNEL_NAME = "sample_rows_sparse_kernel"
+RESIDENT_MAX_V = 53245   # kRMaxV: the largest row one 1024-lane workgroup holds in registers
+SPARSE_MAX_V = 53245     # kSMaxV
 
 
-def read_traffic(workload):
-    """HBM bytes per launch from profiles/*traffic*<workload>*.txt, if measured."""
+def routed_kernel(V, temperature, top_k, top_p, penalty, history=False):
+    """The kernel nis_sample_batch launches for these parameters (launch_rows
+    in capi.hip)."""
+    res_shape = 256 <= V <= RESIDENT_MAX_V
+    no_topk = top_k == 0 or top_k >= V
+    if res_shape and temperature <= 0.0:
+        return "sample_rows_resident_kernel<greedy>"
+    if res_shape and temperature > 0.0 and no_topk and top_p >= 1.0:
+        return "sample_rows_resident_kernel<all>"
+    if 256 <= V <= SPARSE_MAX_V and temperature > 0.0 and 0.0 < top_p <= 0.98 and no_topk \
+            and (penalty == 1.0 or not history):
+        return "sample_rows_sparse_kernel"
+    return "sample_rows_kernel"
+
+
+def host_cpu():
+    """Host CPU model and the logical cores this process may run on."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "nproc": len(os.sched_getaffinity(0)),
+            "os_cpu_count": os.cpu_count()}
+
+
+def reference_worker_count():
+    """threads.rs:12-26 worker_count(): NIMBUS_THREADS when it parses to a
+    positive integer, else every logical core the process may run on
+    (std::thread::available_parallelism follows the affinity mask)."""
+    v = os.environ.get("NIMBUS_THREADS")
+    if v is not None:
+        try:
+            n = int(v)
+            if n > 0:
+                return n
+        except ValueError:
+            pass
+    return len(os.sched_getaffinity(0))
+
+
+def replay_exact(graph_full, graph_tail, G, K):
+    """K launches: K // G replays of the G-launch graph, then the K % G tail."""
+    for _ in range(K // G):
+        graph_full.replay()
+    if K % G:
+        graph_tail.replay()
+
+
+def capture(fn, n):
+    """A hipGraph of fn(0), ..., fn(n-1) captured on a side stream."""
+    import torch
+    if n == 0:
+        return None
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(n):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(cap)
+    return graph
+
+
+def read_traffic(workload, kernel):
+    """HBM bytes per launch of this workload's kernel from the committed
+    rocprofv3 --pmc summary profiles/*traffic*<workload>*.txt (FETCH_SIZE +
+    WRITE_SIZE per dispatch, scaled by a plain copy's reading); None when no
+    summary for this kernel exists.  Returns (bytes, source file)."""
     pdir = os.path.join(ROOT, "profiles")
     if not os.path.isdir(pdir):
-        return None
+        return None, None
+    base = kernel.split("<")[0]
     for fn in sorted(os.listdir(pdir)):
-        if "traffic" in fn and workload in fn and fn.endswith(".txt"):
-            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(os.path.join(pdir, fn)).read(), re.M)
-            if m:
-                return float(m.group(1))
-    return None
+        if "traffic" in fn and fn.endswith(f"_{workload}.txt"):
+            with open(os.path.join(pdir, fn)) as f:
+                text = f.read()
+            k = re.search(r"^kernel:\s*(\S+)", text, re.M)
+            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", text, re.M)
+            if m and (k is None or k.group(1).split("<")[0] == base):
+                return float(m.group(1)), f"profiles/{fn}"
+    return None, None
 
 
 def bench_decode(args, w, sampler, params, bufs, states, tokens):
@@ -62,36 +139,34 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
     done = torch.zeros(B, dtype=torch.uint8, device=dev)
     G = len(bufs)
 
-    def block():
+    def block(n):
         gen_len.zero_()
         done.zero_()
-        for i in range(G):
+        for i in range(n):
             sampler.decode_step(bufs[i], params, states, gen_ids, gen_len, max_new, done,
                                 tokens=tokens)
 
-    for _ in range(max(1, args.warmup // G)):
-        block()
+    for i in range(args.warmup):
+        if i % G == 0:
+            gen_len.zero_()
+            done.zero_()
+        sampler.decode_step(bufs[i % G], params, states, gen_ids, gen_len, max_new, done,
+                            tokens=tokens)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    cap_stream = torch.cuda.Stream()
-    cap_stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cap_stream):
-        with torch.cuda.graph(graph, stream=cap_stream):
-            block()
-    torch.cuda.current_stream().wait_stream(cap_stream)
+    K = max(1, args.steps)
+    g_full = capture(lambda _: block(G), 1)
+    g_tail = capture(lambda _: block(K % G), 1) if K % G else None
     for _ in range(2):
-        graph.replay()
+        g_full.replay()
     torch.cuda.synchronize()
-    K = max(G, (args.steps // G) * G)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(K // G):
-        graph.replay()
+    replay_exact(g_full, g_tail, G, K)
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / K
-    assert int(gen_len[0].item()) == G and int(done.sum().item()) == 0
+    assert int(gen_len[0].item()) == (K % G or G) and int(done.sum().item()) == 0
     alg_bytes = B * (4 * V + 68) + B * (4 + 4 + 1)  # logits, RNG, token + history, length, flag
     print(json.dumps({
         "metric": f"decode steps: tokens/s, B={B} sequences x V={V} fp32, "
@@ -100,8 +175,8 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
         "warmup": args.warmup, "us_per_step": us, "higher_is_better": True,
         "data": "synthetic logits of the workload, 8 rotated batches resident in HBM",
         "config": {"workload": args.workload, "B": B, "V": V, "history_cap": cap,
-                   "launch": f"hipGraph replay of {G} nis_decode_step calls after clearing "
-                             "the lengths and flags"},
+                   "launch": f"hipGraph replays of up to {G} nis_decode_step calls after "
+                             "clearing the lengths and flags"},
         "roofline": {"bound": "hbm", "achieved": alg_bytes / (us * 1e-6) / 1e9,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS},
@@ -298,24 +373,21 @@ def main():
     # whole region on the stream the launches run on; the mean launch
     # duration is their elapsed time over the number of launches.
     G = len(bufs)
-    K = max(G, (args.steps // G) * G)
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(graph, stream=cap):
-            for i in range(G):
-                sampler.sample_batch(bufs[i], params, states, tokens=tokens)
-    torch.cuda.current_stream().wait_stream(cap)
+    K = max(1, args.steps)
+
+    def launch(i):
+        sampler.sample_batch(bufs[i], params, states, tokens=tokens)
+
+    g_full = capture(launch, G)
+    g_tail = capture(launch, K % G)
     for _ in range(2):  # warm replays
-        graph.replay()
+        g_full.replay()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(K // G):
-        graph.replay()
+    replay_exact(g_full, g_tail, G, K)
     e1.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -332,13 +404,13 @@ def main():
 
     alg_bytes = B * (4 * V + 68)
     achieved = alg_bytes / (mean_ms * 1e-3) / 1e9
-    traffic = read_traffic(args.workload)
+    kernel = routed_kernel(V, w.temperature, 0, w.top_p, 1.0)
+    traffic, traffic_src = read_traffic(args.workload, kernel)
 
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import oracle
-        nthreads = args.cpu_threads or int(os.environ.get("NIMBUS_THREADS", "0") or 0) or \
-            min(16, os.cpu_count() or 1)
+        nthreads = args.cpu_threads or reference_worker_count()
         p = oracle.make_params(w.temperature, w.top_p)
         times = []
         for rep in range(6):
@@ -350,8 +422,10 @@ def main():
         med = times[len(times) // 2]
         cpu = {"value": B / med, "unit": "rows/s", "cores": used, "kind": "port",
                "sample": f"C restatement of sampler.rs over the same {B}x{V} batch, "
-                         f"threads.rs fork-join on {used} threads, median of 5 batches after 1 warm-up",
-               "gbs": alg_bytes / med / 1e9}
+                         f"threads.rs fork-join on {used} threads (worker_count(): "
+                         f"NIMBUS_THREADS, else every logical core), median of 5 batches "
+                         f"after 1 warm-up",
+               "gbs": alg_bytes / med / 1e9, "host": host_cpu()}
 
     out = {
         "metric": METRIC,
@@ -368,11 +442,15 @@ def main():
         "data": "synthetic: N(0,3^2) logits from PCG64 seed 7, 8 rotated batches resident in HBM",
         "config": {"workload": args.workload, "B": B, "V": V, "temperature": w.temperature,
                    "top_p": w.top_p, "ld": V, "parallelism": "1 GPU",
-                   "launch": f"hipGraph replay of {G} nis_sample_batch launches",
+                   "launch": f"hipGraph replays: {K // G} x {G} + {K % G} nis_sample_batch "
+                             f"launches",
                    "eager_rows_per_s": eager_rows_s},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": KERNEL_NAME, "kernel_mean_us": mean_ms * 1e3,
+                     "traffic_source": (f"{traffic_src}: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE "
+                                        "per dispatch, scaled by a plain copy's reading")
+                     if traffic_src else None,
+                     "kernel": kernel, "kernel_mean_us": mean_ms * 1e3,
                      "alg_bytes_per_launch": alg_bytes},
         "cpu_baseline": cpu,
         "parity": parity,

@@ -115,6 +115,10 @@ def test_utf8_stream_reference_unit_tests():
     assert Utf8Stream().push_bytes(bytes([0xFF, ord("a")])) == "�a"
     # an announced sequence that is not UTF-8: one replacement for its bytes
     assert Utf8Stream().push_bytes(bytes([0xE4, 0x41, 0x42, 0x43])) == "�C"
+    # ... which differs from decode()'s lossy whole-string conversion
+    assert bytes([0xE4, 0x41, 0x2A]).decode("utf-8", errors="replace") == "�A*"
+    s = Utf8Stream()
+    assert s.push_bytes(bytes([0xE4, 0x41])) == "" and s.push_bytes(b"*") == "�"
     # a truncated tail is held back, and flushed lossily
     s = Utf8Stream()
     assert s.push_bytes("a".encode() + "€".encode()[:2]) == "a" and s.flush() == "�"
