@@ -167,6 +167,22 @@ int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_par
                    const uint32_t* h_generated, int64_t n_generated, uint64_t state_inout[4],
                    uint32_t* token_out);
 
+/* Allocation-free nis_sample_one.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, result and errors as nis_sample_one, but the row is staged
+ * through a fixed static device array (NIS_NOALLOC_MAX_V logits and
+ * NIS_NOALLOC_MAX_GEN history ids, about 1.25 MiB, held by each GPU the
+ * library runs on until the process ends) instead of a context workspace:
+ * it calls no hipMalloc / hipFree.  Larger V or histories return
+ * NIS_ERANGE.  All calls on one GPU share that array, so calls that overlap
+ * on one GPU (two threads, two contexts) race; serialize them. */
+#define NIS_NOALLOC_MAX_V (1 << 18)
+#define NIS_NOALLOC_MAX_GEN (1 << 16)
+int nis_sample_one_noalloc(nis_ctx* ctx, const float* h_logits, int64_t V,
+                           const nis_params* params, const uint32_t* h_generated,
+                           int64_t n_generated, uint64_t state_inout[4], uint32_t* token_out);
+
 /* LM-head weight formats (quant.rs:13-25): dense f32 rows; int8 codes stored
  * as value + 128 in bytes; int4 codes stored as value + 8, two per byte, low
  * nibble first over the global index row * H + k. */

@@ -7,6 +7,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -31,6 +32,42 @@ struct nis_ctx {
 };
 
 namespace {
+
+// Staging area of nis_sample_one_noalloc: RNG state, token, history offsets,
+// history and logits of one row, laid out by noalloc_layout().  Each device
+// holds its own copy for the life of the process; host code reaches it only
+// through the per-device address that hipGetSymbolAddress returns.
+constexpr size_t kNoAllocStateOff = 0;
+constexpr size_t kNoAllocTokOff = 256;
+constexpr size_t kNoAllocGoffOff = 512;
+constexpr size_t kNoAllocGenOff = 1024;
+constexpr size_t kNoAllocLogitsOff = kNoAllocGenOff + (size_t)NIS_NOALLOC_MAX_GEN * 4;
+constexpr size_t kNoAllocBytes = kNoAllocLogitsOff + (size_t)NIS_NOALLOC_MAX_V * 4;
+static_assert(kNoAllocLogitsOff % 256 == 0, "logits staging must stay 256-byte aligned");
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `dev`, which must be the current device.
+// Looked up once per device (at nis_ctx_create, or on the first
+// nis_sample_one_noalloc call if that lookup failed) and kept.
+hipError_t scratch_on_device(int dev, void** out) {
+    *out = nullptr;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!ptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 // Make `dev` current for the duration of a call and restore the caller's.
 struct DeviceGuard {
@@ -217,6 +254,8 @@ int nis_ctx_create(int device, nis_ctx** out) {
         return (int)e;
     }
     ctx->stream = ctx->own_stream;
+    void* scr = nullptr;
+    (void)scratch_on_device(device, &scr);  // retried by nis_sample_one_noalloc on failure
     *out = ctx;
     return NIS_OK;
 }
@@ -417,15 +456,72 @@ int nis_sync(nis_ctx* ctx) {
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "hipStreamSynchronize");
 }
 
-int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_params* params,
-                   const uint32_t* h_generated, int64_t n_generated, uint64_t state_inout[4],
-                   uint32_t* token_out) {
+}  // extern "C"
+
+namespace {
+
+struct OneRowStaging {
+    uint64_t* state;
+    uint32_t* token;
+    int64_t* goff;
+    uint32_t* gen;
+    float* logits;
+};
+
+int check_one_args(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_params* params,
+                   const uint32_t* h_generated, int64_t n_generated, const uint64_t* state_inout,
+                   const uint32_t* token_out) {
     if (!ctx) return NIS_EINVAL;
     if (!h_logits || !params || !state_inout || !token_out || (n_generated > 0 && !h_generated))
         return fail(ctx, NIS_EINVAL, "null pointer argument");
     if (V <= 0 || n_generated < 0) return fail(ctx, NIS_EINVAL, "bad size");
     if (V > NIS_MAX_V) return fail(ctx, NIS_ERANGE, "V exceeds NIS_MAX_V");
     if (params->reserved != 0) return fail(ctx, NIS_EINVAL, "nis_params.reserved must be 0");
+    return NIS_OK;
+}
+
+// Copy one host row (and its history when the penalty applies) into the
+// staging buffers, sample it on the context stream, copy the token and the
+// advanced RNG state back, and wait.
+int sample_one_staged(nis_ctx* ctx, const OneRowStaging& d, const float* h_logits, int64_t V,
+                      const nis_params* params, const uint32_t* h_generated, int64_t n_generated,
+                      bool use_gen, uint64_t state_inout[4], uint32_t* token_out) {
+    hipStream_t s = ctx->stream;
+    hipError_t e;
+#define NIS_TRY(call, what)                           \
+    do {                                              \
+        e = (call);                                   \
+        if (e != hipSuccess) return hip_fail(ctx, e, what); \
+    } while (0)
+    NIS_TRY(hipMemcpyAsync(d.logits, h_logits, (size_t)V * 4, hipMemcpyHostToDevice, s), "H2D logits");
+    NIS_TRY(hipMemcpyAsync(d.state, state_inout, 32, hipMemcpyHostToDevice, s), "H2D rng");
+    if (use_gen) {
+        const int64_t offs[2] = {0, n_generated};
+        NIS_TRY(hipMemcpyAsync(d.gen, h_generated, (size_t)n_generated * 4, hipMemcpyHostToDevice, s),
+                "H2D generated");
+        NIS_TRY(hipMemcpyAsync(d.goff, offs, 16, hipMemcpyHostToDevice, s), "H2D offsets");
+        NIS_TRY(hipStreamSynchronize(s), "sync staging");  // `offs` is stack memory
+    }
+    int rc = nis_sample_batch(ctx, d.logits, V, 1, V, params, d.state, use_gen ? d.gen : nullptr,
+                              use_gen ? d.goff : nullptr, d.token, nullptr);
+    if (rc != NIS_OK) return rc;
+    NIS_TRY(hipMemcpyAsync(token_out, d.token, 4, hipMemcpyDeviceToHost, s), "D2H token");
+    NIS_TRY(hipMemcpyAsync(state_inout, d.state, 32, hipMemcpyDeviceToHost, s), "D2H rng");
+    NIS_TRY(hipStreamSynchronize(s), "sync");
+#undef NIS_TRY
+    return NIS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_params* params,
+                   const uint32_t* h_generated, int64_t n_generated, uint64_t state_inout[4],
+                   uint32_t* token_out) {
+    int rc = check_one_args(ctx, h_logits, V, params, h_generated, n_generated, state_inout,
+                            token_out);
+    if (rc != NIS_OK) return rc;
     DeviceGuard g(ctx->device);
     if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
 
@@ -446,35 +542,35 @@ int nis_sample_one(nis_ctx* ctx, const float* h_logits, int64_t V, const nis_par
         ctx->ws_bytes = need;
     }
     char* ws = (char*)ctx->ws;
-    uint64_t* d_state = (uint64_t*)(ws + off_state);
-    uint32_t* d_tok = (uint32_t*)(ws + off_tok);
-    int64_t* d_goff = (int64_t*)(ws + off_goff);
-    uint32_t* d_gen = (uint32_t*)(ws + off_gen);
-    float* d_logits = (float*)(ws + off_logits);
-    hipStream_t s = ctx->stream;
-    hipError_t e;
-#define NIS_TRY(call, what)                           \
-    do {                                              \
-        e = (call);                                   \
-        if (e != hipSuccess) return hip_fail(ctx, e, what); \
-    } while (0)
-    NIS_TRY(hipMemcpyAsync(d_logits, h_logits, (size_t)V * 4, hipMemcpyHostToDevice, s), "H2D logits");
-    NIS_TRY(hipMemcpyAsync(d_state, state_inout, 32, hipMemcpyHostToDevice, s), "H2D rng");
-    if (use_gen) {
-        const int64_t offs[2] = {0, n_generated};
-        NIS_TRY(hipMemcpyAsync(d_gen, h_generated, (size_t)n_generated * 4, hipMemcpyHostToDevice, s),
-                "H2D generated");
-        NIS_TRY(hipMemcpyAsync(d_goff, offs, 16, hipMemcpyHostToDevice, s), "H2D offsets");
-        NIS_TRY(hipStreamSynchronize(s), "sync staging");  // `offs` is stack memory
-    }
-    int rc = nis_sample_batch(ctx, d_logits, V, 1, V, params, d_state, use_gen ? d_gen : nullptr,
-                              use_gen ? d_goff : nullptr, d_tok, nullptr);
+    OneRowStaging d{(uint64_t*)(ws + off_state), (uint32_t*)(ws + off_tok),
+                    (int64_t*)(ws + off_goff), (uint32_t*)(ws + off_gen),
+                    (float*)(ws + off_logits)};
+    return sample_one_staged(ctx, d, h_logits, V, params, h_generated, n_generated, use_gen,
+                             state_inout, token_out);
+}
+
+int nis_sample_one_noalloc(nis_ctx* ctx, const float* h_logits, int64_t V,
+                           const nis_params* params, const uint32_t* h_generated,
+                           int64_t n_generated, uint64_t state_inout[4], uint32_t* token_out) {
+    int rc = check_one_args(ctx, h_logits, V, params, h_generated, n_generated, state_inout,
+                            token_out);
     if (rc != NIS_OK) return rc;
-    NIS_TRY(hipMemcpyAsync(token_out, d_tok, 4, hipMemcpyDeviceToHost, s), "D2H token");
-    NIS_TRY(hipMemcpyAsync(state_inout, d_state, 32, hipMemcpyDeviceToHost, s), "D2H rng");
-    NIS_TRY(hipStreamSynchronize(s), "sync");
-#undef NIS_TRY
-    return NIS_OK;
+    if (V > NIS_NOALLOC_MAX_V)
+        return fail(ctx, NIS_ERANGE, "V exceeds NIS_NOALLOC_MAX_V (the static staging area)");
+    const bool use_gen = params->repetition_penalty != 1.0f && n_generated > 0;
+    if (use_gen && n_generated > NIS_NOALLOC_MAX_GEN)
+        return fail(ctx, NIS_ERANGE, "n_generated exceeds NIS_NOALLOC_MAX_GEN");
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+    void* base = nullptr;
+    hipError_t e = scratch_on_device(ctx->device, &base);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(scratch)");
+    char* ws = (char*)base;
+    OneRowStaging d{(uint64_t*)(ws + kNoAllocStateOff), (uint32_t*)(ws + kNoAllocTokOff),
+                    (int64_t*)(ws + kNoAllocGoffOff), (uint32_t*)(ws + kNoAllocGenOff),
+                    (float*)(ws + kNoAllocLogitsOff)};
+    return sample_one_staged(ctx, d, h_logits, V, params, h_generated, n_generated, use_gen,
+                             state_inout, token_out);
 }
 
 #ifdef NIS_RES_TIMING

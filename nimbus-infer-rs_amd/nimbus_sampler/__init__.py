@@ -34,7 +34,8 @@ EXPORTED_SYMBOLS = (
     "nis_ctx_create", "nis_ctx_destroy", "nis_ctx_set_stream", "nis_ctx_get_stream",
     "nis_last_error", "nis_status_string", "nis_rng_seed", "nis_rng_next_u64",
     "nis_rng_next_f64", "nis_rng_seed_batch", "nis_sample_batch", "nis_argmax_batch",
-    "nis_apply_repetition_penalty", "nis_sample_one", "nis_sync", "nis_decode_step",
+    "nis_apply_repetition_penalty", "nis_sample_one", "nis_sample_one_noalloc", "nis_sync",
+    "nis_decode_step",
     "nis_lm_head_logits",
 )
 
@@ -108,10 +109,11 @@ def load_library(path: str = LIB_PATH):
                                                ctypes.c_float]
     L.nis_sample_one.argtypes = [vp, vp, ctypes.c_int64, ctypes.POINTER(NisParams), vp,
                                  ctypes.c_int64, u64p, ctypes.POINTER(ctypes.c_uint32)]
+    L.nis_sample_one_noalloc.argtypes = L.nis_sample_one.argtypes
     L.nis_sync.argtypes = [vp]
     for name in ("nis_ctx_create", "nis_ctx_destroy", "nis_ctx_set_stream", "nis_rng_seed_batch",
                  "nis_sample_batch", "nis_argmax_batch", "nis_apply_repetition_penalty",
-                 "nis_sample_one", "nis_sync"):
+                 "nis_sample_one", "nis_sample_one_noalloc", "nis_sync"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
