@@ -45,7 +45,10 @@ def routed_kernel(V, temperature, top_k, top_p, penalty, history=False):
         return "sample_rows_resident_kernel<greedy>"
     if res_shape and temperature > 0.0 and no_topk and top_p >= 1.0:
         return "sample_rows_resident_kernel<all>"
-    if 256 <= V <= SPARSE_MAX_V and temperature > 0.0 and 0.0 < top_p <= 0.98 and no_topk \
+    if res_shape and temperature > 0.0 and no_topk and 0.95 <= top_p < 1.0 \
+            and (penalty == 1.0 or not history):
+        return "sample_rows_dense_kernel"
+    if 256 <= V <= SPARSE_MAX_V and temperature > 0.0 and 0.0 < top_p < 0.95 and no_topk \
             and (penalty == 1.0 or not history):
         return "sample_rows_sparse_kernel"
     return "sample_rows_kernel"

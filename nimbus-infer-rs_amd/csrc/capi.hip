@@ -145,10 +145,12 @@ nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_pa
 // every row exactly; this only picks the faster):
 //   - greedy (T <= 0), 256 <= V <= 53245: the resident kernel's argmax;
 //   - top-p off (>= 1), no top-k: the resident kernel's all-kept walk;
-//   - 0 < top-p <= 0.98, no top-k: the 1024-lane sparse kernel (few kept
-//     tokens);
-//   - anything else (top-k, top-p in (0.98, 1), V outside those ranges): the
-//     512-lane register-resident / general kernel.
+//   - 0.95 <= top-p < 1, no top-k: the 1024-lane dense kernel (a nucleus of
+//     any size: one exact histogram of the whole row built in the stream);
+//   - 0 < top-p < 0.95, no top-k: the 1024-lane sparse kernel (few kept
+//     tokens, listed against a sampled threshold);
+//   - anything else (top-k, V outside 256..53245): the 512-lane
+//     register-resident / general kernel.
 // A row with a repetition-penalty history, or one a kernel cannot prove,
 // runs the general path inside whichever kernel was launched.
 int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
@@ -164,8 +166,12 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
     } else if (res_shape && a.temperature > 0.0f && no_topk && a.top_p >= 1.0f) {
         hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResAll>, dim3((unsigned)B),
                            dim3(nis::kRB), 0, ctx->stream, a);
+    } else if (res_shape && a.temperature > 0.0f && no_topk && a.top_p >= 0.95f && a.top_p < 1.0f &&
+               (a.penalty == 1.0f || a.gen_ids == nullptr)) {
+        hipLaunchKernelGGL(nis::sample_rows_dense_kernel, dim3((unsigned)B), dim3(nis::kDB), 0,
+                           ctx->stream, a);
     } else if (a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f && a.top_p > 0.0f &&
-               a.top_p <= 0.98f && no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)) {
+               a.top_p < 0.95f && no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)) {
         hipLaunchKernelGGL(nis::sample_rows_sparse_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
                            ctx->stream, a);
     } else {
@@ -577,6 +583,14 @@ int nis_sample_one_noalloc(nis_ctx* ctx, const float* h_logits, int64_t V,
 // Profiling builds only: copy the resident path's phase timestamps to the host.
 int nis_debug_res_ts(void* dst, size_t bytes) {
     return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(nis::nis_res_ts), bytes, 0,
+                                    hipMemcpyDeviceToHost);
+}
+#endif
+
+#ifdef NIS_DENSE_TIMING
+// Profiling builds only: copy the dense path's phase timestamps to the host.
+int nis_debug_dense_ts(void* dst, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(nis::nis_dense_ts), bytes, 0,
                                     hipMemcpyDeviceToHost);
 }
 #endif

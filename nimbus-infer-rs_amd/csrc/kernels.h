@@ -2,6 +2,7 @@
 #pragma once
 #include "sparse_path.h"
 #include "resident_path.h"
+#include "dense_path.h"
 
 namespace nis {
 
