@@ -41,6 +41,10 @@ def routed_kernel(V, temperature, top_k, top_p, penalty, history=False):
     in capi.hip)."""
     res_shape = 256 <= V <= RESIDENT_MAX_V
     no_topk = top_k == 0 or top_k >= V
+    if V > RESIDENT_MAX_V and temperature <= 0.0:
+        return "sample_rows_long_kernel<greedy>"
+    if V > RESIDENT_MAX_V and (top_k == 0 or top_k >= V) and (penalty == 1.0 or not history):
+        return "sample_rows_long_kernel<all>" if top_p >= 1.0 else "sample_rows_long_kernel<top-p>"
     if res_shape and temperature <= 0.0:
         return "sample_rows_resident_kernel<greedy>"
     if res_shape and temperature > 0.0 and no_topk and top_p >= 1.0:

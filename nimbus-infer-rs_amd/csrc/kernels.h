@@ -3,6 +3,7 @@
 #include "sparse_path.h"
 #include "resident_path.h"
 #include "dense_path.h"
+#include "long_path.h"
 
 namespace nis {
 

@@ -487,13 +487,23 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         __builtin_amdgcn_s_setprio(0);
         mx = wmax_f32(mx);
         z = wsum_f64(z);
+        // with stats: the elements above -inf (every one of them is kept)
+        uint32_t nfin = 0u;
+        if (a.stats) {
+#pragma unroll
+            for (int k = 0; k < kRN; ++k)
+                if (k < Kw)
+                    nfin += (uint32_t)(xv[k].x > -INFINITY) + (uint32_t)(xv[k].y > -INFINITY) +
+                            (uint32_t)(xv[k].z > -INFINITY) + (uint32_t)(xv[k].w > -INFINITY);
+            nfin = wsum_u32(nfin);
+        }
         if (l == 0) {
             RRec r;
             r.z = z;
             r.mx = mx;
             r.rw = Rz;
             r.thc = 0.0f;
-            r.nc = 0u;
+            r.nc = nfin;
             r.bad = (uint32_t)!(z < INFINITY);
             r.pad = 0u;
             sh.rec[w] = r;
@@ -530,6 +540,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const uint64_t nzw = __ballot(rv & (T > 0.0));
         const int ws = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)nzw));
         if (w != ws) return NIS_REJECT_NONE;
+        const uint32_t nkept = a.stats ? wsum_u32(rv ? rr.nc : 0u) : 0u;
         // r inside this wave, in 2^R_w units
         const double rw_ = ldexp(r - bcast_f64(Tincl - T, ws), (int)(R - Rz));
         // chunk totals (2^Rz units, exact rescales): a transposed sum of the
@@ -609,7 +620,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
                 const double em = exp2((double)xq * c64 - (double)M * c64);
                 const double zM = ldexp(Z, (int)R) * exp2(-(double)M * c64);
                 write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zM, 0.0, u,
-                                (u == 0.0) ? 0.0 : em / zM, (uint64_t)V, 1);
+                                (u == 0.0) ? 0.0 : em / zM, (uint64_t)nkept, 1);
             }
         }
         return NIS_REJECT_NONE;
