@@ -150,8 +150,9 @@ nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_pa
 //   - 0 < top-p < 0.95, no top-k: the 1024-lane sparse kernel (few kept
 //     tokens, listed against a sampled threshold);
 //   - V > 53245 (rows longer than the registers hold), no top-k: the
-//     1024-lane long-row kernel (greedy, top-p off or top-p, the row read
-//     again from cache after its stream);
+//     512-lane long-row kernel (greedy, top-p off or top-p, the row read
+//     again from cache after its stream), then the general path on the rows
+//     it declined;
 //   - anything else (top-k, V < 256): the 512-lane register-resident /
 //     general kernel.
 // A row with a repetition-penalty history, or one a kernel cannot prove,
@@ -177,16 +178,20 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
                a.top_p < 0.95f && no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)) {
         hipLaunchKernelGGL(nis::sample_rows_sparse_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
                            ctx->stream, a);
-    } else if (a.V > nis::kDMaxV && a.temperature <= 0.0f) {
-        hipLaunchKernelGGL(nis::sample_rows_long_kernel<nis::kLongGreedy>, dim3((unsigned)B),
-                           dim3(nis::kLB), 0, ctx->stream, a);
-    } else if (a.V > nis::kDMaxV && no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)) {
-        if (a.top_p >= 1.0f)
+    } else if (a.V > nis::kDMaxV &&
+               (a.temperature <= 0.0f || (no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)))) {
+        if (a.temperature <= 0.0f)
+            hipLaunchKernelGGL(nis::sample_rows_long_kernel<nis::kLongGreedy>, dim3((unsigned)B),
+                               dim3(nis::kLB), 0, ctx->stream, a);
+        else if (a.top_p >= 1.0f)
             hipLaunchKernelGGL(nis::sample_rows_long_kernel<nis::kLongAll>, dim3((unsigned)B),
                                dim3(nis::kLB), 0, ctx->stream, a);
         else
             hipLaunchKernelGGL(nis::sample_rows_long_kernel<nis::kLongTopP>, dim3((unsigned)B),
                                dim3(nis::kLB), 0, ctx->stream, a);
+        // the rows it declined (penalty history, non-finite, exact-tie overflow)
+        hipLaunchKernelGGL(nis::sample_rows_pending_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
+                           ctx->stream, a);
     } else {
         hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
                            ctx->stream, a);

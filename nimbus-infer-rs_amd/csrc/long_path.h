@@ -32,11 +32,13 @@
 
 namespace nis {
 
-constexpr int kLB = 1024;             // lanes per workgroup
+constexpr int kLB = 512;              // lanes per workgroup (two workgroups share a CU)
 constexpr int kLW = kLB / 64;         // waves per workgroup
 constexpr int kLD = 4;                // loads in flight per lane
 constexpr int kLRing = 4096;          // histogram ring: 64 octaves of 64 buckets
 constexpr int kLSpan = 32;            // octaves searched below R (and folded below R_w0)
+constexpr int kLQ = 64 * kLSpan / kLB;  // searched buckets per lane
+constexpr uint32_t kLPending = 0xFFF00000u;  // token of a declined row (| reject code)
 constexpr int kLMem = 2048;           // members of the cutoff bucket listed by the second read
 
 enum { kLongTopP = 0, kLongAll = 1, kLongGreedy = 2 };
@@ -70,7 +72,7 @@ struct LongShared {
 
 template <int MODE>
 __device__ __forceinline__ bool long_eligible(const RowArgs a, int row) {
-    if (a.V <= kDMaxV || a.V > NIS_MAX_V) return false;
+    if (a.V < 256 || a.V > NIS_MAX_V) return false;
     if (MODE == kLongGreedy) {
         if (!(a.temperature <= 0.0f)) return false;
     } else {
@@ -363,24 +365,29 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
     // =====================================================================
     // ---- top-p: cutoff search over the 32 octaves below R ----------------
     const float p = a.top_p;
-    const int jt0 = 64 * Ri - 128 * w - 2 * l;  // lane: buckets jt0, jt0 - 1
-    unsigned long long bm[2];
-    uint32_t bc[2];
+    const int jt0 = 64 * Ri - 64 * kLQ * w - kLQ * l;  // lane: buckets jt0 .. jt0 - kLQ + 1
+    unsigned long long bm[kLQ];
+    uint32_t bc[kLQ];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < kLQ; ++q) {
         const int j = jt0 - q;
         const unsigned long long v = sh.ring[j & (kLRing - 1)];
         bc[q] = (uint32_t)(v >> 48);
         bm[q] = d_u44(v, j >> 6, Ri);
     }
-    const unsigned long long lm = bm[0] + bm[1];
-    const uint32_t lcn = bc[0] + bc[1];
+    unsigned long long lm = 0ull;
+    uint32_t lcn = 0u;
+#pragma unroll
+    for (int q = 0; q < kLQ; ++q) {
+        lm += bm[q];
+        lcn += bc[q];
+    }
     const unsigned long long im = rscan_u64w(lm);
     const uint32_t ic = wscan_u32(lcn);
     // the 32 octaves below the search (and the folded bucket) still count in Z
     unsigned long long lo = 0ull;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < kLQ; ++q) {
         const int j = jt0 - q - 64 * kLSpan;
         lo += d_u44(sh.ring[j & (kLRing - 1)], j >> 6, Ri);
     }
@@ -404,7 +411,7 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         unsigned long long gp_ = 0ull;
         uint32_t np_ = 0u, cp_ = 0u;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < kLQ; ++q) {
             const int j = jt0 - q;
             if ((bc[q] != 0u) && ((double)G - d_mup(j, 0, Ri) <= pz)) {
                 jp = j;
@@ -717,27 +724,34 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
 #undef NIS_LIDX
 }
 
-// One 1024-lane workgroup per long row: the long path in the launch's MODE,
-// the general path (on the first 512 lanes) for a row it declines or cannot
-// take.
+// One 512-lane workgroup per long row (two share a CU, so one's tail runs
+// beside the other's stream).  A row the long path declines or cannot take
+// gets the token kLPending | reason, and sample_rows_pending_kernel, launched
+// after it, runs the general path on exactly those rows.
 template <int MODE>
-__global__ __launch_bounds__(kLB) void sample_rows_long_kernel(RowArgs a) {
-    __shared__ union {
-        GeneralShared g;
-        LongShared s;
-    } sh;
+__global__ __launch_bounds__(kLB, 2) void sample_rows_long_kernel(RowArgs a) {
+    __shared__ LongShared sh;
     const int row = (int)blockIdx.x;
     if (a.done != nullptr && a.done[row]) return;  // a finished sequence (decode step)
     asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
                  "s"(a.penalty), "s"(a.gen_ids), "s"(a.gen_off));
     uint32_t reject = NIS_REJECT_SHAPE;
     if (long_eligible<MODE>(a, row)) {
-        reject = long_row<MODE>(a, row, sh.s);
+        reject = long_row<MODE>(a, row, sh);
         if (reject == NIS_REJECT_NONE) return;
     }
-    if (threadIdx.x >= kBlock) return;
-    __syncthreads();
-    general_row<1>(a, row, sh.g, reject);
+    if (threadIdx.x == 0) a.tokens[row] = kLPending | reject;
+}
+
+// The general path for the rows a long-row launch declined (their token holds
+// kLPending | reason); every other row leaves at once.
+__global__ __launch_bounds__(kBlock) void sample_rows_pending_kernel(RowArgs a) {
+    __shared__ GeneralShared sh;
+    const int row = (int)blockIdx.x;
+    if (a.done != nullptr && a.done[row]) return;
+    const uint32_t t = a.tokens[row];
+    if ((t & kLPending) != kLPending) return;
+    general_row<1>(a, row, sh, t & ~kLPending);
 }
 
 }  // namespace nis
