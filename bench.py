@@ -364,10 +364,16 @@ def main():
         gt, _, _ = oracle.sample_batch(host0, V, oracle.make_params(0.0), oracle.rng_states(w.seeds))
         got = tokens.cpu().numpy().astype(np.uint32)
         boundary = (rs["topp_margin"] <= 1e-6) | (rs["cdf_margin"] <= 1e-6)
+        mism = got != rt
+        margin = np.minimum(rs["topp_margin"], rs["cdf_margin"])
         parity = {
             "greedy_mismatch": int((g.cpu().numpy().astype(np.uint32) != gt).sum()),
-            "sampled_mismatch_outside_boundary": int(((got != rt) & ~boundary).sum()),
+            "sampled_mismatch_outside_boundary": int((mism & ~boundary).sum()),
             "boundary_rows": int(boundary.sum()),
+            # rows whose sampled id differs from the oracle's, all of them on an
+            # oracle boundary, and the largest oracle margin among them
+            "boundary_mismatch": int((mism & boundary).sum()),
+            "max_mismatch_margin": float(margin[mism].max()) if mism.any() else 0.0,
             "rng_state_match": bool(np.array_equal(st_copy.cpu().numpy().view(np.uint64), ref_states)),
         }
 

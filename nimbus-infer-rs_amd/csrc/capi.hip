@@ -5,6 +5,7 @@
 // sampling entry point launches the gfx950 kernels or returns an error.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -190,8 +191,8 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
             hipLaunchKernelGGL(nis::sample_rows_long_kernel<nis::kLongTopP>, dim3((unsigned)B),
                                dim3(nis::kLB), 0, ctx->stream, a);
         // the rows it declined (penalty history, non-finite, exact-tie overflow)
-        hipLaunchKernelGGL(nis::sample_rows_pending_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
-                           ctx->stream, a);
+        hipLaunchKernelGGL(nis::sample_rows_pending_kernel, dim3((unsigned)std::min(B, 256)),
+                           dim3(nis::kBlock), 0, ctx->stream, a, B);
     } else {
         hipLaunchKernelGGL(nis::sample_rows_kernel, dim3((unsigned)B), dim3(nis::kBlock), 0,
                            ctx->stream, a);

@@ -744,14 +744,18 @@ __global__ __launch_bounds__(kLB, 2) void sample_rows_long_kernel(RowArgs a) {
 }
 
 // The general path for the rows a long-row launch declined (their token holds
-// kLPending | reason); every other row leaves at once.
-__global__ __launch_bounds__(kBlock) void sample_rows_pending_kernel(RowArgs a) {
+// kLPending | reason).  At most one workgroup per CU, each stepping over the
+// rows with the grid's stride, so a launch with nothing pending costs one
+// token read per row.
+__global__ __launch_bounds__(kBlock) void sample_rows_pending_kernel(RowArgs a, int32_t B) {
     __shared__ GeneralShared sh;
-    const int row = (int)blockIdx.x;
-    if (a.done != nullptr && a.done[row]) return;
-    const uint32_t t = a.tokens[row];
-    if ((t & kLPending) != kLPending) return;
-    general_row<1>(a, row, sh, t & ~kLPending);
+    for (int row = (int)blockIdx.x; row < B; row += (int)gridDim.x) {
+        if (a.done != nullptr && a.done[row]) continue;
+        const uint32_t t = a.tokens[row];
+        if ((t & kLPending) != kLPending) continue;
+        general_row<1>(a, row, sh, t & ~kLPending);
+        __syncthreads();  // (the next row reuses the shared state)
+    }
 }
 
 }  // namespace nis
