@@ -1,7 +1,6 @@
 // resident_path.h — one row per 1024-lane workgroup (16 wave64s, four per
-// SIMD), the row held in VGPRs (V <= 53245): the hot path of
-// nis_sample_batch for greedy rows, top-p off and top-p rows whose nucleus
-// is a small share of the vocabulary (src/sampler.rs:163-217).
+// SIMD), the row held in VGPRs (V <= 53245): nis_sample_batch for greedy
+// rows and top-p off (src/sampler.rs:163-217).
 //
 // Layout.  The row's float4 slots are split over the 16 waves in whole
 // 64-slot chunks, cpw per wave: chunk k / lane l of wave w holds slot
@@ -14,52 +13,21 @@
 // c_hi = f32(c)): the product of x with c's rounding error is recovered by a
 // second fma, so a mass depends on the depth below the maximum only through
 // the last rounding of its argument.  In the stream, R is an integer
-// reference of the wave (R_w, from its first chunk) and masses are f32,
-// summed in f64: the row total Z and the per-wave totals.  Candidates of the
-// top-p cutoff get exact fixed-point masses instead: bucket b = floor(64 t)
-// of t = f32(x c_hi) (monotone in x), octave o = b >> 6, and
-// fm = 2^f * 2^24 rounded down, f = fma(x, c_lo, fma(x, c_hi, -o)) (the
-// fraction, computed without cancellation), so fm << (o - R + 16) is the
-// mass in units of 2^(R - 40) with a relative error of ~1e-7 at any depth.
+// reference of the wave that follows its running max, and the masses are
+// f32, summed in f64.  The helpers for exact fixed-point masses of one
+// element (r_fm: 2^f * 2^24 rounded down, f = fma(x, c_lo, fma(x, c_hi, -o))
+// the fraction above octave o; r_key: the stable order as one key) serve the
+// dense and long-row kernels.
 //
-// Sparse top-p (sampler.rs:118-160) without a sort.  The reference keeps
-// sorted position pos iff D(pos) = cum_excl(pos) - q(pos) <= p Z; D is
-// non-decreasing in pos, so the kept set is a prefix of the stable order.
-//   Stream.  Each wave histograms the float4 maxima of its first kRS chunks
-//   (1/8-octave bins) and takes thc_w, the lower edge of the top bins holding
-//   at most kRTop of those 256 maxima; it publishes thc_w (an LDS max) and
-//   lists every float4 holding an element >= thl = max(thc_w, the published
-//   maximum so far) in an LDS ring.  Every 64 listed float4s, the wave turns
-//   them into candidates (elements >= thl) one entry per lane: the
-//   candidate's bucket and fm join a shared histogram of buckets (count << 48
-//   | sum of fm) and one of octaves, and the candidate is appended to the
-//   wave's record list (value, index, bucket, fm) in index order.  So the
-//   histogram is complete when the stream ends.
-//   Every element >= x_lo = max_w thc_w is a candidate of its wave, so the
-//   buckets from blo = 64 x_lo up are complete.
-//   Cutoff (every wave, the same data and instructions).  With G(b) the mass
-//   of the buckets above b and m_up(b) a bound of any mass in b, b_p is the
-//   deepest non-empty bucket with G(b) - m_up(b) <= p Z.  Everything below it
-//   is removed, everything above kept (the last element y of the next
-//   non-empty bucket above has D(y) <= G(b_p) - 2 m(y) < p Z), and the cutoff
-//   lies among b_p's members, ranked exactly (descending value, ascending
-//   index) against sampler.rs:150.  G(blo - 1) - m_up(blo - 1) > p Z proves
-//   that nothing below blo is kept.
-//   After the one barrier that ends the stream, each wave sums its kept
-//   records above b_p and lists its members of b_p; after a second barrier
-//   every wave ranks the members, and the wave holding the draw walks its
-//   records (sampler.rs:209-216).  Kept masses are exact integers (u64), so
-//   the totals and the walk agree to the last bit.
 // Top-p off: every element is kept; the walk goes waves -> chunks -> lanes
 // -> elements over the stream's own f32 masses (chunk totals from one
 // transposed LDS sum in the chosen wave), and the drawn token's probability
 // uses its exact mass.
 // Greedy (sampler.rs:172-181): the first index of the maximum.
 //
-// Any row this path cannot prove (non-finite values, a threshold above the
-// cutoff, list or bucket overflow, a kept range deeper than 16 octaves)
-// returns a reject code before anything is written, and the caller runs the
-// general path on it.
+// Any row this path cannot prove (non-finite values, a reference range too
+// wide for f32 masses) returns a reject code before anything is written, and
+// the caller runs the general path on it.
 #pragma once
 #include "fast_path.h"
 
@@ -70,17 +38,7 @@ constexpr int kRW = kRB / 64;              // waves per workgroup
 constexpr int kRN = 13;                    // float4 chunks per lane (at most)
 constexpr int kRMaxV = kRB * 4 * kRN - 3;  // 53245
 constexpr int kRD = 3;                     // loads in flight per lane ahead of the one in use
-constexpr int kRS = 4;                     // sample chunks per wave
-constexpr uint32_t kRTop = 44;             // sampled float4 maxima allowed above thc_w
-constexpr int kRQ = 128;                   // listed float4s awaiting their round (ring, per wave)
-constexpr int kRC = 256;                   // candidate records per wave
-constexpr int kRRes = 64;                  // buckets per octave
-constexpr int kRLog = 6;
-constexpr int kRHB = 32 * kRRes;           // bucket ring: 32 octaves
-constexpr int kRMem = 64;                  // members of the cutoff bucket
-constexpr int kRDeep = 16;                 // kept octaves below R (exact fixed point)
-
-enum { kResSparse = 0, kResAll = 1, kResGreedy = 2 };
+enum { kResAll = 1, kResGreedy = 2 };
 
 // Optional phase timestamps (profiling builds only, compiled out unless
 // NIS_RES_TIMING is defined): each wave keeps the 100 MHz clock of its phases
@@ -107,7 +65,8 @@ __device__ unsigned long long nis_res_ts[2048 * kRW * 16];
     } while (0)
 #endif
 
-// A candidate: its logit, row index, bucket and octave-relative mass.
+// A member of a cutoff bucket (dense and long-row kernels): its logit, row
+// index, octave and octave-relative fixed-point mass.
 struct alignas(16) RCand {
     float x;
     uint32_t idx;
@@ -119,61 +78,16 @@ struct alignas(16) RRec {
     double z;      // sum of 2^(x c - R_w) over the wave's elements (greedy: unused)
     float mx;      // wave max logit
     float rw;      // R_w
-    float thc;     // sample threshold in x c units (-inf: no data); greedy: best index
-    uint32_t nc;   // candidate records (> kRC: overflow)
+    float thc;     // greedy: the first index of the wave max
+    uint32_t nc;   // top-p off with stats: the wave's elements above -inf
     uint32_t bad;  // the wave saw input this path does not take
     uint32_t pad;
 };
 
-// The cutoff (wave 0 writes it between barriers).
-struct alignas(16) RCut {
-    unsigned long long gp;  // G(b_p): mass of the buckets above b_p, 2^(R - 40) units
-    double pz;              // p Z, the same units
-    double zr;              // Z, 2^R units
-    float M;                // row max
-    float R;                // ceil(M c)
-    int32_t bp;             // b_p
-    uint32_t nsel;          // candidates in b_p
-    uint32_t rej;           // NIS_REJECT_*
-    uint32_t nab;           // candidates above b_p
-    uint32_t pad[2];
-};
-// One wave's records after the cutoff: kept mass above b_p and count.
-struct alignas(16) RAbove {
-    unsigned long long m;
-    uint32_t n;
-    uint32_t pad;
-};
-
 struct ResShared {
-    union {
-        struct {
-            f4v q[kRW][kRQ];             // listed float4s, ring per wave
-            uint16_t qpos[kRW][kRQ];     //   chunk * 64 + lane
-            union {
-                RCand cand[kRW][kRC];    // candidates, index order per wave
-                uint32_t whist[kRW][256 * 4];  // (before them) each wave's sample histogram
-            } c;
-        } s;
-        float s4[kRW][kRN][64];          // top-p off: per-chunk per-lane f32 masses
-    } u;
-    unsigned long long hist[kRHB];       // [b & (kRHB-1)]: count << 48 | sum of fm
-    unsigned long long oct[32];          // the same per octave
-    RCand mem[kRMem];                    // members of b_p
+    float s4[kRW][kRN][64];  // top-p off: per-chunk per-lane f32 masses
     RRec rec[kRW];
-    RCut cut;
-    RAbove above[kRW];
-    unsigned long long otot[32];         // cutoff search: octave oM - j's total (2^(R - 40) units)
-    unsigned long long opass[kRW][2];    // each wave's deepest passing bucket (as u64) and G       // per-wave kept mass above b_p (2^(R-40) units)
-    double u0;                           // the draw
-    uint32_t nmem;
-    uint32_t kxlo;                       // running max of the published thresholds (key32)
-    // the waves' stream-end figures, reduced as they arrive (order-preserving keys)
-    uint32_t kmax;                       // row max
-    uint32_t krw;                        // lowest reference of a wave with data
-    uint32_t kth;                        // lowest threshold of a wave with candidates
-    uint32_t knc;                        // most candidate records of a wave
-    uint32_t kbad;                       // a wave saw input this path does not take
+    double u0;               // the draw
 };
 
 // u64 wave sum: DPP row sums, then the four row totals (uniform).
@@ -255,30 +169,11 @@ __device__ __forceinline__ float r_max4(const f4v& v) {
 __device__ __forceinline__ float r_mass(float x, float chi, float clo, float R) {
     return __builtin_amdgcn_exp2f(fmaf(x, clo, fmaf(x, chi, -R)));
 }
-// Bucket floor(64 f32(x c_hi)): monotone in x.
-__device__ __forceinline__ int r_bucket(float x, float chi) {
-    int b;
-    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(b) : "v"((x * chi) * (float)kRRes));
-    return b;
-}
 // Octave-relative fixed-point mass of x in octave o: 2^(x c - o) * 2^24,
 // rounded down (bounded by 2^25 + a few units: x c may round across o + 1).
 __device__ __forceinline__ uint32_t r_fm(float x, float chi, float clo, int o) {
     const float f = fmaf(x, clo, fmaf(x, chi, -(float)o));
     return (uint32_t)(__builtin_amdgcn_exp2f(f) * 16777216.0f);
-}
-// fm in octave o as an integer in 2^(R - 40) units (o >= R - 16 exact; a
-// deeper octave is truncated, which only ever lowers a sum).
-__device__ __forceinline__ unsigned long long r_u40(unsigned long long fm, int o, int R) {
-    const int sh = o - R + 16;
-    return sh >= 0 ? (fm << (uint32_t)min(sh, 63)) : (fm >> (uint32_t)min(-sh, 63));
-}
-// Upper bound of one element's mass in bucket b (its upper edge, inflated
-// for the roundings of x c and exp2), 2^(R - 40) units, as f64.
-__device__ __forceinline__ double r_mup(int b, int R) {
-    return ldexp((double)__builtin_amdgcn_exp2f((float)((b + 1) & (kRRes - 1)) * (1.0f / kRRes)) *
-                     1.0001,
-                 ((b + 1) >> kRLog) - R + 40);
 }
 // Stable descending order of sampler.rs:140 as one key: value, then index.
 __device__ __forceinline__ unsigned long long r_key(float x, uint32_t idx) {
@@ -292,7 +187,7 @@ __device__ __forceinline__ bool resident_eligible(const RowArgs a, int row) {
         if (!(a.temperature <= 0.0f)) return false;
     } else {
         if (!(a.temperature > 0.0f) || (a.top_k > 0 && a.top_k < (uint64_t)a.V)) return false;
-        if (MODE == kResAll ? !(a.top_p >= 1.0f) : !(a.top_p > 0.0f && a.top_p < 1.0f)) return false;
+        if (!(a.top_p >= 1.0f)) return false;
     }
     int64_t g0 = 0, g1 = 0;
     if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) return false;
@@ -330,20 +225,6 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     f4v xv[kRN];
     xv[0] = nis_buffer_load_f4(rsrc, (Kw > 0) ? 16 * max(slot0, f_lo) : 0x7FFFFFF0, 0, 2);
     __builtin_amdgcn_sched_barrier(0);
-    if (MODE == kResSparse) {
-        *reinterpret_cast<u4v*>(&sh.hist[w * (kRHB / kRW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
-        if (l < 32 / kRW) sh.oct[w * (32 / kRW) + l] = 0ull;
-        if (w == 0 && l == 0) {
-            sh.nmem = 0u;
-            sh.kxlo = 0u;
-            sh.kmax = 0u;
-            sh.krw = 0xFFFFFFFFu;
-            sh.kth = 0xFFFFFFFFu;
-            sh.knc = 0u;
-            sh.kbad = 0u;
-        }
-        lds_barrier();
-    }
     const int voff = 16 * slot0;
 #define NIS_RLOAD(k)                                                                          \
     do {                                                                                      \
@@ -545,7 +426,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const double rw_ = ldexp(r - bcast_f64(Tincl - T, ws), (int)(R - Rz));
         // chunk totals (2^Rz units, exact rescales): a transposed sum of the
         // per-lane chunk masses
-        float* const s4w = &sh.u.s4[w][0][0];
+        float* const s4w = &sh.s4[w][0][0];
 #pragma unroll
         for (int k = 0; k < kRN; ++k) s4w[k * 64 + l] = ldexpf(s4v[k], (int)(Rk[k] - Rz));
         lds_wave_fence();
@@ -626,422 +507,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         return NIS_REJECT_NONE;
     }
 
-    // =====================================================================
-    // ---- sparse top-p -----------------------------------------------------
-    const float p = a.top_p;
-    const float RwH = Rw + 8.0f;  // top of the sample histogram (8 octaves of head room)
-    double z = 0.0;
-    float mx = -INFINITY;
-    float czh = chi, czl = clo, Rz = Rw;
-    asm volatile("" : "+v"(czh), "+v"(czl));
-    float thc = INFINITY;  // this wave's sample threshold (x c units, a multiple of 1/8)
-    float thl = INFINITY;  // its listing threshold: thc raised to the waves' running max
-    float thx = INFINITY;  // the same in logit units, rounded down
-    uint32_t nq = 0;       // float4s listed (ring position)
-    uint32_t np = 0;       // of them turned into candidates
-    uint32_t nc = 0;       // candidate records
-    float mcs[kRS];
-    uint32_t* const whist = &sh.u.s.c.whist[w][0];
-    *reinterpret_cast<u4v*>(&whist[4 * l]) = u4v{0u, 0u, 0u, 0u};
-    const uint32_t q0 = lds_addr(&sh.u.s.q[w][0]), qp0 = lds_addr(&sh.u.s.qpos[w][0]);
-    const uint32_t cand0 = lds_addr(&sh.u.s.c.cand[w][0]);
-    const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
-
-    // list the float4s of chunk k holding an element >= the threshold
-#define NIS_RLIST(k, cond)                                                                  \
-    {                                                                                       \
-        const uint64_t mk = __ballot(cond);                                                 \
-        const uint32_t slot = (nq + lane_rank(mk)) & (uint32_t)(kRQ - 1);                   \
-        lds_put_x4_u16(mk, q0 + 16 * slot, xv[k], qp0 + 2 * slot, (uint32_t)((k) * 64 + l)); \
-        nq += (uint32_t)__popcll(mk);                                                       \
-    }
-    // One round: lane j takes listed float4 np + j (if listed); its elements
-    // >= thl become candidates: histograms and records (index order).
-    auto round = [&](uint32_t navail) {
-        const uint32_t j = np + (uint32_t)l;
-        const bool has = (uint32_t)l < navail;
-        lds_wave_fence();
-        const uint32_t slot = j & (uint32_t)(kRQ - 1);
-        const f4v v = sh.u.s.q[w][slot];
-        const uint32_t pos = sh.u.s.qpos[w][slot];
-        const int ib = 4 * (wbase + 64 * (int)(pos >> 6) + (int)(pos & 63u)) - mis;
-        uint32_t cm = 0u;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) cm |= (has & (elem(v, qq) * chi >= thl)) ? (1u << qq) : 0u;
-        const uint32_t cnt = (uint32_t)__popc(cm);
-        const uint32_t incl = wscan_u32(cnt);
-        const uint32_t cb = nc + incl - cnt;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-            const bool ok = (cm >> qq) & 1u;
-            const uint64_t am = __ballot(ok);
-            if (am) {
-                const float x = elem(v, qq);
-                const int b = r_bucket(x, chi);
-                const int o = b >> kRLog;
-                const uint32_t fm = r_fm(x, chi, clo, o);
-                const uint32_t rs = cb + (uint32_t)__popc(cm & ((1u << qq) - 1u));
-                lds_add_u64x2(am, hist0 + 8 * ((uint32_t)b & (uint32_t)(kRHB - 1)),
-                              oct0 + 8 * ((uint32_t)o & 31u), (1ull << 48) | (uint64_t)fm);
-                const uint64_t wm = __ballot(ok & (rs < (uint32_t)kRC));
-                lds_put_b128_m(wm, cand0 + 16 * min(rs, (uint32_t)kRC - 1),
-                               u4v{__float_as_uint(x), (uint32_t)(ib + qq), (uint32_t)b, fm});
-            }
-        }
-        nc += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-        np += min(navail, 64u);
-    };
-
-#pragma unroll
-    for (int k = 0; k < kRN; ++k) {
-        if (k + kRD < kRN) NIS_RLOAD(k + kRD);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k >= Kw && k >= kRS) continue;
-        if (k > 0) NIS_RFIX(k);
-        const f4v x = xv[k];
-        const float m4 = r_max4(x);
-        mx = fmaxf(mx, m4);
-        NIS_RESCALE(m4)
-        const float e0 = r_mass(x.x, czh, czl, Rz), e1 = r_mass(x.y, czh, czl, Rz);
-        const float e2 = r_mass(x.z, czh, czl, Rz), e3 = r_mass(x.w, czh, czl, Rz);
-        z += (double)((e0 + e1) + (e2 + e3));
-        if (k < kRS) {
-            const float mc = m4 * chi;
-            mcs[k] = mc;
-            const float tb = floorf((RwH - mc) * 8.0f);  // -inf -> +inf
-            atomicAdd(&whist[(uint32_t)fminf(fmaxf(tb, 0.0f), 255.0f)], 1u);
-        }
-        if (k == kRS - 1) {
-            lds_wave_fence();  // (the wave's own histogram adds)
-            const u4v hc = *reinterpret_cast<const u4v*>(&whist[4 * l]);  // bins 4l..4l+3
-            const uint32_t hs = hc.x + hc.y + hc.z + hc.w;
-            const uint32_t hi = wscan_u32(hs);
-            const uint32_t c0 = hi - hs + hc.x, c1 = c0 + hc.y, c2 = c1 + hc.z, c3 = c2 + hc.w;
-            const uint32_t nok = (uint32_t)(c0 <= kRTop) + (uint32_t)(c1 <= kRTop) +
-                                 (uint32_t)(c2 <= kRTop) + (uint32_t)(c3 <= kRTop);
-            const int bw = (int)wsum_u32(nok) - 1;  // last bin whose cumulative count fits
-            thc = (bw < 0 || Kw == 0) ? INFINITY : RwH - (float)(bw + 1) * 0.125f;
-            // x_lo = max_w thc_w bounds the complete range, so nothing below
-            // the running max of the thresholds published so far is needed
-            if (Kw > 0 && l == 0) atomicMax(&sh.kxlo, key32(thc));
-            lds_wave_fence();
-            thl = fmaxf(thc, unkey32(sh.kxlo));
-            // thl in logit units, rounded down: x >= thx whenever x * c >= thl
-            thx = thl < INFINITY ? thl / chi - fabsf(thl / chi) * 1.0e-6f - 1.0e-30f : INFINITY;
-#pragma unroll
-            for (int j = 0; j < kRS; ++j) {
-                NIS_RLIST(j, mcs[j] >= thl)
-                if (nq - np >= 64u) round(64u);  // (the ring holds at most 127 pending)
-            }
-        }
-        if (k >= kRS) {
-            NIS_RLIST(k, m4 >= thx)
-            if (nq - np >= 64u) round(64u);
-        }
-    }
-#undef NIS_RLIST
-
-    // ---- stream end ----------------------------------------------------------
-    NIS_RTS(2);
-    __builtin_amdgcn_s_setprio(0);
-    thl = fmaxf(thl, unkey32(sh.kxlo));
-    while (nq != np) round(nq - np);  // (at most two rounds)
-    mx = wmax_f32(mx);
-    z = wsum_f64(z);
-    if (l == 0) {
-        RRec r;
-        r.z = z;
-        r.mx = mx;
-        r.rw = Rz;
-        r.thc = Kw > 0 ? thc : -INFINITY;
-        r.nc = nc;
-        r.bad = (uint32_t)!(z < INFINITY);
-        r.pad = 0u;
-        sh.rec[w] = r;
-        atomicMax(&sh.kmax, key32(mx));
-        if (mx > -INFINITY) atomicMin(&sh.krw, key32(Rz));
-        if (nc > 0u) atomicMin(&sh.kth, key32(thc));
-        atomicMax(&sh.knc, nc);
-        if (!(z < INFINITY)) atomicOr(&sh.kbad, 1u);
-    }
-    // the row's one draw (sampler.rs:209), by wave 0; the advanced state is
-    // stored once the row cannot be declined any more
-    uint64_t rst = 0;
-    if (w == 0) {
-        uint64_t st[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
-        const double u0 = rng_next_f64(st);
-        if (l == 0) sh.u0 = u0;
-        rst = (l == 0) ? st[0] : (l == 1) ? st[1] : (l == 2) ? st[2] : st[3];
-    }
-    // ---- B1: every wave's stream, histogram and records are complete ---------
-    NIS_RTS(3);
-    lds_barrier();
-    NIS_RTS(4);
-    const bool rv = l < kRW;
-    // the row max and R = ceil(M c) (every wave)
-    const float M = unkey32(sh.kmax);
-    const float R = (M > -INFINITY && fabsf(M * chi) < 1e30f) ? ceilf(M * chi) : 0.0f;
-    const int Ri = (int)R;
-    if (w == 0) {
-        // ---- wave 0: Z, the checks and the cutoff ----------------------------
-        const RRec rr = sh.rec[rv ? l : 0];
-        const double ZR = r16_sum(rv ? ldexp(rr.z, (int)(rr.rw - R)) : 0.0);
-        const double pz = (double)p * ZR * 1099511627776.0;  // p Z in 2^(R - 40) units
-        const float xlo = unkey32(sh.kxlo);
-        const float rwmin = unkey32(sh.krw), thmin = unkey32(sh.kth);
-        const bool fin = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * chi) < 1e6f) & (ZR > 0.0) &
-                         (ZR < INFINITY) & (sh.kbad == 0u) & (fmaf(M, chi, -rwmin) <= 100.0f);
-        const int bM = fin ? r_bucket(M, chi) : 0;
-        const bool xok = (xlo < INFINITY) & (xlo <= M * chi);
-        const int blo = xok ? (int)(xlo * (float)kRRes) : 0;  // xlo: a multiple of 1/8
-        const int oM = bM >> kRLog, olo = blo >> kRLog;
-        RCut cut;
-        cut.gp = 0ull;
-        cut.pz = pz;
-        cut.zr = ZR;
-        cut.M = M;
-        cut.R = R;
-        cut.bp = 0;
-        cut.nsel = 0u;
-        cut.nab = 0u;
-        cut.rej = NIS_REJECT_NONE;
-        if (!fin) {
-            cut.rej = NIS_REJECT_NONFINITE;
-        } else if (sh.knc > (uint32_t)kRC || !(bM - (int)(thmin * (float)kRRes) < kRHB - kRRes)) {
-            cut.rej = NIS_REJECT_CAPACITY;
-        } else if (!xok) {
-            cut.rej = NIS_REJECT_WINDOW;
-        } else {
-            // level 1: lane l takes octave oM - l; the octaves above olo are
-            // complete (their own histogram), octave olo only from blo up (its
-            // buckets, summed beside)
-            const int o = oM - l;
-            const bool oin = l <= oM - olo;
-            const bool ofull = l < oM - olo;
-            const unsigned long long ovr = ofull ? sh.oct[(uint32_t)o & 31u] : 0ull;
-            const int bl = kRRes * olo + l;
-            const unsigned long long lv = (bl >= blo && bl <= bM) ? sh.hist[(uint32_t)bl & (kRHB - 1)] : 0ull;
-            const unsigned long long omf = r_u40(ovr & 0xFFFFFFFFFFFFull, o, Ri);
-            const unsigned long long lm = r_u40(lv & 0xFFFFFFFFFFFFull, olo, Ri);
-            const uint32_t onf = (uint32_t)(ovr >> 48), ln = (uint32_t)(lv >> 48);
-            const unsigned long long oincl = rscan_u64w(omf);  // the two scans run side by side
-            const unsigned long long lincl = rscan_u64w(lm);
-            const uint32_t ocincl = wscan_u32(onf), lcincl = wscan_u32(ln);
-            const unsigned long long gfull = rbcast_u64(oincl, 63);   // octaves above olo
-            const unsigned long long mlo = rbcast_u64(lincl, 63);     // octave olo from blo up
-            const uint32_t cfull = bcast_u32(ocincl, 63), clo_n = bcast_u32(lcincl, 63);
-            const bool islo = l == oM - olo;
-            const unsigned long long om = islo ? mlo : omf;
-            const uint32_t on = islo ? clo_n : onf;
-            const unsigned long long Go = islo ? gfull : oincl - omf;  // mass of the octaves above
-            const uint32_t Co = islo ? cfull : ocincl - onf;
-            const unsigned long long gtot = gfull + mlo;  // everything >= blo
-            const uint64_t P = __ballot(oin & (on != 0u) & ((double)Go - ldexp(1.0001, o + 1 - Ri + 40) <= pz));
-            const uint64_t NEo = __ballot(oin & (on != 0u));
-            (void)om;
-            // everything below blo is removed: G(blo - 1) - m_up(blo - 1) > p Z
-            if (!((double)gtot - r_mup(blo - 1, Ri) > pz) || !P) {
-                cut.rej = NIS_REJECT_WINDOW;
-            } else {
-                const int lp = 63 - __clzll((long long)P);  // deepest passing octave
-                const uint64_t up = NEo & ((1ull << lp) - 1ull);
-                const int la = up ? 63 - __clzll((long long)up) : -1;  // next non-empty octave above
-                // level 2: lane l takes bucket 64 O + 63 - l of O = Op (then Oa)
-                int L = -1;
-#pragma unroll
-                for (int pass2 = 0; pass2 < 2; ++pass2) {
-                    if (L < 0 && (pass2 == 0 || la >= 0)) {
-                        const int lo2 = pass2 == 0 ? lp : la;
-                        const int O = oM - lo2;
-                        const unsigned long long GO = rbcast_u64(Go, lo2);
-                        const uint32_t CO = bcast_u32(Co, lo2);
-                        const int b = kRRes * O + (kRRes - 1) - l;
-                        const bool bin = (b >= blo) & (b <= bM);
-                        const unsigned long long bv = bin ? sh.hist[(uint32_t)b & (kRHB - 1)] : 0ull;
-                        const uint32_t bn = (uint32_t)(bv >> 48);
-                        const unsigned long long bm = r_u40(bv & 0xFFFFFFFFFFFFull, O, Ri);
-                        const unsigned long long Gb = GO + (rscan_u64w(bm) - bm);
-                        const uint32_t Cb = CO + (wscan_u32(bn) - bn);
-                        // Op: its deepest passing bucket; Oa (when Op has none):
-                        // its lowest non-empty bucket, which then passes
-                        const uint64_t sel = pass2 == 0
-                                                 ? __ballot((bn != 0u) & ((double)Gb - r_mup(b, Ri) <= pz))
-                                                 : __ballot(bn != 0u);
-                        if (sel) {
-                            L = 63 - __clzll((long long)sel);
-                            cut.bp = (int32_t)bcast_u32((uint32_t)b, L);
-                            cut.gp = rbcast_u64(Gb, L);
-                            cut.nsel = bcast_u32(bn, L);
-                            cut.nab = bcast_u32(Cb, L);
-                        }
-                    }
-                }
-                // kept masses stay exact integers: b_p within kRDeep octaves of R
-                if (L < 0 || (cut.bp >> kRLog) < Ri - kRDeep) cut.rej = NIS_REJECT_WINDOW;
-                else if (cut.nsel > (uint32_t)kRMem) cut.rej = NIS_REJECT_BUCKET;
-            }
-        }
-        if (l == 0) sh.cut = cut;
-    }
-    // every wave: its records, j = 64 i + l (consecutive lanes, consecutive
-    // slots), and their masses, while wave 0 searches
-    const int nrec = (int)min(nc, (uint32_t)kRC);
-    RCand cr[4];
-    unsigned long long cmu[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cr[i] = sh.u.s.c.cand[w][64 * i + l];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (64 * i + l >= nrec) cr[i].b = INT32_MIN;  // below any b_p: never kept, never a member
-        cmu[i] = r_u40(cr[i].fm, cr[i].b >> kRLog, Ri);
-    }
-    // ---- B1b: the cutoff bucket is known ------------------------------------
-    lds_barrier();
-    NIS_RTS(5);
-    const RCut cut = sh.cut;
-    if (cut.rej != NIS_REJECT_NONE) return cut.rej;
-    const int bp = cut.bp;
-    // this wave's kept mass above b_p and its members of b_p
-    {
-        unsigned long long al = 0ull;
-        uint32_t mb = 0u;  // bit i: record 64 i + l is a member of b_p
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            al += (cr[i].b > bp) ? cmu[i] : 0ull;
-            mb |= (cr[i].b == bp) ? (1u << i) : 0u;
-        }
-        const unsigned long long at = wsum_u64(al);
-        if (__ballot(mb != 0u)) {
-            const uint32_t mcnt = (uint32_t)__popc(mb);
-            const uint32_t mincl = wscan_u32(mcnt);
-            const uint32_t mtot = (uint32_t)__builtin_amdgcn_readlane((int)mincl, 63);
-            uint32_t mbase = 0u;
-            if (l == 0) mbase = atomicAdd(&sh.nmem, mtot);
-            uint32_t slot = bcast_u32(mbase, 0) + mincl - mcnt;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if ((mb >> i) & 1u) {
-                    RCand m = cr[i];
-                    m.b = w;  // (the owner wave travels in place of the bucket)
-                    sh.mem[min(slot, (uint32_t)kRMem - 1)] = m;
-                    ++slot;
-                }
-            }
-        }
-        if (l == 0) sh.above[w].m = at;
-    }
-    // ---- B2: members and per-wave sums are complete ------------------------
-    lds_barrier();
-    NIS_RTS(6);
-    const int n = (int)sh.nmem;
-    if ((uint32_t)n != cut.nsel) return NIS_REJECT_BUCKET;
-    if (w != 0) {
-        NIS_RTFLUSH();
-        return NIS_REJECT_NONE;
-    }
-    const unsigned long long gp = cut.gp;
-    const double pz = cut.pz;
-    // ---- wave 0: rank the members (stable descending order: value, index),
-    // pick the wave holding the draw and walk its records -------------------
-    if (l < 4) a.rng[4 * (int64_t)row + l] = rst;
-    const bool valid = l < n;
-    const RCand mr = sh.mem[min(l, kRMem - 1)];
-    const unsigned long long Km = valid ? r_key(mr.x, mr.idx) : 0ull;
-    const unsigned long long em = valid ? r_u40(mr.fm, bp >> kRLog, Ri) : 0ull;
-    unsigned long long pre = 0ull;  // mass of the members ahead of this one
-    uint32_t rk = 0u;
-    for (int j = 0; j < n; ++j) {
-        const unsigned long long Kj = rbcast_u64(Km, j);
-        const unsigned long long ej = rbcast_u64(em, j);
-        pre += (Kj > Km) ? ej : 0ull;
-        rk += (Kj > Km) ? 1u : 0u;
-    }
-    // sampler.rs:150 in rank order: D = G + pre - e; the kept ones are the
-    // longest prefix of ranks with D <= p Z
-    const bool pass = valid & ((double)(long long)(gp + pre - em) <= pz);
-    uint32_t nkept = (uint32_t)n;
-    if (__ballot(valid & !pass)) nkept = wmin_u32((valid && !pass) ? rk : 0xFFFFFFFFu);
-    const bool kept = valid & (rk < nkept);
-    const uint64_t lastm = __ballot(valid & (rk + 1u == nkept));
-    const unsigned long long Kcut = lastm ? rbcast_u64(Km, __ffsll((long long)lastm) - 1) : ~0ull;
-    const unsigned long long kmass = kept ? em : 0ull;
-    const unsigned long long zk = gp + rbcast_u64(rscan_u64w(kmass), 63);
-    // per-wave kept totals: above b_p plus the kept members each wave owns
-    const RAbove abv = sh.above[rv ? l : 0];
-    unsigned long long T = rv ? abv.m : 0ull;
-    for (int j = 0; j < n; ++j) {
-        const unsigned long long ej = rbcast_u64(kmass, j);
-        const int oj = (int)bcast_u32((uint32_t)mr.b, j);
-        T += (l == oj) ? ej : 0ull;
-    }
-    const unsigned long long Tincl = rscan16_u64(T);
-    const double u = sh.u0;
-    // the walk stops at the first kept element whose inclusive prefix P
-    // reaches r = u Z_kept; P is an integer, so P >= r iff P >= ceil(r)
-    const unsigned long long rc = (unsigned long long)ceil(u * (double)zk);
-    const uint64_t hw = __ballot(rv & (T > 0ull) & (Tincl >= rc));
-    const uint64_t nzw = __ballot(rv & (T > 0ull));
-    const int ws = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)(nzw | 1ull)));
-    unsigned long long acc = rbcast_u64(Tincl - T, ws);
-    NIS_RTS(8);
-    // the chosen wave's kept records in index order j = 64 i + l (round i,
-    // then lane): the round holding the crossing, then the lane
-    const int nrw = (int)min(sh.rec[ws].nc, (uint32_t)kRC);
-    RCand wr[4];
-    unsigned long long me[4], sc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wr[i] = sh.u.s.c.cand[ws][64 * i + l];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const bool kp = (64 * i + l < nrw) &
-                        ((wr[i].b > bp) | ((wr[i].b == bp) & (r_key(wr[i].x, wr[i].idx) >= Kcut)));
-        me[i] = kp ? r_u40(wr[i].fm, wr[i].b >> kRLog, Ri) : 0ull;
-        sc[i] = rscan_u64w(me[i]);
-    }
-    int ic = -1, lc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const unsigned long long tot = rbcast_u64(sc[i], 63);
-        if (ic < 0 && tot > 0ull) {
-            if (acc + tot >= rc || i == 3 || 64 * (i + 1) >= nrw) {
-                // the crossing (or, if rounding leaves r above every prefix,
-                // the last kept record) lies in this round
-                const uint64_t hl = __ballot((me[i] > 0ull) & (acc + sc[i] >= rc));
-                const uint64_t nzl = __ballot(me[i] > 0ull);
-                lc = hl ? (__ffsll((long long)hl) - 1) : (63 - __clzll((long long)nzl));
-                ic = i;
-            }
-            acc += tot;
-        }
-    }
-    if (ic < 0) ic = 0;  // (cannot happen: the chosen wave holds kept mass)
-    const uint32_t nab = cut.nab;
-    if (l == lc) {
-        RCand t = wr[0];
-        unsigned long long et = me[0];
-#pragma unroll
-        for (int i = 1; i < 4; ++i)
-            if (i == ic) {
-                t = wr[i];
-                et = me[i];
-            }
-        uint32_t tok = t.idx;
-        if (u == 0.0) tok = 0u;  // r == 0 stops the reference's walk at index 0
-        emit_token(a, row, tok);
-        if (a.stats) {
-            // 2^(R - M c): units of 2^R -> units of the max element's mass
-            const double rho = exp2((double)cut.R - (double)cut.M * c64);
-            write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)cut.M / temp,
-                            (double)zk / 1099511627776.0 * rho, cut.zr * rho, u,
-                            (u == 0.0) ? 0.0 : (double)et / (double)zk, (uint64_t)(nab + nkept), 1);
-        }
-    }
-    NIS_RTS(9);
-    NIS_RTFLUSH();
-    return NIS_REJECT_NONE;
+    return NIS_REJECT_NONE;  // (no other mode)
 #undef NIS_RLOAD
 #undef NIS_RFIX
 #undef NIS_RIDX

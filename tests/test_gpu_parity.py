@@ -360,3 +360,30 @@ def test_invalid_arguments_are_rejected(sampler):
     assert b"reserved" in L.nis_last_error(h)
     with pytest.raises(ns.SamplerError):
         sampler.sample_batch(x, ns.SamplingParams(), st, V=32)
+
+
+def test_penalty_launch_rows_without_history_take_the_512_lane_fast_path(sampler):
+    # A penalty launch runs on the 512-lane kernel; its rows whose history is
+    # still empty take that kernel's register-resident routes (kernel == 1):
+    # the sparse route (reject 0) at top-p 0.9, the dense route at top-p off
+    # (reject 0: no sparse attempt); rows with a history run the general path
+    # (kernel == 2).  Top-p 0.99 is checked for parity only.
+    from nimbus_sampler import workloads
+    B, V = 32, 50257
+    rnd = np.random.Generator(np.random.PCG64(31))
+    x = workloads.headline(B)
+    gen = [np.array([], np.int64) if r % 2 == 0 else rnd.integers(0, V, size=12) for r in range(B)]
+    off = np.zeros(B + 1, np.int64)
+    off[1:] = np.cumsum([len(g) for g in gen])
+    ids = np.concatenate(gen).astype(np.uint32)
+    empty = np.array([len(g) == 0 for g in gen])
+    for p in (0.9, 0.99, 1.0):
+        params = _params(temperature=0.8, top_p=p, repetition_penalty=1.2)
+        gpu = run_gpu(sampler, x, V, params, list(range(B)), ids, off)
+        ref = run_oracle(x, V, params, list(range(B)), ids, off)
+        compare(gpu, ref, greedy=False)
+        st = gpu[1]
+        assert (st["kernel"][~empty] == 2).all(), st["kernel"]
+        if p != 0.99:
+            assert (st["kernel"][empty] == 1).all(), st["kernel"]
+            assert (st["reject"][empty] == 0).all(), st["reject"]
