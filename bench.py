@@ -139,15 +139,18 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
     import torch
     B, V = w.B, w.V
     dev = tokens.device
-    cap = 64
-    gen_ids = torch.zeros((B, cap), dtype=torch.int32, device=dev)
+    H = args.history
+    cap = 64 + H
+    # the first H ids of every history: random tokens already generated
+    gen_ids = torch.randint(0, V, (B, cap), generator=torch.Generator().manual_seed(3),
+                            dtype=torch.int32).to(dev)
     gen_len = torch.zeros(B, dtype=torch.int32, device=dev)
     max_new = torch.full((B,), cap, dtype=torch.int32, device=dev)
     done = torch.zeros(B, dtype=torch.uint8, device=dev)
     G = len(bufs)
 
     def block(n):
-        gen_len.zero_()
+        gen_len.fill_(H)
         done.zero_()
         for i in range(n):
             sampler.decode_step(bufs[i], params, states, gen_ids, gen_len, max_new, done,
@@ -155,7 +158,7 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
 
     for i in range(args.warmup):
         if i % G == 0:
-            gen_len.zero_()
+            gen_len.fill_(H)
             done.zero_()
         sampler.decode_step(bufs[i % G], params, states, gen_ids, gen_len, max_new, done,
                             tokens=tokens)
@@ -173,15 +176,18 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / K
-    assert int(gen_len[0].item()) == (K % G or G) and int(done.sum().item()) == 0
+    assert int(gen_len[0].item()) == H + (K % G or G) and int(done.sum().item()) == 0
     alg_bytes = B * (4 * V + 68) + B * (4 + 4 + 1)  # logits, RNG, token + history, length, flag
+    if params.repetition_penalty != 1.0:
+        alg_bytes += B * 4 * H  # the histories read as penalty lists (at least H ids each)
     print(json.dumps({
         "metric": f"decode steps: tokens/s, B={B} sequences x V={V} fp32, "
-                  f"T={w.temperature} top-p={w.top_p}",
+                  f"T={w.temperature} top-p={w.top_p} repetition-penalty={params.repetition_penalty}",
         "value": B / (us * 1e-6), "unit": "tokens/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "us_per_step": us, "higher_is_better": True,
         "data": "synthetic logits of the workload, 8 rotated batches resident in HBM",
         "config": {"workload": args.workload, "B": B, "V": V, "history_cap": cap,
+                   "history_at_start": H, "repetition_penalty": params.repetition_penalty,
                    "launch": f"hipGraph replays of up to {G} nis_decode_step calls after "
                              "clearing the lengths and flags"},
         "roofline": {"bound": "hbm", "achieved": alg_bytes / (us * 1e-6) / 1e9,
@@ -292,6 +298,11 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="time nis_decode_step (sample + on-device history / stop / budget "
                          "update) on the workload instead, and print that line")
+    ap.add_argument("--penalty", type=float, default=1.0,
+                    help="repetition penalty of --decode (sampler.rs:83-101; the histories "
+                         "are the penalty lists)")
+    ap.add_argument("--history", type=int, default=0,
+                    help="ids already in every history when a --decode replay starts")
     ap.add_argument("--lm-head", choices=("f32", "int8", "int4"), default=None,
                     help="time the LM-head logits producer with these weights instead")
     ap.add_argument("--lm-b", type=int, default=256, help="hidden rows for --lm-head")
@@ -334,7 +345,8 @@ def main():
     B, V = w.B, w.V
     dev = torch.device("cuda:0")
     sampler = ns.Sampler(0)
-    params = ns.SamplingParams(temperature=w.temperature, top_p=w.top_p)
+    params = ns.SamplingParams(temperature=w.temperature, top_p=w.top_p,
+                               repetition_penalty=args.penalty if args.decode else 1.0)
 
     host0 = w.make(B)
     # distinct batches of the same distribution: rows permuted, columns rolled

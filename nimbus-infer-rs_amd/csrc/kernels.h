@@ -33,8 +33,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(RowArgs a) {
 // Sparse top-p rows: one 1024-lane workgroup per row.  A row the sparse
 // path declines (or cannot take) runs the general path on the first 512
 // lanes; the other waves leave first, so the general path's barriers count
-// only its own eight waves.
-__global__ __launch_bounds__(kSB) void sample_rows_sparse_kernel(RowArgs a) {
+// only its own eight waves.  PEN: the launch carries a repetition-penalty
+// history, applied inside the sparse path.
+template <bool PEN>
+__device__ __forceinline__ void sparse_rows_body(const RowArgs& a) {
     __shared__ union {
         GeneralShared g;
         WideShared s;
@@ -44,13 +46,19 @@ __global__ __launch_bounds__(kSB) void sample_rows_sparse_kernel(RowArgs a) {
     asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
                  "s"(a.penalty), "s"(a.top_k), "s"(a.gen_ids), "s"(a.gen_off));
     uint32_t reject = NIS_REJECT_SHAPE;
-    if (sparse_eligible(a, row)) {
-        reject = sparse_row(a, row, sh.s);
+    if (sparse_eligible<PEN>(a, row)) {
+        reject = sparse_row<PEN>(a, row, sh.s);
         if (reject == NIS_REJECT_NONE) return;
     }
     if (threadIdx.x >= kBlock) return;
     __syncthreads();
     general_row<1>(a, row, sh.g, reject);
+}
+__global__ __launch_bounds__(kSB) void sample_rows_sparse_kernel(RowArgs a) {
+    sparse_rows_body<false>(a);
+}
+__global__ __launch_bounds__(kSB) void sample_rows_sparse_pen_kernel(RowArgs a) {
+    sparse_rows_body<true>(a);
 }
 
 // General path only (used by tests to cross-check the two paths).

@@ -1,6 +1,7 @@
 // sparse_path.h — sparse top-p sampler: one row per 1024-lane workgroup
 // (16 wave64s, four per SIMD), for rows whose nucleus holds a small share of
-// the vocabulary (V <= 53245, 0 < top_p < 1, T > 0, no penalty, no top-k).
+// the vocabulary (V <= 53245, 0 < top_p < 1, T > 0, no top-k; a repetition-
+// penalty history is applied by the PEN form, described at sparse_row).
 //
 // Stream.  Chunk k / lane l of wave w holds float4 slot base_w + 64k + l, so
 // each wave owns a contiguous index range of up to 13 chunks.  Every lane
@@ -68,6 +69,12 @@ constexpr int kSHB = 32 * kSRes;            // bucket ring: 32 octaves
 constexpr int kSPer = kSHB / 64;            // search rounds (64 buckets each, at most)
 constexpr int kSMem = 64;                   // members of the cutoff bucket
 constexpr uint32_t kSNone = 0x80000000u;    // packed bucket of no candidate (below any b_p)
+// repetition penalty (sample_rows_sparse_pen_kernel)
+constexpr int kSHist = 4 * kSB;             // history entries per row (raw, with repeats)
+constexpr int kSSide = 48;                  // penalised elements per wave
+constexpr int kSSlot = 32;                  // float4 slots holding them, per wave
+constexpr int kSNibW = kSMaxV / 32 + 2;     // words of 4-bit slot masks (8 slots per word)
+constexpr int kSPslW = kSMaxV / 256 + 2;    // slot bitmap words (64-bit)
 constexpr int kSRounds = 4 * kSSeg;         // candidates per lane (at most)
 constexpr double kS40 = 1099511627776.0;    // 2^40
 
@@ -113,7 +120,8 @@ struct alignas(16) SRec {
     float rw;     // R_w
     float thc;    // listing threshold in units of x*c (-inf: the wave holds no data)
     uint32_t n;   // float4s listed (may exceed kSE: overflow)
-    uint32_t pad[2];
+    uint32_t ns;  // penalised elements on the side list (PEN)
+    uint32_t pad;
 };
 // A member of the cutoff bucket.
 struct alignas(16) SMem {
@@ -156,6 +164,22 @@ struct WideShared {
     uint32_t kthmin;               // min listing threshold of a wave with entries
     uint32_t krwmin;               // min R_w of a wave with data
     uint32_t nmax;                 // largest list
+    // repetition penalty only (sparse_row<true>)
+    unsigned long long pslot[kSPslW];  // bit s: float4 slot s holds a penalised element
+    uint32_t pnib[kSNibW];             // bits 4 (s % 8) + q of word s / 8: element q of slot s
+    f4v sx4[kSW][kSSlot];              // slots met in the stream holding penalised elements
+    uint32_t sslot[kSW][kSSlot];       //   slot << 4 | mask of the penalised elements
+    double memy[kSMem];                // members' values after the penalty (f64)
+    unsigned long long kymax;          // key64 of the largest penalised value (f64)
+    uint32_t kmaxp;                    // key32 of the same rounded up to a float
+    uint32_t pover;                    // some wave met more than kSSide penalised elements
+};
+// A penalised element after the stream (16 bytes; kept in its wave's
+// sample-histogram slot, which is free by then).
+struct alignas(16) SSide {
+    double y;      // penalised logit (f64, sampler.rs:94-98)
+    uint32_t idx;  // row index
+    uint32_t tag;  // bit 0: candidate; after the cutoff: class << 8 | segment << 16
 };
 
 // Octave-relative fixed-point mass of a logit with t = x*c already rounded:
@@ -184,6 +208,34 @@ __device__ __forceinline__ double s_mup(int b, int R) {
                      1.0001,
                  ((b + 1) >> kSLog) - R + 40);
 }
+// 2^(yc - R) in f64 for a penalised element (yc = y c in f64): the f32 exp2
+// of the fractional part, scaled exactly.
+__device__ __forceinline__ double s_pmass(double yc, float R) {
+    const double d = yc - (double)R;
+    if (!(d == d)) return d;  // NaN stays NaN (the row is declined through Z)
+    if (d < -1100.0) return 0.0;
+    if (d > 1100.0) return INFINITY;
+    const double fl = floor(d);
+    return ldexp((double)__builtin_amdgcn_exp2f((float)(d - fl)), (int)fl);
+}
+// Octave-relative fixed-point mass of a penalised element: 2^(yc - floor(t))
+// * 2^24 with t = (float)yc, as s_fm is for an f32 logit.
+__device__ __forceinline__ uint32_t s_pfm(double yc, float t) {
+    return (uint32_t)(__builtin_amdgcn_exp2f((float)(yc - (double)floorf(t))) * 16777216.0f);
+}
+// The smallest float >= y (y finite or infinite; NaN passes through).
+__device__ __forceinline__ float s_f32_up(double y) {
+    const float f = (float)y;
+    if (!((double)f < y)) return f;
+    if (f == 0.0f) return __uint_as_float(1u);  // the least positive float
+    const uint32_t b = __float_as_uint(f);
+    return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);  // (FLT_MAX + 1 ulp: +inf)
+}
+// apply_repetition_penalty's update of one logit (sampler.rs:94-98), in f64.
+__device__ __forceinline__ double s_penalise(float x, double pen) {
+    return (x > 0.0f) ? (double)x / pen : (double)x * pen;
+}
+
 // max of a float4 and of two floats without the canonicalising moves fmaxf
 // adds (NaN inputs are caught through Z later)
 __device__ __forceinline__ float s_max4(const f4v& v) {
@@ -351,18 +403,34 @@ __device__ __forceinline__ void lds_put2_u32_m(uint64_t mask, uint32_t a, uint32
         : "memory");
 }
 
+// PEN: the row may carry a penalty history (its length is checked inside,
+// so no load waits before the stream starts).
+template <bool PEN>
 __device__ __forceinline__ bool sparse_eligible(const RowArgs a, int row) {
     if (a.V < 256 || a.V > kSMaxV) return false;
     if (!(a.temperature > 0.0f) || !(a.top_p > 0.0f) || !(a.top_p < 1.0f)) return false;
     if (a.top_k > 0 && a.top_k < (uint64_t)a.V) return false;
+    if (PEN) return true;
     int64_t g0 = 0, g1 = 0;
-    if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0)
-        return false;
+    if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) return false;
     return true;
 }
 
 // Returns NIS_REJECT_NONE when the row is done, else (uniformly across the
 // workgroup) why it must be recomputed; nothing has been written then.
+//
+// PEN: the row's penalty history is applied on the fly.  Its ids go into two
+// LDS bitmaps (elements, and float4 slots) before the stream; a chunk whose
+// slots hold none costs one scalar test, and in one that does the owner lanes
+// move each penalised logit to their wave's side list and leave -inf in its
+// place, so every register-side step skips it.  At the stream end each wave
+// takes its side list in f64 (sampler.rs:94-98): the masses join Z, the
+// values the max (rounded up), and the ones at or above the listing threshold
+// the histograms, with the bucket of (float)(y c) (monotone in y, and equal
+// to the f32 bucket rule on unpenalised values).  After the cutoff they join
+// the segment sums, the members (ranked on f64 keys) and the final walk,
+// placed by row index.
+template <bool PEN>
 __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, WideShared& sh) {
     const int l = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -399,6 +467,42 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     // all, which it does only as the row's data arrives.
     xv[0] = nis_buffer_load_f4(rsrc, (Kw > 0) ? 16 * max(slot0, f_lo) : 0x7FFFFFF0, 0, 2);
     __builtin_amdgcn_sched_barrier(0);
+    // PEN: the raw history ids (behind chunk 0), and the bitmaps cleared
+    const int tid = (int)threadIdx.x;
+    uint32_t hid[PEN ? kSHist / kSB : 1];
+    bool hlong = false;  // a history past kSHist ids: the row is declined
+    if constexpr (PEN) {
+        if (a.gen_len != nullptr) {
+            // a decode step: the history's slots are known before its length,
+            // so both loads go out at once and the length masks the ids after
+            const int64_t g0 = (int64_t)row * a.gen_cap;
+            const int nc = (int)min(a.gen_cap, (int64_t)kSHist);
+#pragma unroll
+            for (int i = 0; i < kSHist / kSB; ++i) {
+                const int j = tid + kSB * i;
+                hid[i] = (j < nc) ? a.gen_ids[g0 + j] : 0xFFFFFFFFu;
+            }
+            const int nh = (int)min((int64_t)max(a.gen_len[row], 0), a.gen_cap);
+            hlong = nh > kSHist;
+#pragma unroll
+            for (int i = 0; i < kSHist / kSB; ++i)
+                if (tid + kSB * i >= nh) hid[i] = 0xFFFFFFFFu;
+        } else {
+            int64_t g0 = 0, g1 = 0;
+            if (!gen_range(a, row, g0, g1)) g1 = g0;
+            hlong = g1 - g0 > (int64_t)kSHist;
+            const int nh = (int)min(g1 - g0, (int64_t)kSHist);
+#pragma unroll
+            for (int i = 0; i < kSHist / kSB; ++i) {
+                const int j = tid + kSB * i;
+                hid[i] = (j < nh) ? a.gen_ids[g0 + j] : 0xFFFFFFFFu;
+            }
+        }
+        sh.pnib[tid] = 0u;
+        if (tid + kSB < kSNibW) sh.pnib[tid + kSB] = 0u;
+        if (tid < kSPslW) sh.pslot[tid] = 0ull;
+        if (tid == 0) sh.pover = hlong ? 1u : 0u;
+    }
     *reinterpret_cast<u4v*>(&sh.hist[w * (kSHB / kSW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
     if (l < 32 / kSW) sh.oct[w * (32 / kSW) + l] = 0ull;
     if (w == 0 && l == 0) {
@@ -410,6 +514,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         sh.kthmin = 0xFFFFFFFFu;
         sh.krwmin = 0xFFFFFFFFu;
         sh.nmax = 0u;
+        if (PEN) {
+            sh.kymax = 0ull;
+            sh.kmaxp = 0u;
+        }
     }
     lds_barrier();
     const int voff = 16 * slot0;  // (chunks past the first never hold slot 0)
@@ -426,6 +534,32 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     typedef const __attribute__((address_space(1))) uint64_t* gu64p;
     uint64_t rsv = 0;
     if (w == 0) rsv = ((gu64p)(a.rng + 4 * (int64_t)row))[l & 3];
+    // PEN: the bitmaps, then bit k of pany: chunk k of this wave has a slot
+    // holding a penalised element, and bits 4k..4k+3 of pnl: which elements
+    // of this lane's slot in chunk k are penalised
+    uint32_t pany = 0u;
+    uint64_t pnl = 0ull;
+    if constexpr (PEN) {
+#pragma unroll
+        for (int i = 0; i < kSHist / kSB; ++i) {
+            const uint32_t id = hid[i];
+            if (id < (uint32_t)V) {
+                const uint32_t f = id + (uint32_t)mis;  // float position from the slot base
+                atomicOr(&sh.pnib[f >> 5], 1u << (f & 31u));
+                atomicOr(reinterpret_cast<uint32_t*>(&sh.pslot[0]) + (f >> 7), 1u << ((f >> 2) & 31u));
+            }
+        }
+        lds_barrier();
+        const unsigned long long m = (l < Kw) ? sh.pslot[(wbase >> 6) + min(l, kSN - 1)] : 0ull;
+        pany = (uint32_t)__ballot(m != 0ull);
+#pragma unroll
+        for (int k = 0; k < kSN; ++k) {
+            if ((pany >> k) & 1u) {
+                const uint32_t s = (uint32_t)(slot0 + 64 * k);
+                pnl |= (uint64_t)((sh.pnib[s >> 3] >> (4u * (s & 7u))) & 15u) << (4 * k);
+            }
+        }
+    }
 
     // The CU serves the waves' loads in wave order, so later waves get their
     // data later and sit on the critical path: they run at a higher priority
@@ -453,10 +587,30 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const float c = (float)(1.4426950408889634 / temp);     // log2(e) / T
     const float p = a.top_p;
     const f4v ninf4 = f4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    // PEN: the slots of chunk k holding penalised elements go to the wave's
+    // side list whole (with their element mask); -inf stays in their place
+    uint32_t ns = 0u;  // this wave's listed slots so far
+#define NIS_SPEN(k)                                                                             \
+    if constexpr (PEN) {                                                                        \
+        if ((pany >> (k)) & 1u) {                                                              \
+            const uint32_t s_ = (uint32_t)(slot0 + 64 * (k));                                   \
+            const uint32_t nb_ = (uint32_t)(pnl >> (4 * (k))) & 15u;                            \
+            const uint64_t mq_ = __ballot(nb_ != 0u);                                           \
+            const uint32_t p_ = ns + lane_rank(mq_);                                            \
+            if (nb_ != 0u && p_ < (uint32_t)kSSlot) {                                           \
+                sh.sx4[w][p_] = xv[k];                                                          \
+                sh.sslot[w][p_] = (s_ << 4) | nb_;                                              \
+            }                                                                                   \
+            ns += (uint32_t)__popcll(mq_);                                                      \
+            xv[k] = f4v{(nb_ & 1u) ? -INFINITY : xv[k].x, (nb_ & 2u) ? -INFINITY : xv[k].y,     \
+                        (nb_ & 4u) ? -INFINITY : xv[k].z, (nb_ & 8u) ? -INFINITY : xv[k].w};    \
+        }                                                                                       \
+    }
 
     // wave reference from the first chunk
     if (Kw == 0) xv[0] = ninf4;
     else if (edge_wave) NIS_SFIX(0);
+    NIS_SPEN(0)
     const float m0 = wmax_f32(max4(xv[0]));
     const float Rw = (m0 > -INFINITY && fabsf(m0 * c) < 1e30f) ? ceilf(m0 * c) : 0.0f;
     const float RwH = Rw + 8.0f;  // top of the sample histogram (8 octaves of head room)
@@ -493,6 +647,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         if (k > 0) {                                                                         \
             if (k >= Kw) xv[k] = ninf4;                                                      \
             else if (FIX) NIS_SFIX(k);                                                       \
+            NIS_SPEN(k)                                                                      \
         }                                                                                    \
         const f4v x = xv[k];                                                                 \
         const float e0 = __builtin_amdgcn_exp2f(fmaf(x.x, cz, -Rz));                         \
@@ -539,10 +694,66 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
 #undef NIS_SLIST
 #undef NIS_SLOAD
 #undef NIS_SFIX
+#undef NIS_SPEN
 
     // ---- stream end: this wave's candidates into the histograms ----------
     NIS_STS(1);
     __builtin_amdgcn_s_setprio(0);
+    thl = fmaxf(thl, unkey32(sh.kxlo));
+    // ---- PEN: this wave's penalised elements, in f64 ------------------------
+    // One per lane (row order): the f64 value (sampler.rs:94-98) and its mass
+    // into this lane's part of Z; its exact value and its f32 value rounded up
+    // into the row maxima (the latter bounds every element's x c); at or above
+    // thl, into the histograms.  The records stay for the tail.
+    uint32_t nsc = 0u;  // of them at or above the listing threshold (candidates)
+    uint32_t nsw = 0u;  // of them on the side list
+    if constexpr (PEN) {
+        if (ns != 0u) {  // (wave-uniform: most waves meet no penalised element)
+            lds_wave_fence();
+            const uint32_t nsl = min(ns, (uint32_t)kSSlot);
+            const f4v e4 = sh.sx4[w][min(l, kSSlot - 1)];
+            const uint32_t sm = (l < (int)nsl) ? sh.sslot[w][min(l, kSSlot - 1)] : 0u;
+            const uint32_t cnt = (uint32_t)__popc(sm & 15u);
+            const uint32_t incl = wscan_u32(cnt);
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            if ((ns > (uint32_t)kSSlot || tot > (uint32_t)kSSide) && l == 0) sh.pover = 1u;
+            nsw = min(tot, (uint32_t)kSSide);
+            SSide* const srec = reinterpret_cast<SSide*>(&sh.whist[w][0]);
+            uint32_t pos = incl - cnt;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (((sm >> q) & 1u) && pos < (uint32_t)kSSide) {
+                    uint32_t* const r32 = reinterpret_cast<uint32_t*>(&srec[pos]);
+                    r32[0] = __float_as_uint(e4[q]);  // the logit, until the lane below takes it
+                    r32[2] = 4u * (sm >> 4) + (uint32_t)q - (uint32_t)mis;
+                }
+                pos += (sm >> q) & 1u;
+            }
+            lds_wave_fence();
+            const bool sv = l < (int)nsw;
+            const u4v rr = *reinterpret_cast<const u4v*>(&srec[min(l, kSSide - 1)]);
+            const double y = sv ? s_penalise(__uint_as_float(rr.x), (double)a.penalty) : -INFINITY;
+            const double yc = y * (double)c;
+            const float ts = (float)yc;
+            if (sv) {
+                z += s_pmass(yc, Rw);
+                if (y > -INFINITY) {
+                    atomicMax(&sh.kymax, key64(y));
+                    atomicMax(&sh.kmaxp, key32(s_f32_up(y)));
+                }
+            }
+            const bool cand = sv && ts >= thl;
+            const uint64_t cmk = __ballot(cand);
+            if (cmk) {
+                const int b = s_bucket(ts);
+                lds_add2_u64_m(cmk, lds_addr(&sh.hist[0]) + 8 * ((uint32_t)b & (uint32_t)(kSHB - 1)),
+                               lds_addr(&sh.oct[0]) + 8 * ((uint32_t)(b >> kSLog) & 31u),
+                               (1ull << 48) | (uint64_t)s_pfm(yc, ts));
+            }
+            nsc = (uint32_t)__popcll(cmk);
+            if (sv) srec[l] = SSide{y, rr.z, cand ? 1u : 0u};
+        }
+    }
     mx = wmax_f32(mx);
     z = wsum_f64(z);
     NIS_STS(4);
@@ -553,7 +764,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     // holds few of them), the round's element read back from the list by its
     // LDS address.  Each round's bucket (with the element's place) and fm
     // stay in registers for the kept sums after the search.
-    thl = fmaxf(thl, unkey32(sh.kxlo));
     const uint32_t ne = min(nw, (uint32_t)kSE);
     const int sg = (int)((ne + 63u) >> 6);
     const int e0 = l * sg;  // the lane's first entry
@@ -603,7 +813,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const uint32_t ra = lds_addr(&sh.rec[w]);
         lds_put_b128_m(1ull, ra, u4v{(uint32_t)zb, (uint32_t)(zb >> 32), __float_as_uint(mx),
                                      __float_as_uint(Rw)});
-        lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, 0u, 0u});
+        lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, nsw, 0u});
     }
     // the row's one draw (sampler.rs:209), made by wave 0 off the critical
     // path; wave 0 stores the advanced state once the row cannot be declined
@@ -620,7 +830,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     if (l == 0) {
         const float thr = Kw > 0 ? thc : -INFINITY;
         atomicMax(&sh.kmax, key32(mx));
-        if (nw > 0u) atomicMin(&sh.kthmin, key32(thr));
+        if (nw > 0u || nsc > 0u) atomicMin(&sh.kthmin, key32(thr));
         if (mx > -INFINITY) atomicMin(&sh.krwmin, key32(Rw));
         atomicMax(&sh.nmax, nw);
     }
@@ -640,7 +850,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const u4v ra = *reinterpret_cast<const u4v*>(&sh.rec[li]);
         const float rrw = __uint_as_float(ra.w);
         const double rz = __longlong_as_double((long long)(((uint64_t)ra.y << 32) | ra.x));
-        const float M = unkey32(sh.kmax);
+        const float M = PEN ? fmaxf(unkey32(sh.kmax), unkey32(sh.kmaxp)) : unkey32(sh.kmax);
         const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
         const int Ri = (int)R;
         const float xlo = unkey32(sh.kxlo);
@@ -675,7 +885,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         cut.R = R;
         if (!fin || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok) {
             cut.reject = NIS_REJECT_NONFINITE;
-        } else if (!xfin || nmax > (uint32_t)kSE ||
+        } else if (!xfin || nmax > (uint32_t)kSE || (PEN && sh.pover != 0u) ||
                    !(bM - (int)(thmin * (float)kSRes) < kSHB - kSRes) || oM - olo > 30) {
             cut.reject = NIS_REJECT_CAPACITY;
         } else {
@@ -782,6 +992,49 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                 mb |= (b == bp) ? (1u << (cbk[r] & 15u)) : 0u;
             }
         }
+        if (PEN && nsw != 0u) {
+            // the side list: class (1: kept, above b_p; 2: member of b_p), lane
+            // segment (the last one whose first entry's slot is at or before
+            // the element's slot, so the segments stay in row order) and the
+            // kept masses into those segments' sums
+            SSide* const srec = reinterpret_cast<SSide*>(&sh.whist[w][0]);
+            const bool sv = l < (int)nsw;
+            const SSide sd = srec[min(l, kSSide - 1)];
+            const double yc = sd.y * (double)c;
+            const float ts = (float)yc;
+            const int b = s_bucket(ts);
+            const bool cand = sv && (sd.tag & 1u) != 0u;
+            const uint32_t cls = !cand ? 0u : (b > bp ? 1u : (b == bp ? 2u : 0u));
+            const uint32_t fm = s_pfm(yc, ts);
+            const unsigned long long km =
+                cls == 1u ? (unsigned long long)fm << ((uint32_t)((b >> kSLog) - Ri + 16) & 63u) : 0ull;
+            const int jj = l * sg;
+            const int fs = (jj < (int)ne) ? (int)sh.epos[w][min(jj, kSE - 1)] : 0x7FFFFFFF;
+            uint32_t sseg = 0u;
+            uint64_t todo = __ballot(cls != 0u);
+            while (todo) {  // (few: the penalised elements at or above b_p)
+                const int sl = __ffsll((long long)todo) - 1;
+                todo &= todo - 1ull;
+                const int ss = (int)bcast_u32((sd.idx + (uint32_t)mis) >> 2, sl) - wbase;
+                const uint64_t le = __ballot(fs <= ss);  // a prefix of the segments
+                const uint32_t sg_s = le ? (uint32_t)(63 - __clzll((long long)le)) : 0u;
+                if (l == sl) sseg = sg_s;
+                const unsigned long long ks = bcast_u64(km, sl);
+                if (l == (int)sg_s) isum += ks;
+            }
+            if (sv) srec[l].tag = (sd.tag & 1u) | (cls << 8) | (sseg << 16);
+            const uint64_t smk = __ballot(cls == 2u);
+            if (smk) {
+                uint32_t base = 0u;
+                if (l == 0) base = atomicAdd(&sh.nmem, (uint32_t)__popcll(smk));
+                const uint32_t slot = bcast_u32(base, 0) + lane_rank(smk);
+                if (cls == 2u) {
+                    const uint32_t sl = min(slot, (uint32_t)kSMem - 1);
+                    sh.mem[sl] = SMem{(float)sd.y, sd.idx, fm, ((uint32_t)w << 16) | sseg};
+                    sh.memy[sl] = sd.y;
+                }
+            }
+        }
         const double ssum = (double)isum;
         sh.seg[w][l] = ssum;
         const double tsum = wsum_f64(ssum);
@@ -800,6 +1053,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                 const uint32_t idx = (uint32_t)(4 * (wbase + (int)sh.epos[w][e]) - mis + q);
                 sh.mem[min(slot, (uint32_t)kSMem - 1)] =
                     SMem{x, idx, s_fm(x, c, x * c), ((uint32_t)w << 16) | (uint32_t)l};
+                if constexpr (PEN) sh.memy[min(slot, (uint32_t)kSMem - 1)] = (double)x;
                 ++slot;
             }
         }
@@ -825,10 +1079,14 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const u4v mr = *reinterpret_cast<const u4v*>(&sh.mem[min(l, kSMem - 1)]);
     const float xm = __uint_as_float(mr.x);
     const uint32_t im = mr.y;
-    const float tm = xm * c;
+    double ym = 0.0;  // PEN: the member's value in f64
+    if constexpr (PEN) ym = sh.memy[min(l, kSMem - 1)];
+    const float tm = PEN ? (float)(ym * (double)c) : xm * c;
     const double em = valid ? s_m40(mr.z, (int)floorf(tm), Ri) : 0.0;
-    // stable descending order of sampler.rs:140: value, then index
-    const unsigned long long Km = valid ? (((unsigned long long)key32(xm) << 32) | (uint32_t)~im) : 0ull;
+    // stable descending order of sampler.rs:140: value, then index (PEN: the
+    // f64 value's key, the index compared on its own)
+    const unsigned long long Km =
+        !valid ? 0ull : PEN ? key64(ym) : (((unsigned long long)key32(xm) << 32) | (uint32_t)~im);
     NIS_STS1(11);
     double pre = 0.0;
     uint32_t rk = 0u;  // members ahead of this one
@@ -836,8 +1094,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     for (int j = 0; j < n; ++j) {
         const unsigned long long Kj = bcast_u64(Km, j);
         const double ej = bcast_f64(em, j);
-        pre += (Kj > Km) ? ej : 0.0;
-        rk += (Kj > Km) ? 1u : 0u;
+        bool ahead = Kj > Km;
+        if constexpr (PEN) ahead |= (Kj == Km) & (bcast_u32(im, j) < im);
+        pre += ahead ? ej : 0.0;
+        rk += ahead ? 1u : 0u;
     }
     NIS_STS1(12);
     const bool kept = valid & (gp + pre - em <= pz);  // sampler.rs:150
@@ -847,6 +1107,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     // largest, the keys being distinct); elements of b_p at or above it are kept
     const uint64_t lastm = __ballot(valid & (rk + 1u == nkept));
     const unsigned long long Kcut = lastm ? bcast_u64(Km, __ffsll((long long)lastm) - 1) : ~0ull;
+    const uint32_t Icut = lastm ? bcast_u32(im, __ffsll((long long)lastm) - 1) : 0u;  // (PEN)
     // the kept members join their wave's and their segment's kept mass
     {
         const int mw = min((int)(mr.w >> 16), kSW - 1), ms = (int)(mr.w & 63u);
@@ -879,21 +1140,88 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const uint32_t ide = (uint32_t)(4 * (64 * cpw * ws + (int)sh.epos[ws][jec]) - mis + (l & 3));
     const float te = xe * c;
     const int be = s_bucket(te);
-    const unsigned long long Ke = ((unsigned long long)key32(xe) << 32) | (uint32_t)~ide;
-    const bool kje = (l < 4 * sgs) & (je < (int)nes) & ((be > bp) | ((be == bp) & (Ke >= Kcut)));
-    const double ee = kje ? s_m40(s_fm(xe, c, te), (int)floorf(te), Ri) : 0.0;
-    NIS_STS1(6);
-    const double pe_incl = rscan_f64(ee);
-    const uint64_t he = __ballot(kje & (runl + pe_incl >= r));
-    const int le = he ? (__ffsll((long long)he) - 1) : 0;
+    bool kje;
+    double ee;
+    uint32_t idl = ide;  // the lane's row index
+    int le;              // the lane holding the drawn element
+    if constexpr (!PEN) {
+        const unsigned long long Ke = ((unsigned long long)key32(xe) << 32) | (uint32_t)~ide;
+        kje = (l < 4 * sgs) & (je < (int)nes) & ((be > bp) | ((be == bp) & (Ke >= Kcut)));
+        ee = kje ? s_m40(s_fm(xe, c, te), (int)floorf(te), Ri) : 0.0;
+        NIS_STS1(6);
+        const double pe_incl = rscan_f64(ee);
+        const uint64_t he = __ballot(kje & (runl + pe_incl >= r));
+        le = he ? (__ffsll((long long)he) - 1) : 0;
+    } else {
+        // lanes 0..15: the segment's listed elements (row order); lanes 16..63:
+        // the chosen wave's side list, the kept ones of this segment taking part
+        const bool reg = (l < 4 * sgs) & (je < (int)nes);
+        const unsigned long long kd = key64((double)xe);
+        const bool ge = (kd > Kcut) | ((kd == Kcut) & (ide <= Icut));
+        const bool kreg = reg & ((be > bp) | ((be == bp) & ge));
+        const double er = kreg ? s_m40(s_fm(xe, c, te), (int)floorf(te), Ri) : 0.0;
+        bool ks = false;  // lane >= 16: a kept side element of this segment
+        double es = 0.0;  //   and its mass
+        const uint32_t nss = min(sh.rec[ws].ns, (uint32_t)kSSide);
+        if (nss != 0u) {
+            const SSide* const srec = reinterpret_cast<const SSide*>(&sh.whist[ws][0]);
+            const int ts_ = l - 16;
+            const bool sl_ = (ts_ >= 0) & (ts_ < (int)nss);
+            const SSide sd = srec[min(max(ts_, 0), kSSide - 1)];
+            const uint32_t cls = (sd.tag >> 8) & 0xFFu;
+            const unsigned long long kds = key64(sd.y);
+            ks = sl_ & ((sd.tag >> 16) == (uint32_t)ls) &
+                 ((cls == 1u) | ((cls == 2u) & ((kds > Kcut) | ((kds == Kcut) & (sd.idx <= Icut)))));
+            const double ycs = sd.y * (double)c;
+            const float tss = (float)ycs;
+            es = ks ? s_m40(s_pfm(ycs, tss), (int)floorf(tss), Ri) : 0.0;
+            if (l >= 16) idl = sd.idx;
+        }
+        kje = (l < 16) ? kreg : ks;
+        ee = (l < 16) ? er : es;
+        NIS_STS1(6);
+        // inclusive prefix in row order: the listed elements' scan, plus every
+        // kept side element below; a side element's own prefix adds the scan
+        // of the last listed position below it
+        const double pr = rscan_f64(l < 16 ? er : 0.0);
+        double pe = (l < 16) ? pr : es;
+        const uint64_t regm = __ballot(reg);
+        uint64_t svm = __ballot((l >= 16) & ks);
+        while (svm) {  // (few: the kept penalised elements of this segment)
+            const int sl = __ffsll((long long)svm) - 1;
+            svm &= svm - 1ull;
+            const double e1 = bcast_f64(es, sl);
+            const uint32_t i1 = bcast_u32(idl, sl);
+            if (idl > i1) pe += e1;
+            const uint64_t below = regm & __ballot(idl < i1);
+            const double rp = below ? bcast_f64(pr, 63 - __clzll((long long)below)) : 0.0;
+            if (l == sl) pe += rp;
+        }
+        // the crossing: the lowest row index whose inclusive prefix reaches r
+        // (lane order is row order when no side element takes part)
+        const bool hit = kje & (runl + pe >= r);
+        uint64_t he = __ballot(hit);
+        if (he >> 16) {
+            uint32_t imin = hit ? idl : 0xFFFFFFFFu;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) imin = min(imin, (uint32_t)__shfl_xor((int)imin, o));
+            he = __ballot(hit & (idl == imin));
+        }
+        le = he ? (__ffsll((long long)he) - 1) : 0;
+    }
     if (l == le) {
-        const uint32_t tok = (u == 0.0) ? 0u : ide;  // r == 0 stops the reference's walk at index 0
+        const uint32_t tok = (u == 0.0) ? 0u : idl;  // r == 0 stops the reference's walk at index 0
         emit_token(a, row, tok);
         if (a.stats) {
             const double prob = (u == 0.0) ? 0.0 : ee / zk;
             // 2^(R - M c): units of 2^R -> units of the max element's mass
-            const double rho = (double)__builtin_amdgcn_exp2f(-fmaf(M, c, -R));
-            write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zk / kS40 * rho,
+            double Mx = (double)M;
+            double rho = (double)__builtin_amdgcn_exp2f(-fmaf(M, c, -R));
+            if constexpr (PEN) {  // the exact max after the penalty
+                Mx = fmax((double)unkey32(sh.kmax), unkey64(sh.kymax));
+                rho = (double)__builtin_amdgcn_exp2f(-(float)(Mx * (double)c - (double)R));
+            }
+            write_row_stats(a, row, tok, NIS_PATH_DRAW, Mx / temp, zk / kS40 * rho,
                             cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
         }
     }

@@ -22,7 +22,7 @@ def sampler():
     s.close()
 
 
-def _run(sampler, B, V, steps, cap, params_kw, seed):
+def _run(sampler, B, V, steps, cap, params_kw, seed, kernels=None, sigma=2.0):
     import torch
     import nimbus_sampler as ns
     from oracle import oracle
@@ -32,7 +32,7 @@ def _run(sampler, B, V, steps, cap, params_kw, seed):
     max_new = rnd.integers(0, steps + 1, size=B).astype(np.int32)
     max_new[:3] = [0, 1, steps]
     stop = rnd.choice(V, size=3, replace=False).astype(np.uint32)
-    logits = (rnd.standard_normal((steps, B, V), dtype=np.float32) * np.float32(2.0))
+    logits = (rnd.standard_normal((steps, B, V), dtype=np.float32) * np.float32(sigma))
     # plant a stop id on top of some rows at some steps, so sequences stop early
     for s in range(steps):
         rows = rnd.choice(B, size=B // 6, replace=False)
@@ -51,11 +51,19 @@ def _run(sampler, B, V, steps, cap, params_kw, seed):
     stop_d = torch.from_numpy(stop.view(np.int32)).to(dev)
     tokens = torch.full((B,), -1, dtype=torch.int32, device=dev)
     gpu_tokens = []
+    stats = torch.zeros((B, 64), dtype=torch.uint8, device=dev)
     for s in range(steps):
         tokens.fill_(-1)
+        stats.zero_()
         x = torch.from_numpy(np.ascontiguousarray(logits[s])).to(dev)
-        sampler.decode_step(x, params, states, gen_ids, gen_len, maxn, done, stop_d, tokens=tokens)
-        gpu_tokens.append(tokens.cpu().numpy().view(np.uint32).copy())
+        sampler.decode_step(x, params, states, gen_ids, gen_len, maxn, done, stop_d, tokens=tokens,
+                            stats=stats)
+        t = tokens.cpu().numpy().view(np.uint32).copy()
+        gpu_tokens.append(t)
+        if kernels is not None:  # (kernel, reject) of every row that sampled
+            st = ns.stats_view(stats)
+            ran = t != 0xFFFFFFFF
+            kernels.append((st["kernel"][ran].copy(), st["reject"][ran].copy()))
     torch.cuda.synchronize()
     g_len = gen_len.cpu().numpy()
     g_buf = gen_buf.cpu().numpy()
@@ -118,6 +126,23 @@ def test_decode_steps_match_oracle_loop(sampler, V, kw, cap):
     assert n_done > 0 and n_started > 0
     if cap < 7:
         assert n_full > 0, "no history reached its capacity"
+
+
+@pytest.mark.parametrize("pen", [1.3, 0.8])
+def test_penalised_decode_stays_on_the_sparse_kernel(sampler, pen):
+    # V = 50257, top-p 0.9 with a penalty, logits of the headline's spread
+    # (N(0, 3^2): nuclei of a few hundred tokens): every step of every
+    # sequence runs in the sparse kernel with its history applied in registers
+    kernels = []
+    kw = dict(temperature=0.8, top_p=0.9, repetition_penalty=pen)
+    diverged, n_done, n_started, _ = _run(sampler, B=24, V=50257, steps=7, cap=8, params_kw=kw,
+                                          seed=77, kernels=kernels, sigma=3.0)
+    assert diverged <= 1 and n_started > 0
+    k = np.concatenate([a for a, _ in kernels])
+    r = np.concatenate([b for _, b in kernels])
+    print(f"[decode] penalty {pen}: {k.size} row-steps, kernels {np.unique(k).tolist()}, "
+          f"rejects {np.unique(r).tolist()}", flush=True)
+    assert k.size > 0 and (k == 1).all() and (r == 0).all()
 
 
 def test_decode_step_rejects_bad_arguments(sampler):
