@@ -183,7 +183,8 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
         alg_bytes += B * 4 * H  # the histories read as penalty lists (at least H ids each)
     print(json.dumps({
         "metric": f"decode steps: tokens/s, B={B} sequences x V={V} fp32, "
-                  f"T={w.temperature} top-p={w.top_p} repetition-penalty={params.repetition_penalty}",
+                  f"T={params.temperature} top-p={w.top_p} "
+                  f"repetition-penalty={params.repetition_penalty}",
         "value": B / (us * 1e-6), "unit": "tokens/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "us_per_step": us, "higher_is_better": True,
         "data": "synthetic logits of the workload, 8 rotated batches resident in HBM",
@@ -321,6 +322,8 @@ def main():
     ap.add_argument("--penalty", type=float, default=1.0,
                     help="repetition penalty of --decode (sampler.rs:83-101; the histories "
                          "are the penalty lists)")
+    ap.add_argument("--temperature", type=float, default=None,
+                    help="temperature of --decode instead of the workload's (0: greedy)")
     ap.add_argument("--history", type=int, default=0,
                     help="ids already in every history when a --decode replay starts")
     ap.add_argument("--lm-head", choices=("f32", "int8", "int4"), default=None,
@@ -365,7 +368,8 @@ def main():
     B, V = w.B, w.V
     dev = torch.device("cuda:0")
     sampler = ns.Sampler(0)
-    params = ns.SamplingParams(temperature=w.temperature, top_p=w.top_p,
+    temp = args.temperature if (args.decode and args.temperature is not None) else w.temperature
+    params = ns.SamplingParams(temperature=temp, top_p=w.top_p,
                                repetition_penalty=args.penalty if args.decode else 1.0)
 
     host0 = w.make(B)

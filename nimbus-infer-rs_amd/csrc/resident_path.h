@@ -30,6 +30,7 @@
 // the caller runs the general path on it.
 #pragma once
 #include "fast_path.h"
+#include "penalty_bits.h"
 
 namespace nis {
 
@@ -38,7 +39,8 @@ constexpr int kRW = kRB / 64;              // waves per workgroup
 constexpr int kRN = 13;                    // float4 chunks per lane (at most)
 constexpr int kRMaxV = kRB * 4 * kRN - 3;  // 53245
 constexpr int kRD = 3;                     // loads in flight per lane ahead of the one in use
-enum { kResAll = 1, kResGreedy = 2 };
+enum { kResAll = 1, kResGreedy = 2, kResGreedyPen = 3 };
+static_assert(kRB == kPB && kRMaxV == kPMaxV, "penalty bitmaps sized for this layout");
 
 // Optional phase timestamps (profiling builds only, compiled out unless
 // NIS_RES_TIMING is defined): each wave keeps the 100 MHz clock of its phases
@@ -75,11 +77,13 @@ struct alignas(16) RCand {
 };
 // Stream-end record of one wave (lane 0 writes it).
 struct alignas(16) RRec {
-    double z;      // sum of 2^(x c - R_w) over the wave's elements (greedy: unused)
+    double z;      // sum of 2^(x c - R_w) over the wave's elements (greedy with a
+                   // penalty: the wave's largest penalised value, f64)
     float mx;      // wave max logit
     float rw;      // R_w
     float thc;     // greedy: the first index of the wave max
-    uint32_t nc;   // top-p off with stats: the wave's elements above -inf
+    uint32_t nc;   // top-p off with stats: the wave's elements above -inf (greedy
+                   // with a penalty: the first index of that penalised value)
     uint32_t bad;  // the wave saw input this path does not take
     uint32_t pad;
 };
@@ -88,6 +92,8 @@ struct ResShared {
     float s4[kRW][kRN][64];  // top-p off: per-chunk per-lane f32 masses
     RRec rec[kRW];
     double u0;               // the draw
+    PenBits pb;              // greedy with a penalty: the history's bitmaps
+    uint32_t hlong;          //   and whether it was too long
 };
 
 // u64 wave sum: DPP row sums, then the four row totals (uniform).
@@ -183,8 +189,9 @@ __device__ __forceinline__ unsigned long long r_key(float x, uint32_t idx) {
 template <int MODE>
 __device__ __forceinline__ bool resident_eligible(const RowArgs a, int row) {
     if (a.V < 256 || a.V > kRMaxV) return false;
-    if (MODE == kResGreedy) {
+    if (MODE == kResGreedy || MODE == kResGreedyPen) {
         if (!(a.temperature <= 0.0f)) return false;
+        if (MODE == kResGreedyPen) return true;  // any history (its length is checked inside)
     } else {
         if (!(a.temperature > 0.0f) || (a.top_k > 0 && a.top_k < (uint64_t)a.V)) return false;
         if (!(a.top_p >= 1.0f)) return false;
@@ -197,8 +204,17 @@ __device__ __forceinline__ bool resident_eligible(const RowArgs a, int row) {
 // Returns NIS_REJECT_NONE when the row is done, else (uniformly across the
 // workgroup) why the general path must recompute it; nothing has been
 // written then.
+//
+// kResGreedyPen: greedy with a repetition-penalty history.  The history goes
+// into LDS bitmaps before the stream (penalty_bits.h); in a chunk holding
+// penalised elements their owner lanes take them out of the register max
+// (-inf in their place) and keep the largest penalised value in f64
+// (sampler.rs:94-98) with its first index; the two maxima are merged at the
+// end, equal values going to the lower index (sampler.rs:172-181).
 template <int MODE>
 __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row, ResShared& sh) {
+    constexpr bool GREEDY = MODE == kResGreedy || MODE == kResGreedyPen;
+    constexpr bool PEN = MODE == kResGreedyPen;
     const int l = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const int V = (int)a.V;
@@ -225,6 +241,14 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     f4v xv[kRN];
     xv[0] = nis_buffer_load_f4(rsrc, (Kw > 0) ? 16 * max(slot0, f_lo) : 0x7FFFFFF0, 0, 2);
     __builtin_amdgcn_sched_barrier(0);
+    // PEN: the raw history ids (behind chunk 0), and the bitmaps cleared
+    const int tid = (int)threadIdx.x;
+    uint32_t hid[kPHist / kPB];
+    if constexpr (PEN) {
+        const bool hl = pen_load_ids(a, row, tid, hid);
+        pen_clear(sh.pb, tid);
+        if (tid == 0) sh.hlong = hl ? 1u : 0u;
+    }
     const int voff = 16 * slot0;
 #define NIS_RLOAD(k)                                                                          \
     do {                                                                                      \
@@ -237,7 +261,17 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     }
     typedef const __attribute__((address_space(1))) uint64_t* gu64p;
     uint64_t rsv = 0;
-    if (MODE != kResGreedy && w == 0) rsv = ((gu64p)(a.rng + 4 * (int64_t)row))[l & 3];
+    if (!GREEDY && w == 0) rsv = ((gu64p)(a.rng + 4 * (int64_t)row))[l & 3];
+    // PEN: bit k of pany: chunk k of this wave holds a penalised element;
+    // bits 4k..4k+3 of pnl: which elements of this lane's slot in chunk k
+    uint32_t pany = 0u;
+    uint64_t pnl = 0ull;
+    if constexpr (PEN) {
+        lds_barrier();
+        pen_set_bits(sh.pb, hid, V, mis);
+        lds_barrier();
+        pen_masks<kRN>(sh.pb, wbase, Kw, l, pany, pnl);
+    }
     // the CU serves the waves' loads in wave order: later waves run at a
     // higher priority until their stream ends
     __builtin_amdgcn_s_setprio(0);
@@ -280,17 +314,38 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     const float clo = (float)(c64 - (double)chi);
 
     // =====================================================================
-    if constexpr (MODE == kResGreedy) {
+    if constexpr (GREEDY) {
         // ---- greedy: first index of the maximum (sampler.rs:172-181) ----
         float bx = -INFINITY;
         int bi = 0x7FFFFFFF;
         float fs = 0.0f;  // NaN probe: a NaN element makes it NaN (so may +inf beside -inf)
+        double py = -INFINITY;  // PEN: this lane's largest penalised value
+        int pi = 0x7FFFFFFF;    //   and its first index
+        const double pen = (double)a.penalty;
 #pragma unroll
         for (int k = 0; k < kRN; ++k) {
             if (k + kRD < kRN) NIS_RLOAD(k + kRD);
             __builtin_amdgcn_sched_barrier(0);
             if (k >= Kw) continue;
             NIS_RFIX(k);
+            if constexpr (PEN) {
+                if ((pany >> k) & 1u) {
+                    const uint32_t nb = (uint32_t)(pnl >> (4 * k)) & 15u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if ((nb >> q) & 1u) {
+                            const double y = pen_value(xv[k][q], pen);
+                            const int idx = NIS_RIDX(k, q);
+                            if (y != y) fs = NAN;
+                            if (y > py || (y == py && idx < pi)) {
+                                py = y;
+                                pi = idx;
+                            }
+                            xv[k][q] = -INFINITY;
+                        }
+                    }
+                }
+            }
             const f4v x = xv[k];
             fs += (x.x + x.y) + (x.z + x.w);
             const float m4 = r_max4(x);
@@ -304,13 +359,21 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const float wm = wmax_f32(bx);
         const int wi = (int)wmin_u32((uint32_t)((bx == wm) ? bi : 0x7FFFFFFF));
         const uint32_t bad = (uint32_t)(__ballot(fs != fs) != 0ull);
+        double wy = -INFINITY;  // PEN: the wave's largest penalised value
+        uint32_t wpi = 0x7FFFFFFFu;
+        if (PEN && pany != 0u) {
+            wy = py;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) wy = fmax(wy, __shfl_xor(wy, o));
+            wpi = wmin_u32((uint32_t)((py == wy) ? pi : 0x7FFFFFFF));
+        }
         if (l == 0) {
             RRec r;
-            r.z = 0.0;
+            r.z = wy;
             r.mx = wm;
             r.rw = 0.0f;
             r.thc = __int_as_float(wi);
-            r.nc = 0u;
+            r.nc = wpi;
             r.bad = bad;
             r.pad = 0u;
             sh.rec[w] = r;
@@ -319,12 +382,25 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const bool rv = l < kRW;
         const RRec rr = sh.rec[rv ? l : 0];
         const uint32_t anybad = (uint32_t)(__ballot(rv & (rr.bad != 0u)) != 0ull);
+        if (PEN && sh.hlong != 0u) return NIS_REJECT_CAPACITY;
         if (anybad) return NIS_REJECT_NONFINITE;
         const float rm = rv ? rr.mx : -INFINITY;
         const float M = wmax_f32(rm);
         int tok = (int)wmin_u32((uint32_t)((rv && rr.mx == M) ? __float_as_int(rr.thc) : 0x7FFFFFFF));
+        double Mx = (double)M;
+        if constexpr (PEN) {
+            // the penalised maximum against the register one: the larger value,
+            // on equal values the lower index
+            double Y = rv ? rr.z : -INFINITY;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) Y = fmax(Y, __shfl_xor(Y, o));
+            const int ty = (int)wmin_u32((rv && rr.z == Y) ? rr.nc : 0x7FFFFFFFu);
+            if (Y > Mx) tok = ty;
+            else if (Y == Mx) tok = min(tok, ty);
+            Mx = fmax(Mx, Y);
+        }
         if (tok == 0x7FFFFFFF) tok = 0;  // every element -inf: nothing exceeds work[0]
-        if (w == 0 && l == 0) write_row_result(a, row, (uint32_t)tok, NIS_PATH_GREEDY, (double)M, 0.0,
+        if (w == 0 && l == 0) write_row_result(a, row, (uint32_t)tok, NIS_PATH_GREEDY, Mx, 0.0,
                                                0.0, -1.0, 0.0, 0, 1);
         return NIS_REJECT_NONE;
     }

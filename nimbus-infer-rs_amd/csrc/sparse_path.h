@@ -51,6 +51,7 @@
 // caller then runs the general path on the row.
 #pragma once
 #include "fast_path.h"
+#include "penalty_bits.h"
 
 namespace nis {
 
@@ -70,11 +71,9 @@ constexpr int kSPer = kSHB / 64;            // search rounds (64 buckets each, a
 constexpr int kSMem = 64;                   // members of the cutoff bucket
 constexpr uint32_t kSNone = 0x80000000u;    // packed bucket of no candidate (below any b_p)
 // repetition penalty (sample_rows_sparse_pen_kernel)
-constexpr int kSHist = 4 * kSB;             // history entries per row (raw, with repeats)
 constexpr int kSSide = 48;                  // penalised elements per wave
 constexpr int kSSlot = 32;                  // float4 slots holding them, per wave
-constexpr int kSNibW = kSMaxV / 32 + 2;     // words of 4-bit slot masks (8 slots per word)
-constexpr int kSPslW = kSMaxV / 256 + 2;    // slot bitmap words (64-bit)
+static_assert(kSB == kPB && kSMaxV == kPMaxV, "penalty bitmaps sized for this layout");
 constexpr int kSRounds = 4 * kSSeg;         // candidates per lane (at most)
 constexpr double kS40 = 1099511627776.0;    // 2^40
 
@@ -165,8 +164,7 @@ struct WideShared {
     uint32_t krwmin;               // min R_w of a wave with data
     uint32_t nmax;                 // largest list
     // repetition penalty only (sparse_row<true>)
-    unsigned long long pslot[kSPslW];  // bit s: float4 slot s holds a penalised element
-    uint32_t pnib[kSNibW];             // bits 4 (s % 8) + q of word s / 8: element q of slot s
+    PenBits pb;                        // the history's bitmaps
     f4v sx4[kSW][kSSlot];              // slots met in the stream holding penalised elements
     uint32_t sslot[kSW][kSSlot];       //   slot << 4 | mask of the penalised elements
     double memy[kSMem];                // members' values after the penalty (f64)
@@ -231,11 +229,6 @@ __device__ __forceinline__ float s_f32_up(double y) {
     const uint32_t b = __float_as_uint(f);
     return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);  // (FLT_MAX + 1 ulp: +inf)
 }
-// apply_repetition_penalty's update of one logit (sampler.rs:94-98), in f64.
-__device__ __forceinline__ double s_penalise(float x, double pen) {
-    return (x > 0.0f) ? (double)x / pen : (double)x * pen;
-}
-
 // max of a float4 and of two floats without the canonicalising moves fmaxf
 // adds (NaN inputs are caught through Z later)
 __device__ __forceinline__ float s_max4(const f4v& v) {
@@ -469,38 +462,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     __builtin_amdgcn_sched_barrier(0);
     // PEN: the raw history ids (behind chunk 0), and the bitmaps cleared
     const int tid = (int)threadIdx.x;
-    uint32_t hid[PEN ? kSHist / kSB : 1];
-    bool hlong = false;  // a history past kSHist ids: the row is declined
+    uint32_t hid[kPHist / kPB];
     if constexpr (PEN) {
-        if (a.gen_len != nullptr) {
-            // a decode step: the history's slots are known before its length,
-            // so both loads go out at once and the length masks the ids after
-            const int64_t g0 = (int64_t)row * a.gen_cap;
-            const int nc = (int)min(a.gen_cap, (int64_t)kSHist);
-#pragma unroll
-            for (int i = 0; i < kSHist / kSB; ++i) {
-                const int j = tid + kSB * i;
-                hid[i] = (j < nc) ? a.gen_ids[g0 + j] : 0xFFFFFFFFu;
-            }
-            const int nh = (int)min((int64_t)max(a.gen_len[row], 0), a.gen_cap);
-            hlong = nh > kSHist;
-#pragma unroll
-            for (int i = 0; i < kSHist / kSB; ++i)
-                if (tid + kSB * i >= nh) hid[i] = 0xFFFFFFFFu;
-        } else {
-            int64_t g0 = 0, g1 = 0;
-            if (!gen_range(a, row, g0, g1)) g1 = g0;
-            hlong = g1 - g0 > (int64_t)kSHist;
-            const int nh = (int)min(g1 - g0, (int64_t)kSHist);
-#pragma unroll
-            for (int i = 0; i < kSHist / kSB; ++i) {
-                const int j = tid + kSB * i;
-                hid[i] = (j < nh) ? a.gen_ids[g0 + j] : 0xFFFFFFFFu;
-            }
-        }
-        sh.pnib[tid] = 0u;
-        if (tid + kSB < kSNibW) sh.pnib[tid + kSB] = 0u;
-        if (tid < kSPslW) sh.pslot[tid] = 0ull;
+        const bool hlong = pen_load_ids(a, row, tid, hid);  // too long: the row is declined
+        pen_clear(sh.pb, tid);
         if (tid == 0) sh.pover = hlong ? 1u : 0u;
     }
     *reinterpret_cast<u4v*>(&sh.hist[w * (kSHB / kSW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
@@ -540,25 +505,9 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     uint32_t pany = 0u;
     uint64_t pnl = 0ull;
     if constexpr (PEN) {
-#pragma unroll
-        for (int i = 0; i < kSHist / kSB; ++i) {
-            const uint32_t id = hid[i];
-            if (id < (uint32_t)V) {
-                const uint32_t f = id + (uint32_t)mis;  // float position from the slot base
-                atomicOr(&sh.pnib[f >> 5], 1u << (f & 31u));
-                atomicOr(reinterpret_cast<uint32_t*>(&sh.pslot[0]) + (f >> 7), 1u << ((f >> 2) & 31u));
-            }
-        }
+        pen_set_bits(sh.pb, hid, V, mis);
         lds_barrier();
-        const unsigned long long m = (l < Kw) ? sh.pslot[(wbase >> 6) + min(l, kSN - 1)] : 0ull;
-        pany = (uint32_t)__ballot(m != 0ull);
-#pragma unroll
-        for (int k = 0; k < kSN; ++k) {
-            if ((pany >> k) & 1u) {
-                const uint32_t s = (uint32_t)(slot0 + 64 * k);
-                pnl |= (uint64_t)((sh.pnib[s >> 3] >> (4u * (s & 7u))) & 15u) << (4 * k);
-            }
-        }
+        pen_masks<kSN>(sh.pb, wbase, Kw, l, pany, pnl);
     }
 
     // The CU serves the waves' loads in wave order, so later waves get their
@@ -732,7 +681,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             lds_wave_fence();
             const bool sv = l < (int)nsw;
             const u4v rr = *reinterpret_cast<const u4v*>(&srec[min(l, kSSide - 1)]);
-            const double y = sv ? s_penalise(__uint_as_float(rr.x), (double)a.penalty) : -INFINITY;
+            const double y = sv ? pen_value(__uint_as_float(rr.x), (double)a.penalty) : -INFINITY;
             const double yc = y * (double)c;
             const float ts = (float)yc;
             if (sv) {

@@ -151,3 +151,75 @@ def test_crowded_histories_fall_back_to_the_general_path(sampler):
     st = gpu[1]
     assert (st["kernel"][0::2] == 1).all() and (st["reject"][0::2] == 0).all()
     assert (st["kernel"][1::2] == 2).all()
+
+
+# ---------------------------------------------------------------------------
+# greedy rows: the resident kernel's penalised mode (kResGreedyPen)
+
+@pytest.mark.parametrize("pen", [1.3, 0.8, 2.0])
+def test_greedy_random_histories(sampler, pen):
+    from nimbus_sampler import workloads
+    B, V = 64, 50257
+    rnd = np.random.Generator(np.random.PCG64(int(pen * 1000)))
+    x = workloads.headline(B)
+    gen = [rnd.integers(0, V + 8, size=int(rnd.integers(0, 400))) for _ in range(B)]
+    _check(sampler, x, V, _params(temperature=0.0, repetition_penalty=pen), gen,
+           f"greedy random pen={pen}")
+
+
+@pytest.mark.parametrize("pen", [1.0001, 1.3, 0.7])
+def test_greedy_histories_on_the_top(sampler, pen):
+    # the history holds each row's top tokens: the answer moves to the best
+    # unpenalised token or stays on a penalised one, depending on the penalty
+    from nimbus_sampler import workloads
+    B, V = 64, 50257
+    rnd = np.random.Generator(np.random.PCG64(3 + int(pen * 10)))
+    x = workloads.headline(B)
+    x[: B // 2] -= 30.0  # rows of negative logits: the penalty multiplies them
+    order = np.argsort(-x, axis=1, kind="stable")
+    gen = [order[r, : int(rnd.integers(1, 40))] for r in range(B)]
+    gpu, _ = _check(sampler, x, V, _params(temperature=0.0, repetition_penalty=pen), gen,
+                    f"greedy top pen={pen}")
+    on_pen = sum(int(gpu[0][r]) in set(gen[r].tolist()) for r in range(B))
+    print(f"[penalty] greedy rows answered by a penalised token: {on_pen}/{B}", flush=True)
+
+
+def test_greedy_ties_between_penalised_and_plain_values(sampler):
+    # logits on a 1/8 lattice, row max m > 0.  Odd rows: six more elements
+    # set to 2m and penalised (2m / 2 == m exactly), tying with the plain
+    # maxima.  Rows r % 4 == 0: the same six set to m and penalised (m / 2),
+    # plus index 0 set to 2m and penalised: a penalised tie at index 0.
+    # Other rows: no history.  The lowest index of the f64 maximum must win.
+    B, V = 32, 50257
+    rnd = np.random.Generator(np.random.PCG64(19))
+    x = np.round(rnd.standard_normal((B, V)) * 16.0).astype(np.float32) / np.float32(8.0)
+    gen = []
+    for r in range(B):
+        m = float(x[r].max())
+        cand = rnd.choice(np.arange(1, V), size=6, replace=False)
+        if r % 2:
+            x[r, cand] = np.float32(2.0 * m)
+            gen.append(cand)
+        elif r % 4 == 0:
+            x[r, cand] = np.float32(m)
+            x[r, 0] = np.float32(2.0 * m)
+            gen.append(np.concatenate([cand, [0]]))
+        else:
+            gen.append(np.array([], np.int64))
+    gpu, _ = _check(sampler, x, V, _params(temperature=0.0, repetition_penalty=2.0), gen,
+                    "greedy ties")
+    assert all(int(gpu[0][r]) == 0 for r in range(0, B, 4))
+
+
+def test_greedy_non_finite_and_long_histories_fall_back(sampler):
+    # NaN among the penalised logits, and histories past 4096 ids: declined,
+    # recomputed by the general path (kernel == 2), same answers
+    from nimbus_sampler import workloads
+    B, V = 4, 50257
+    x = workloads.headline(B)
+    x[1, 77] = np.float32(np.nan)
+    gen = [np.arange(10), np.array([77, 5]), np.arange(5000) % V, np.array([], np.int64)]
+    gpu, _ = _check(sampler, x, V, _params(temperature=0.0, repetition_penalty=1.5), gen,
+                    "greedy fallbacks", on_kernel=False)
+    st = gpu[1]
+    assert list(st["kernel"]) == [1, 2, 2, 1], st["kernel"]
