@@ -45,10 +45,11 @@ def routed_kernel(V, temperature, top_k, top_p, penalty, history=False):
         return "sample_rows_long_kernel<greedy>"
     if V > RESIDENT_MAX_V and (top_k == 0 or top_k >= V) and (penalty == 1.0 or not history):
         return "sample_rows_long_kernel<all>" if top_p >= 1.0 else "sample_rows_long_kernel<top-p>"
+    pen = penalty != 1.0 and history
     if res_shape and temperature <= 0.0:
-        return "sample_rows_resident_kernel<greedy>"
+        return "sample_rows_resident_kernel<greedy-pen>" if pen else "sample_rows_resident_kernel<greedy>"
     if res_shape and temperature > 0.0 and no_topk and top_p >= 1.0:
-        return "sample_rows_resident_kernel<all>"
+        return "sample_rows_resident_kernel<all-pen>" if pen else "sample_rows_resident_kernel<all>"
     if res_shape and temperature > 0.0 and no_topk and 0.95 <= top_p < 1.0 \
             and (penalty == 1.0 or not history):
         return "sample_rows_dense_kernel"
@@ -183,7 +184,7 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
         alg_bytes += B * 4 * H  # the histories read as penalty lists (at least H ids each)
     print(json.dumps({
         "metric": f"decode steps: tokens/s, B={B} sequences x V={V} fp32, "
-                  f"T={params.temperature} top-p={w.top_p} "
+                  f"T={params.temperature} top-p={params.top_p} "
                   f"repetition-penalty={params.repetition_penalty}",
         "value": B / (us * 1e-6), "unit": "tokens/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "us_per_step": us, "higher_is_better": True,
@@ -324,6 +325,8 @@ def main():
                          "are the penalty lists)")
     ap.add_argument("--temperature", type=float, default=None,
                     help="temperature of --decode instead of the workload's (0: greedy)")
+    ap.add_argument("--top-p", type=float, default=None,
+                    help="top-p of --decode instead of the workload's (1: off)")
     ap.add_argument("--history", type=int, default=0,
                     help="ids already in every history when a --decode replay starts")
     ap.add_argument("--lm-head", choices=("f32", "int8", "int4"), default=None,
@@ -369,7 +372,8 @@ def main():
     dev = torch.device("cuda:0")
     sampler = ns.Sampler(0)
     temp = args.temperature if (args.decode and args.temperature is not None) else w.temperature
-    params = ns.SamplingParams(temperature=temp, top_p=w.top_p,
+    top_p = args.top_p if (args.decode and args.top_p is not None) else w.top_p
+    params = ns.SamplingParams(temperature=temp, top_p=top_p,
                                repetition_penalty=args.penalty if args.decode else 1.0)
 
     host0 = w.make(B)

@@ -173,8 +173,12 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
             hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResGreedy>, dim3((unsigned)B),
                                dim3(nis::kRB), 0, ctx->stream, a);
     } else if (res_shape && a.temperature > 0.0f && no_topk && a.top_p >= 1.0f) {
-        hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResAll>, dim3((unsigned)B),
-                           dim3(nis::kRB), 0, ctx->stream, a);
+        if (a.penalty != 1.0f && a.gen_ids != nullptr)  // the penalty applied in registers
+            hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResAllPen>, dim3((unsigned)B),
+                               dim3(nis::kRB), 0, ctx->stream, a);
+        else
+            hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResAll>, dim3((unsigned)B),
+                               dim3(nis::kRB), 0, ctx->stream, a);
     } else if (res_shape && a.temperature > 0.0f && no_topk && a.top_p >= 0.95f && a.top_p < 1.0f &&
                (a.penalty == 1.0f || a.gen_ids == nullptr)) {
         hipLaunchKernelGGL(nis::sample_rows_dense_kernel, dim3((unsigned)B), dim3(nis::kDB), 0,

@@ -103,4 +103,24 @@ __device__ __forceinline__ double pen_value(float x, double pen) {
     return (x > 0.0f) ? (double)x / pen : (double)x * pen;
 }
 
+// 2^(yc - R) in f64 for a penalised value (yc = y c in f64): the f32 exp2 of
+// the fractional part, scaled exactly.
+__device__ __forceinline__ double pen_mass(double yc, float R) {
+    const double d = yc - (double)R;
+    if (!(d == d)) return d;  // NaN stays NaN (the row is declined through Z)
+    if (d < -1100.0) return 0.0;
+    if (d > 1100.0) return INFINITY;
+    const double fl = floor(d);
+    return ldexp((double)__builtin_amdgcn_exp2f((float)(d - fl)), (int)fl);
+}
+
+// The smallest float >= y (y finite or infinite; NaN passes through).
+__device__ __forceinline__ float pen_f32_up(double y) {
+    const float f = (float)y;
+    if (!((double)f < y)) return f;
+    if (f == 0.0f) return __uint_as_float(1u);  // the least positive float
+    const uint32_t b = __float_as_uint(f);
+    return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);  // (FLT_MAX + 1 ulp: +inf)
+}
+
 }  // namespace nis

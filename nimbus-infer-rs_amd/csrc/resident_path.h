@@ -39,7 +39,7 @@ constexpr int kRW = kRB / 64;              // waves per workgroup
 constexpr int kRN = 13;                    // float4 chunks per lane (at most)
 constexpr int kRMaxV = kRB * 4 * kRN - 3;  // 53245
 constexpr int kRD = 3;                     // loads in flight per lane ahead of the one in use
-enum { kResAll = 1, kResGreedy = 2, kResGreedyPen = 3 };
+enum { kResAll = 1, kResGreedy = 2, kResGreedyPen = 3, kResAllPen = 4 };
 static_assert(kRB == kPB && kRMaxV == kPMaxV, "penalty bitmaps sized for this layout");
 
 // Optional phase timestamps (profiling builds only, compiled out unless
@@ -92,8 +92,9 @@ struct ResShared {
     float s4[kRW][kRN][64];  // top-p off: per-chunk per-lane f32 masses
     RRec rec[kRW];
     double u0;               // the draw
-    PenBits pb;              // greedy with a penalty: the history's bitmaps
-    uint32_t hlong;          //   and whether it was too long
+    PenBits pb;              // with a penalty: the history's bitmaps
+    float pmx[kRW];          // top-p off with a penalty: each wave's penalised max, rounded up
+    double pymx[kRW];        //   and exact (f64)
 };
 
 // u64 wave sum: DPP row sums, then the four row totals (uniform).
@@ -195,6 +196,7 @@ __device__ __forceinline__ bool resident_eligible(const RowArgs a, int row) {
     } else {
         if (!(a.temperature > 0.0f) || (a.top_k > 0 && a.top_k < (uint64_t)a.V)) return false;
         if (!(a.top_p >= 1.0f)) return false;
+        if (MODE == kResAllPen) return true;
     }
     int64_t g0 = 0, g1 = 0;
     if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) return false;
@@ -214,7 +216,8 @@ __device__ __forceinline__ bool resident_eligible(const RowArgs a, int row) {
 template <int MODE>
 __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row, ResShared& sh) {
     constexpr bool GREEDY = MODE == kResGreedy || MODE == kResGreedyPen;
-    constexpr bool PEN = MODE == kResGreedyPen;
+    constexpr bool ALL = MODE == kResAll || MODE == kResAllPen;
+    constexpr bool PEN = MODE == kResGreedyPen || MODE == kResAllPen;
     const int l = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const int V = (int)a.V;
@@ -244,10 +247,10 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     // PEN: the raw history ids (behind chunk 0), and the bitmaps cleared
     const int tid = (int)threadIdx.x;
     uint32_t hid[kPHist / kPB];
+    bool hlong = false;  // (the same in every lane) a history too long: the row is declined
     if constexpr (PEN) {
-        const bool hl = pen_load_ids(a, row, tid, hid);
+        hlong = pen_load_ids(a, row, tid, hid);
         pen_clear(sh.pb, tid);
-        if (tid == 0) sh.hlong = hl ? 1u : 0u;
     }
     const int voff = 16 * slot0;
 #define NIS_RLOAD(k)                                                                          \
@@ -297,9 +300,9 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     // an element more than one octave above it, it moves up to that max and
     // the wave's mass sum is rescaled by the exact power of two.  Masses near
     // the max (the ones that matter) then always have a small argument.
-#define NIS_RESCALE(m4)                                                        \
+#define NIS_RESCALE(m4, MXR)                                                   \
     if (__ballot((m4) * chi > Rz + 1.0f)) {                                    \
-        const float Rn_ = ceilf(wmax_f32(mx) * chi);                           \
+        const float Rn_ = ceilf(wmax_f32(MXR) * chi);                          \
         if (fabsf(Rn_) < 1e30f) {                                              \
             z = ldexp(z, (int)(Rz - Rn_));                                     \
             Rz = Rn_;                                                          \
@@ -382,7 +385,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const bool rv = l < kRW;
         const RRec rr = sh.rec[rv ? l : 0];
         const uint32_t anybad = (uint32_t)(__ballot(rv & (rr.bad != 0u)) != 0ull);
-        if (PEN && sh.hlong != 0u) return NIS_REJECT_CAPACITY;
+        if (hlong) return NIS_REJECT_CAPACITY;
         if (anybad) return NIS_REJECT_NONFINITE;
         const float rm = rv ? rr.mx : -INFINITY;
         const float M = wmax_f32(rm);
@@ -414,12 +417,28 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     const float Rw = (m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f;
 
     // =====================================================================
-    if constexpr (MODE == kResAll) {
+    if constexpr (ALL) {
         // ---- top-p off: every element kept ------------------------------
+        // (with a penalty, a penalised element keeps its logit in registers
+        // and its f64 value's mass in the chunk sums; the max splits into
+        // the unpenalised one, the penalised one rounded up, which with it
+        // bounds every mass's argument, and the exact penalised one.  Top-p
+        // off ranks nothing, so the value may be x * (1/pen): within an ulp
+        // of the reference's quotient, far below the masses' own rounding.
+        // Its mass is the f32 form of the unpenalised ones, y split as
+        // yh + yl, so the walk recomputes it bit for bit.)
         double z = 0.0;
         float mx = -INFINITY;
+        float mxp = -INFINITY;    // PEN: largest penalised value, rounded up
+        double ymx = -INFINITY;   // PEN: the same, exact
+        const double pen = (double)a.penalty, rpen = 1.0 / pen;
+        auto pval = [&](float x) -> double { return (x > 0.0f) ? (double)x * rpen : (double)x * pen; };
         float czh = chi, czl = clo, Rz = Rw;
         asm volatile("" : "+v"(czh), "+v"(czl));
+        auto pmass = [&](double y, float R) -> float {
+            const float yh = (float)y, yl = (float)(y - (double)yh);
+            return __builtin_amdgcn_exp2f(fmaf(yl, czh, fmaf(yh, czl, fmaf(yh, czh, -R))));
+        };
         float s4v[kRN];  // this lane's float4 mass of chunk k, against reference Rk[k]
         float Rk[kRN];
 #pragma unroll
@@ -431,12 +450,39 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             if (k >= Kw) continue;
             if (k > 0) NIS_RFIX(k);
             const f4v x = xv[k];
-            const float m4 = r_max4(x);
+            f4v xm = x;                // the unpenalised values (-inf for penalised ones)
+            uint32_t nb = 0u;          // PEN: penalised elements of this float4
+            double yv[4] = {0.0, 0.0, 0.0, 0.0};
+            float m4p = -INFINITY;     // PEN: their max, rounded up
+            if constexpr (PEN) {
+                if ((pany >> k) & 1u) {
+                    nb = (uint32_t)(pnl >> (4 * k)) & 15u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if ((nb >> q) & 1u) {
+                            yv[q] = pval(x[q]);
+                            xm[q] = -INFINITY;
+                            m4p = fmaxf(m4p, pen_f32_up(yv[q]));
+                            ymx = fmax(ymx, yv[q]);
+                        }
+                    }
+                    mxp = fmaxf(mxp, m4p);
+                }
+            }
+            const float m4 = r_max4(xm);
             mx = fmaxf(mx, m4);
-            NIS_RESCALE(m4)
+            NIS_RESCALE(fmaxf(m4, m4p), fmaxf(mx, mxp))
             Rk[k] = Rz;
-            const float e0 = r_mass(x.x, czh, czl, Rz), e1 = r_mass(x.y, czh, czl, Rz);
-            const float e2 = r_mass(x.z, czh, czl, Rz), e3 = r_mass(x.w, czh, czl, Rz);
+            float e0 = r_mass(x.x, czh, czl, Rz), e1 = r_mass(x.y, czh, czl, Rz);
+            float e2 = r_mass(x.z, czh, czl, Rz), e3 = r_mass(x.w, czh, czl, Rz);
+            if constexpr (PEN) {
+                if ((pany >> k) & 1u) {
+                    if (nb & 1u) e0 = pmass(yv[0], Rz);
+                    if (nb & 2u) e1 = pmass(yv[1], Rz);
+                    if (nb & 4u) e2 = pmass(yv[2], Rz);
+                    if (nb & 8u) e3 = pmass(yv[3], Rz);
+                }
+            }
             const float s4 = (e0 + e1) + (e2 + e3);
             s4v[k] = s4;
             z += (double)s4;
@@ -444,6 +490,15 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         __builtin_amdgcn_s_setprio(0);
         mx = wmax_f32(mx);
         z = wsum_f64(z);
+        if constexpr (PEN) {
+            mxp = wmax_f32(mxp);
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ymx = fmax(ymx, __shfl_xor(ymx, o));
+            if (l == 0) {
+                sh.pmx[w] = mxp;
+                sh.pymx[w] = ymx;
+            }
+        }
         // with stats: the elements above -inf (every one of them is kept)
         uint32_t nfin = 0u;
         if (a.stats) {
@@ -476,11 +531,25 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             rst = (l == 0) ? st[0] : (l == 1) ? st[1] : (l == 2) ? st[2] : st[3];
         }
         lds_barrier();
+        if (hlong) return NIS_REJECT_CAPACITY;
         const bool rv = l < kRW;
         const RRec rr = sh.rec[rv ? l : 0];
-        const float M = wmax_f32(rv ? rr.mx : -INFINITY);
+        // M bounds every element's x c (with a penalty, the penalised values
+        // rounded up); Mx is the exact row max, for the statistics
+        float M = wmax_f32(rv ? rr.mx : -INFINITY);
+        double Mx = (double)M;
+        bool wdata = rv && rr.mx > -INFINITY;  // the wave holds an element above -inf
+        if constexpr (PEN) {
+            const float pm = rv ? sh.pmx[l] : -INFINITY;
+            double py = rv ? sh.pymx[l] : -INFINITY;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) py = fmax(py, __shfl_xor(py, o));
+            Mx = fmax(Mx, py);
+            M = fmaxf(M, wmax_f32(pm));
+            wdata |= rv && pm > -INFINITY;
+        }
         const float R = (M > -INFINITY && fabsf(M * chi) < 1e30f) ? ceilf(M * chi) : 0.0f;
-        const float rwmin = -wmax_f32(rv && rr.mx > -INFINITY ? -rr.rw : -INFINITY);
+        const float rwmin = -wmax_f32(wdata ? -rr.rw : -INFINITY);
         // each wave's total in 2^R units (exact power-of-two rescales)
         const double T = rv ? ldexp(rr.z, (int)(rr.rw - R)) : 0.0;
         const double Tincl = rscan16_f64(T);
@@ -552,8 +621,20 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const int lc = hl ? (__ffsll((long long)hl) - 1) : (63 - __clzll((long long)(nzl | 1ull)));
         if (l == lc) {
             double run = rk_ - (lincl - sl);
-            const float ev[4] = {ldexpf(r_mass(xc.x, czh, czl, Rc), dc), ldexpf(r_mass(xc.y, czh, czl, Rc), dc),
-                                 ldexpf(r_mass(xc.z, czh, czl, Rc), dc), ldexpf(r_mass(xc.w, czh, czl, Rc), dc)};
+            float ev[4] = {ldexpf(r_mass(xc.x, czh, czl, Rc), dc), ldexpf(r_mass(xc.y, czh, czl, Rc), dc),
+                           ldexpf(r_mass(xc.z, czh, czl, Rc), dc), ldexpf(r_mass(xc.w, czh, czl, Rc), dc)};
+            double vq[4] = {(double)xc.x, (double)xc.y, (double)xc.z, (double)xc.w};  // values after the penalty
+            if constexpr (PEN) {
+                // the penalised elements' masses exactly as the stream summed them
+                const uint32_t nbc = (uint32_t)(pnl >> (4 * kc)) & 15u;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if ((nbc >> q) & 1u) {
+                        vq[q] = pval(xc[q]);
+                        ev[q] = ldexpf(pmass(vq[q], Rc), dc);
+                    }
+                }
+            }
             // the first element whose running mass reaches r (the last with
             // mass if rounding leaves r above them all)
             int q = -1, qlast = 0;
@@ -568,15 +649,15 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
                 }
             }
             if (q < 0) q = qlast;
-            const float xq = elem(xc, q);
+            const double xq = vq[q];
             uint32_t tok = (uint32_t)NIS_RIDX(kc, q);
             if (u == 0.0) tok = 0u;  // r == 0 stops the reference's walk at index 0
             emit_token(a, row, tok);
             if (a.stats) {
                 // the drawn token's mass against the row max, exactly reduced
-                const double em = exp2((double)xq * c64 - (double)M * c64);
-                const double zM = ldexp(Z, (int)R) * exp2(-(double)M * c64);
-                write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zM, 0.0, u,
+                const double em = exp2(xq * c64 - Mx * c64);
+                const double zM = ldexp(Z, (int)R) * exp2(-Mx * c64);
+                write_row_stats(a, row, tok, NIS_PATH_DRAW, Mx / temp, zM, 0.0, u,
                                 (u == 0.0) ? 0.0 : em / zM, (uint64_t)nkept, 1);
             }
         }

@@ -206,28 +206,10 @@ __device__ __forceinline__ double s_mup(int b, int R) {
                      1.0001,
                  ((b + 1) >> kSLog) - R + 40);
 }
-// 2^(yc - R) in f64 for a penalised element (yc = y c in f64): the f32 exp2
-// of the fractional part, scaled exactly.
-__device__ __forceinline__ double s_pmass(double yc, float R) {
-    const double d = yc - (double)R;
-    if (!(d == d)) return d;  // NaN stays NaN (the row is declined through Z)
-    if (d < -1100.0) return 0.0;
-    if (d > 1100.0) return INFINITY;
-    const double fl = floor(d);
-    return ldexp((double)__builtin_amdgcn_exp2f((float)(d - fl)), (int)fl);
-}
 // Octave-relative fixed-point mass of a penalised element: 2^(yc - floor(t))
 // * 2^24 with t = (float)yc, as s_fm is for an f32 logit.
 __device__ __forceinline__ uint32_t s_pfm(double yc, float t) {
     return (uint32_t)(__builtin_amdgcn_exp2f((float)(yc - (double)floorf(t))) * 16777216.0f);
-}
-// The smallest float >= y (y finite or infinite; NaN passes through).
-__device__ __forceinline__ float s_f32_up(double y) {
-    const float f = (float)y;
-    if (!((double)f < y)) return f;
-    if (f == 0.0f) return __uint_as_float(1u);  // the least positive float
-    const uint32_t b = __float_as_uint(f);
-    return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);  // (FLT_MAX + 1 ulp: +inf)
 }
 // max of a float4 and of two floats without the canonicalising moves fmaxf
 // adds (NaN inputs are caught through Z later)
@@ -685,10 +667,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const double yc = y * (double)c;
             const float ts = (float)yc;
             if (sv) {
-                z += s_pmass(yc, Rw);
+                z += pen_mass(yc, Rw);
                 if (y > -INFINITY) {
                     atomicMax(&sh.kymax, key64(y));
-                    atomicMax(&sh.kmaxp, key32(s_f32_up(y)));
+                    atomicMax(&sh.kmaxp, key32(pen_f32_up(y)));
                 }
             }
             const bool cand = sv && ts >= thl;

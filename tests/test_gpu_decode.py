@@ -128,20 +128,21 @@ def test_decode_steps_match_oracle_loop(sampler, V, kw, cap):
         assert n_full > 0, "no history reached its capacity"
 
 
-@pytest.mark.parametrize("pen,T", [(1.3, 0.8), (0.8, 0.8), (1.2, 0.0)])
-def test_penalised_decode_stays_on_the_register_kernels(sampler, pen, T):
+@pytest.mark.parametrize("pen,T,p", [(1.3, 0.8, 0.9), (0.8, 0.8, 0.9), (1.2, 0.0, 0.9),
+                                     (1.2, 0.8, 1.0)])
+def test_penalised_decode_stays_on_the_register_kernels(sampler, pen, T, p):
     # V = 50257, top-p 0.9 (or greedy) with a penalty, logits of the
     # headline's spread (N(0, 3^2): nuclei of a few hundred tokens): every
     # step of every sequence runs in the sparse (resident) kernel with its
     # history applied in registers
     kernels = []
-    kw = dict(temperature=T, top_p=0.9, repetition_penalty=pen)
+    kw = dict(temperature=T, top_p=p, repetition_penalty=pen)
     diverged, n_done, n_started, _ = _run(sampler, B=24, V=50257, steps=7, cap=8, params_kw=kw,
                                           seed=77, kernels=kernels, sigma=3.0)
     assert diverged <= 1 and n_started > 0
     k = np.concatenate([a for a, _ in kernels])
     r = np.concatenate([b for _, b in kernels])
-    print(f"[decode] penalty {pen} T={T}: {k.size} row-steps, kernels {np.unique(k).tolist()}, "
+    print(f"[decode] penalty {pen} T={T} p={p}: {k.size} row-steps, kernels {np.unique(k).tolist()}, "
           f"rejects {np.unique(r).tolist()}", flush=True)
     assert k.size > 0 and (k == 1).all() and (r == 0).all()
 

@@ -211,15 +211,56 @@ def test_greedy_ties_between_penalised_and_plain_values(sampler):
     assert all(int(gpu[0][r]) == 0 for r in range(0, B, 4))
 
 
-def test_greedy_non_finite_and_long_histories_fall_back(sampler):
+@pytest.mark.parametrize("T,p", [(0.0, 1.0), (0.8, 1.0), (0.8, 0.9)])
+def test_non_finite_and_long_histories_fall_back(sampler, T, p):
     # NaN among the penalised logits, and histories past 4096 ids: declined,
-    # recomputed by the general path (kernel == 2), same answers
+    # recomputed by the general path (kernel == 2), same answers; greedy,
+    # top-p off and sparse top-p
     from nimbus_sampler import workloads
     B, V = 4, 50257
     x = workloads.headline(B)
     x[1, 77] = np.float32(np.nan)
     gen = [np.arange(10), np.array([77, 5]), np.arange(5000) % V, np.array([], np.int64)]
-    gpu, _ = _check(sampler, x, V, _params(temperature=0.0, repetition_penalty=1.5), gen,
-                    "greedy fallbacks", on_kernel=False)
+    ids, off = _csr(gen)
+    params = _params(temperature=T, top_p=p, repetition_penalty=1.5)
+    gpu = run_gpu(sampler, x, V, params, list(range(B)), ids, off)
+    ref = run_oracle(x, V, params, list(range(B)), ids, off)
+    # the NaN row: token and RNG state only, as for every non-finite row (its
+    # statistics follow no reference value)
+    assert gpu[0][1] == ref[0][1] and np.array_equal(gpu[2][1], ref[2][1])
+    keep = [0, 2, 3]
+    compare((gpu[0][keep], gpu[1][keep], gpu[2][keep]), (ref[0][keep], ref[1][keep], ref[2][keep]),
+            greedy=params.greedy())
     st = gpu[1]
     assert list(st["kernel"]) == [1, 2, 2, 1], st["kernel"]
+
+
+# ---------------------------------------------------------------------------
+# top-p off: the resident kernel's penalised mode (kResAllPen)
+
+@pytest.mark.parametrize("pen,T", [(1.3, 0.8), (0.8, 1.0), (2.0, 0.5), (1.01, 1.3)])
+def test_top_p_off_random_histories(sampler, pen, T):
+    from nimbus_sampler import workloads
+    B, V = 64, 50257
+    rnd = np.random.Generator(np.random.PCG64(int(pen * 100) + int(T * 10)))
+    x = workloads.headline(B)
+    gen = [rnd.integers(0, V + 8, size=int(rnd.integers(0, 400))) for _ in range(B)]
+    _check(sampler, x, V, _params(temperature=T, top_p=1.0, repetition_penalty=pen), gen,
+           f"top-p off pen={pen} T={T}")
+
+
+@pytest.mark.parametrize("pen", [1.0001, 0.5])
+def test_top_p_off_histories_on_the_top(sampler, pen):
+    # the history holds each row's top tokens: with penalty < 1 their values
+    # rise past the row's unpenalised max (the reference moves up with them)
+    from nimbus_sampler import workloads
+    B, V = 64, 50257
+    rnd = np.random.Generator(np.random.PCG64(23 + int(pen * 10)))
+    x = workloads.headline(B)
+    order = np.argsort(-x, axis=1, kind="stable")
+    gen = [order[r, : int(rnd.integers(1, 60))] for r in range(B)]
+    gpu, _ = _check(sampler, x, V, _params(temperature=0.8, top_p=1.0, repetition_penalty=pen),
+                    gen, f"top-p off top pen={pen}")
+    drew = sum(int(gpu[0][r]) in set(gen[r].tolist()) for r in range(B))
+    print(f"[penalty] top-p off rows that drew a penalised token: {drew}/{B}", flush=True)
+    assert drew > B // 4
