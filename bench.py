@@ -240,9 +240,20 @@ def bench_lm_head(args):
     heads = [(data, scales)] + [(data.clone(), scales.clone() if scales is not None else None)
                                 for _ in range(ncopy - 1)]
 
+    greedy = args.greedy and B == 1
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+
     def run(i):
         d, sc = heads[i % ncopy]
+        if greedy:
+            sampler.lm_head_greedy(x[0], fmt, d, V, scales=sc, group_size=group, token=tok)
+        else:
+            sampler.lm_head_logits(x, fmt, d, V, scales=sc, group_size=group, out=out)
+
+    def run_split(i):  # the two-call form the fused one replaces
+        d, sc = heads[i % ncopy]
         sampler.lm_head_logits(x, fmt, d, V, scales=sc, group_size=group, out=out)
+        sampler.argmax_batch(out, tokens=tok)
 
     for i in range(args.warmup):
         run(i)
@@ -257,8 +268,18 @@ def bench_lm_head(args):
     e1.record(stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / K
+    split_us = None
+    if greedy:
+        for i in range(args.warmup):
+            run_split(i)
+        e0.record(stream)
+        for i in range(K):
+            run_split(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        split_us = e0.elapsed_time(e1) * 1e3 / K
     flops = 2.0 * B * V * H
-    alg_bytes = wbytes + B * H * 4 + B * V * 4
+    alg_bytes = wbytes + B * H * 4 + (4 if greedy else B * V * 4)
     t_mfma = flops / (MFMA_F32_PEAK_TFLOPS * 1e12)
     t_hbm = alg_bytes / (HBM_PEAK_GBS * 1e9)
     if t_mfma >= t_hbm:
@@ -292,7 +313,9 @@ def bench_lm_head(args):
                          "restatement of quant.rs/simd.rs (not the reference's f32 SIMD loop)",
                "check": f"GPU rows within {err:.3f} of the f32 summation error bound"}
     print(json.dumps({
-        "metric": f"LM-head logits: hidden rows/s, B={B} x H={H} -> V={V}, {args.lm_head} weights"
+        "metric": (f"LM head + greedy token (fused): decode steps/s, H={H} -> V={V}, "
+                   f"{args.lm_head} weights" if greedy else
+                   f"LM-head logits: hidden rows/s, B={B} x H={H} -> V={V}, {args.lm_head} weights")
                   + (f" (groups of {group})" if group else ""),
         "value": B / (us * 1e-6), "unit": "hidden rows/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True,
@@ -301,7 +324,8 @@ def bench_lm_head(args):
                 "(working set past the 256 MiB MALL)",
         "config": {"workload": f"lm_head_{args.lm_head}", "B": B, "H": H, "V": V,
                    "group_size": group, "alg_bytes": alg_bytes, "flops": flops,
-                   "head_copies": ncopy},
+                   "head_copies": ncopy,
+                   "split_logits_then_argmax_us": split_us},
         "roofline": roof, "cpu_baseline": cpu,
     }))
     sampler.close()
@@ -332,6 +356,10 @@ def main():
     ap.add_argument("--lm-head", choices=("f32", "int8", "int4"), default=None,
                     help="time the LM-head logits producer with these weights instead")
     ap.add_argument("--lm-b", type=int, default=256, help="hidden rows for --lm-head")
+    ap.add_argument("--greedy", action="store_true",
+                    help="with --lm-head and --lm-b 1: time nis_lm_head_greedy (GEMV with the "
+                         "greedy token in its epilogue) and, beside it, nis_lm_head_logits + "
+                         "nis_argmax_batch")
     ap.add_argument("--lm-h", type=int, default=768, help="hidden size for --lm-head")
     ap.add_argument("--lm-group", type=int, default=0, help="group size for quantized --lm-head")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",

@@ -210,6 +210,22 @@ typedef struct nis_weights {
 int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t B, int32_t H,
                        const nis_weights* w, int64_t V, float* d_logits, int64_t ld);
 
+/* Greedy decoding of one hidden row: *d_token = the first index of the
+ * maximum of the logits nis_lm_head_logits would produce for B = 1
+ * (Model::logits_last, model.rs:317-325, then sample()'s greedy branch,
+ * sampler.rs:172-181: a NaN at index 0 gives 0, other NaNs never win).  The
+ * one-row GEMV keeps each workgroup's first maximum in its epilogue and one
+ * small workgroup reduces those, so the logits are not read again.  d_logits
+ * [V] may be null (then they are not written).  No counterpart in the
+ * reference, which has no fused form: it is nis_lm_head_logits followed by
+ * nis_argmax_batch in one pass, for a decode loop that wants the token only.
+ * The first call allocates the context's key buffer (512 KiB); a shape the
+ * one-row kernel does not take runs those two calls instead (with a context-
+ * owned logits buffer when d_logits is null).  Asynchronous on the context
+ * stream. */
+int nis_lm_head_greedy(nis_ctx* ctx, const float* d_hidden, int32_t H, const nis_weights* w, int64_t V,
+                       float* d_logits, uint32_t* d_token);
+
 /* Wait for all work queued on the context stream. */
 int nis_sync(nis_ctx* ctx);
 

@@ -30,6 +30,11 @@ struct nis_ctx {
     // staging for nis_sample_one
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // nis_lm_head_greedy: the workgroup keys, and logits when the caller
+    // passes none to a call that needs them
+    unsigned long long* gpart = nullptr;
+    float* glogits = nullptr;
+    int64_t glogits_n = 0;
 };
 
 namespace {
@@ -237,8 +242,13 @@ void launch_lm_head_f(const nis::LmHeadArgs& a, bool vec, bool grouped, int nb, 
 // 16-byte runs per row (H % R == 0), one scale per run, aligned operands and
 // at most KMAX runs per lane with 16 or 64 lanes per row.  Returns false to
 // leave the call to the matrix-core kernel.
-template <int FMT>
-bool launch_lm_head_row(const nis::LmHeadArgs& a, bool grouped, uintptr_t wp, hipStream_t st) {
+// nis_lm_head_greedy: workgroup keys kept per context (a fused launch of more
+// workgroups takes the two-launch form instead)
+constexpr int64_t kGreedyMaxBlocks = 1 << 16;
+
+template <int FMT, bool GREEDY = false>
+bool launch_lm_head_row(const nis::LmHeadArgs& a, bool grouped, uintptr_t wp, hipStream_t st,
+                        int64_t* blocks = nullptr) {
     constexpr int R = nis::LhRowCfg<FMT>::R;
     constexpr int KMAX = nis::LhRowCfg<FMT>::KMAX;
     if (a.H % R != 0 || (wp & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
@@ -251,11 +261,66 @@ bool launch_lm_head_row(const nis::LmHeadArgs& a, bool grouped, uintptr_t wp, hi
     const int64_t rows_per_wave = (int64_t)(64 >> log2L) * nis::LhRowCfg<FMT>::ITER;
     const int64_t waves = (a.V + rows_per_wave - 1) / rows_per_wave;
     const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if (blocks) *blocks = (int64_t)grid.x;
+    if (GREEDY && (int64_t)grid.x > kGreedyMaxBlocks) return false;
     if (grouped)
-        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, true>), grid, block, 0, st, a, log2L, runs);
+        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, true, GREEDY>), grid, block, 0, st, a, log2L, runs);
     else
-        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, false>), grid, block, 0, st, a, log2L, runs);
+        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, false, GREEDY>), grid, block, 0, st, a, log2L,
+                           runs);
     return true;
+}
+
+// Argument checks of the LM-head entry points, and their kernel arguments.
+int lm_head_setup(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t B, int32_t H,
+                  const nis_weights* w, int64_t V, float* d_logits, int64_t ld, bool logits_optional,
+                  nis::LmHeadArgs& a, bool& grouped, bool& vec, uintptr_t& wp) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_hidden || !w || (!d_logits && !logits_optional) || !w->d_data)
+        return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (B <= 0 || H <= 0 || V <= 0) return fail(ctx, NIS_EINVAL, "B, H and V must be positive");
+    if (ldh < H || ld < V) return fail(ctx, NIS_EINVAL, "ldh must be >= H and ld >= V");
+    if (B > NIS_MAX_B || V > NIS_MAX_V || H > NIS_MAX_H) return fail(ctx, NIS_ERANGE, "B, H or V too large");
+    const int fmt = w->format;
+    if (fmt != NIS_W_F32 && fmt != NIS_W_INT8 && fmt != NIS_W_INT4)
+        return fail(ctx, NIS_EINVAL, "unknown weight format");
+    const int32_t g = w->group_size;
+    if (fmt == NIS_W_F32) {
+        if (g != 0) return fail(ctx, NIS_EINVAL, "f32 weights take no group size");
+    } else {
+        if (!w->d_scales) return fail(ctx, NIS_EINVAL, "quantized weights need scales");
+        if (g < 0 || (g > 0 && H % g != 0)) return fail(ctx, NIS_EINVAL, "group size must divide H");
+        // the reference's int4 row / group reader starts at a low nibble
+        // (quant.rs:130-133, 150-152), which is its packing only at even offsets
+        if (fmt == NIS_W_INT4 && (H % 2 != 0 || g % 2 != 0))
+            return fail(ctx, NIS_EINVAL, "int4 weights need an even H and group size");
+    }
+    if (((uintptr_t)d_hidden & 3u) || ((uintptr_t)d_logits & 3u) || ((uintptr_t)w->d_scales & 3u) ||
+        (fmt == NIS_W_F32 && ((uintptr_t)w->d_data & 3u)))
+        return fail(ctx, NIS_EALIGN, "hidden, logits, scales and f32 weights must be 4-byte aligned");
+
+    a.x = d_hidden;
+    a.ldx = ldh;
+    a.B = B;
+    a.H = H;
+    a.w = w->d_data;
+    a.scales = w->d_scales;
+    a.group = g > 0 ? g : H;
+    a.groups = H / a.group;
+    // ceil(2^32 / group) fits 32 bits for group >= 2; group 1 is marked by 0
+    a.gmagic = a.group == 1 ? 0u
+                            : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)a.group - 1) / (uint64_t)a.group);
+    a.V = V;
+    a.out = d_logits;
+    a.ld = ld;
+    a.part = nullptr;
+    grouped = fmt != NIS_W_F32 && a.groups > 1;
+    wp = (uintptr_t)w->d_data;
+    vec = H % 4 == 0 && ldh % 4 == 0 && ((uintptr_t)d_hidden & 15u) == 0 &&
+          (!grouped || a.group % 4 == 0) &&
+          ((fmt == NIS_W_F32 && (wp & 15u) == 0) || (fmt == NIS_W_INT8 && (wp & 3u) == 0) ||
+           (fmt == NIS_W_INT4 && (wp & 1u) == 0));
+    return NIS_OK;
 }
 
 }  // namespace
@@ -308,6 +373,8 @@ int nis_ctx_destroy(nis_ctx* ctx) {
         (void)hipStreamDestroy(ctx->own_stream);
     }
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->gpart) (void)hipFree(ctx->gpart);
+    if (ctx->glogits) (void)hipFree(ctx->glogits);
     delete ctx;
     return rc;
 }
@@ -416,52 +483,14 @@ int nis_apply_repetition_penalty(nis_ctx* ctx, double* d_logits, int64_t V,
 
 int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t B, int32_t H,
                        const nis_weights* w, int64_t V, float* d_logits, int64_t ld) {
-    if (!ctx) return NIS_EINVAL;
-    if (!d_hidden || !w || !d_logits || !w->d_data) return fail(ctx, NIS_EINVAL, "null pointer argument");
-    if (B <= 0 || H <= 0 || V <= 0) return fail(ctx, NIS_EINVAL, "B, H and V must be positive");
-    if (ldh < H || ld < V) return fail(ctx, NIS_EINVAL, "ldh must be >= H and ld >= V");
-    if (B > NIS_MAX_B || V > NIS_MAX_V || H > NIS_MAX_H) return fail(ctx, NIS_ERANGE, "B, H or V too large");
+    nis::LmHeadArgs a;
+    bool grouped = false, vec = false;
+    uintptr_t wp = 0;
+    int rc = lm_head_setup(ctx, d_hidden, ldh, B, H, w, V, d_logits, ld, false, a, grouped, vec, wp);
+    if (rc != NIS_OK) return rc;
     const int fmt = w->format;
-    if (fmt != NIS_W_F32 && fmt != NIS_W_INT8 && fmt != NIS_W_INT4)
-        return fail(ctx, NIS_EINVAL, "unknown weight format");
-    const int32_t g = w->group_size;
-    if (fmt == NIS_W_F32) {
-        if (g != 0) return fail(ctx, NIS_EINVAL, "f32 weights take no group size");
-    } else {
-        if (!w->d_scales) return fail(ctx, NIS_EINVAL, "quantized weights need scales");
-        if (g < 0 || (g > 0 && H % g != 0)) return fail(ctx, NIS_EINVAL, "group size must divide H");
-        // the reference's int4 row / group reader starts at a low nibble
-        // (quant.rs:130-133, 150-152), which is its packing only at even offsets
-        if (fmt == NIS_W_INT4 && (H % 2 != 0 || g % 2 != 0))
-            return fail(ctx, NIS_EINVAL, "int4 weights need an even H and group size");
-    }
-    if (((uintptr_t)d_hidden & 3u) || ((uintptr_t)d_logits & 3u) || ((uintptr_t)w->d_scales & 3u) ||
-        (fmt == NIS_W_F32 && ((uintptr_t)w->d_data & 3u)))
-        return fail(ctx, NIS_EALIGN, "hidden, logits, scales and f32 weights must be 4-byte aligned");
     DeviceGuard dg(ctx->device);
     if (dg.status != hipSuccess) return hip_fail(ctx, dg.status, "hipSetDevice");
-
-    nis::LmHeadArgs a;
-    a.x = d_hidden;
-    a.ldx = ldh;
-    a.B = B;
-    a.H = H;
-    a.w = w->d_data;
-    a.scales = w->d_scales;
-    a.group = g > 0 ? g : H;
-    a.groups = H / a.group;
-    // ceil(2^32 / group) fits 32 bits for group >= 2; group 1 is marked by 0
-    a.gmagic = a.group == 1 ? 0u
-                            : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)a.group - 1) / (uint64_t)a.group);
-    a.V = V;
-    a.out = d_logits;
-    a.ld = ld;
-    const bool grouped = fmt != NIS_W_F32 && a.groups > 1;
-    const uintptr_t wp = (uintptr_t)w->d_data;
-    const bool vec = H % 4 == 0 && ldh % 4 == 0 && ((uintptr_t)d_hidden & 15u) == 0 &&
-                     (!grouped || a.group % 4 == 0) &&
-                     ((fmt == NIS_W_F32 && (wp & 15u) == 0) || (fmt == NIS_W_INT8 && (wp & 3u) == 0) ||
-                      (fmt == NIS_W_INT4 && (wp & 1u) == 0));
     if (B == 1 && fmt == NIS_W_F32) {
         if (launch_lm_head_row<nis::kLhF32>(a, false, wp, ctx->stream)) goto launched;
     } else if (B == 1 && fmt == NIS_W_INT8) {
@@ -485,6 +514,58 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
 launched:
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "lm_head kernel launch");
+}
+
+int nis_lm_head_greedy(nis_ctx* ctx, const float* d_hidden, int32_t H, const nis_weights* w, int64_t V,
+                       float* d_logits, uint32_t* d_token) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_token) return fail(ctx, NIS_EINVAL, "null pointer argument");
+    nis::LmHeadArgs a;
+    bool grouped = false, vec = false;
+    uintptr_t wp = 0;
+    int rc = lm_head_setup(ctx, d_hidden, H, 1, H, w, V, d_logits, V, true, a, grouped, vec, wp);
+    if (rc != NIS_OK) return rc;
+    DeviceGuard dg(ctx->device);
+    if (dg.status != hipSuccess) return hip_fail(ctx, dg.status, "hipSetDevice");
+    if (!ctx->gpart) {  // once per context: the fused launch's workgroup keys
+        hipError_t e = hipMalloc((void**)&ctx->gpart, (size_t)kGreedyMaxBlocks * sizeof(unsigned long long));
+        if (e != hipSuccess) {
+            ctx->gpart = nullptr;
+            return hip_fail(ctx, e, "hipMalloc greedy keys");
+        }
+    }
+    a.part = ctx->gpart;
+    const int fmt = w->format;
+    int64_t blocks = 0;
+    bool fused = false;
+    if (fmt == NIS_W_F32) fused = launch_lm_head_row<nis::kLhF32, true>(a, false, wp, ctx->stream, &blocks);
+    else if (fmt == NIS_W_INT8) fused = launch_lm_head_row<nis::kLhInt8, true>(a, grouped, wp, ctx->stream, &blocks);
+    else fused = launch_lm_head_row<nis::kLhInt4, true>(a, grouped, wp, ctx->stream, &blocks);
+    if (fused) {
+        hipLaunchKernelGGL(nis::lm_head_greedy_final_kernel, dim3(1), dim3(1024), 0, ctx->stream,
+                           (const unsigned long long*)ctx->gpart, (int)blocks, d_token);
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "lm_head greedy launch");
+    }
+    // a shape the one-row kernel does not take: the logits, then the greedy
+    // row kernel over them
+    float* lg = d_logits;
+    if (!lg) {
+        if (ctx->glogits_n < V) {
+            if (ctx->glogits) (void)hipFree(ctx->glogits);
+            ctx->glogits_n = 0;
+            hipError_t e = hipMalloc((void**)&ctx->glogits, (size_t)V * sizeof(float));
+            if (e != hipSuccess) {
+                ctx->glogits = nullptr;
+                return hip_fail(ctx, e, "hipMalloc greedy logits");
+            }
+            ctx->glogits_n = V;
+        }
+        lg = ctx->glogits;
+    }
+    rc = nis_lm_head_logits(ctx, d_hidden, H, 1, H, w, V, lg, V);
+    if (rc != NIS_OK) return rc;
+    return nis_argmax_batch(ctx, lg, V, 1, V, d_token);
 }
 
 int nis_sync(nis_ctx* ctx) {

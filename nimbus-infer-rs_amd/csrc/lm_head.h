@@ -52,9 +52,28 @@ struct LmHeadArgs {
     int32_t wv;            // waves of a workgroup along v (wv * wb waves)
     int32_t wb;            // waves of a workgroup along b
     int64_t V;
-    float* out;            // logits [B][ld]
+    float* out;            // logits [B][ld] (greedy form: may be null)
     int64_t ld;
+    unsigned long long* part;  // greedy form: one key per workgroup (lh_greedy_key)
 };
+
+// Greedy order of one logit (sampler.rs:172-181: the first index of the
+// maximum; a NaN at index 0 stops every comparison, so index 0 wins; any
+// other NaN never wins): larger keys win, and on equal values the lower index
+// (its complement sits in the low half).
+__device__ __forceinline__ unsigned long long lh_greedy_key(float x, int64_t v) {
+    const uint32_t lo = 0xFFFFFFFFu - (uint32_t)v;
+    if (x != x) return v == 0 ? ~0ull : (((unsigned long long)key32(-INFINITY) << 32) | lo);
+    return ((unsigned long long)key32(x) << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long lh_wave_max_u64(unsigned long long k) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long t = (unsigned long long)__shfl_xor((long long)k, o);
+        k = t > k ? t : k;
+    }
+    return k;
+}
 
 // floor(h / group) for 0 <= h < 2^31: the product with ceil(2^32/group) is
 // exact or one too high.  Group 1 (magic 0) is h itself.
@@ -271,7 +290,12 @@ __device__ __forceinline__ float lh_run_dot(const uint4& raw, const float* xr) {
     return part;
 }
 
-template <int FMT, bool GROUPED>
+// GREEDY: greedy decoding fused into the epilogue.  Each lane holding a
+// finished row keeps the best greedy key of its rows; the workgroup's best
+// goes to a.part[blockIdx.x], and lm_head_greedy_final_kernel reduces those.
+// (The last workgroup to finish reducing them instead needs a release fence
+// per workgroup, which writes the L2 back each time: far slower.)
+template <int FMT, bool GROUPED, bool GREEDY = false>
 __global__ __launch_bounds__(256) void lm_head_row_kernel(LmHeadArgs a, int log2L, int runs) {
     constexpr int R = LhRowCfg<FMT>::R;
     constexpr int KMAX = LhRowCfg<FMT>::KMAX;
@@ -281,7 +305,16 @@ __global__ __launch_bounds__(256) void lm_head_row_kernel(LmHeadArgs a, int log2
     const int P = 64 >> log2L;
     constexpr int ITER = LhRowCfg<FMT>::ITER;
     const int64_t wave_row0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * P * ITER;
-    if (wave_row0 >= a.V) return;  // wave-uniform
+    __shared__ unsigned long long gk[GREEDY ? 4 : 1];  // greedy: each wave's best key
+    if (wave_row0 >= a.V) {  // wave-uniform
+        if (GREEDY) {
+            if (lane == 0) gk[threadIdx.x >> 6] = 0ull;
+            __syncthreads();
+            if (threadIdx.x == 0) a.part[blockIdx.x] = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
+        }
+        return;
+    }
+    unsigned long long best = 0ull;  // greedy: this lane's best key
     const int gl = lane >> log2L;
     const int64_t row_bytes = FMT == kLhF32 ? (int64_t)a.H * 4 : (FMT == kLhInt8 ? (int64_t)a.H : (int64_t)a.H / 2);
 
@@ -332,9 +365,36 @@ __global__ __launch_bounds__(256) void lm_head_row_kernel(LmHeadArgs a, int log2
         for (int off = L >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
         if (li == 0 && v < a.V) {
             if (FMT != kLhF32 && !GROUPED) acc *= a.scales[v];  // dot * scale (quant.rs:128)
-            a.out[v] = acc;
+            if (!GREEDY || a.out != nullptr) a.out[v] = acc;
+            if (GREEDY) {
+                const unsigned long long k = lh_greedy_key(acc, v);
+                best = k > best ? k : best;
+            }
         }
     }
+    if constexpr (GREEDY) {
+        best = lh_wave_max_u64(best);
+        if (lane == 0) gk[threadIdx.x >> 6] = best;
+        __syncthreads();  // (waves past V took the same barrier)
+        if (threadIdx.x == 0) a.part[blockIdx.x] = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
+    }
 }
+
+// The greedy token from n workgroup keys: one workgroup of 1024 lanes.
+__global__ __launch_bounds__(1024) void lm_head_greedy_final_kernel(const unsigned long long* part,
+                                                                    int n, uint32_t* token) {
+    __shared__ unsigned long long wk[16];
+    unsigned long long k = 0ull;
+    for (int i = (int)threadIdx.x; i < n; i += 1024) k = part[i] > k ? part[i] : k;
+    k = lh_wave_max_u64(k);
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        unsigned long long t = threadIdx.x < 16 ? wk[threadIdx.x] : 0ull;
+        t = lh_wave_max_u64(t);
+        if (threadIdx.x == 0) *token = 0xFFFFFFFFu - (uint32_t)t;
+    }
+}
+
 
 }  // namespace nis

@@ -36,7 +36,7 @@ EXPORTED_SYMBOLS = (
     "nis_rng_next_f64", "nis_rng_seed_batch", "nis_sample_batch", "nis_argmax_batch",
     "nis_apply_repetition_penalty", "nis_sample_one", "nis_sample_one_noalloc", "nis_sync",
     "nis_decode_step",
-    "nis_lm_head_logits",
+    "nis_lm_head_logits", "nis_lm_head_greedy",
 )
 
 
@@ -105,6 +105,8 @@ def load_library(path: str = LIB_PATH):
                                   ctypes.c_int32, vp, vp, vp]
     L.nis_lm_head_logits.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                      ctypes.POINTER(NisWeights), ctypes.c_int64, vp, ctypes.c_int64]
+    L.nis_lm_head_greedy.argtypes = [vp, vp, ctypes.c_int32, ctypes.POINTER(NisWeights),
+                                     ctypes.c_int64, vp, vp]
     L.nis_apply_repetition_penalty.argtypes = [vp, vp, ctypes.c_int64, vp, ctypes.c_int64,
                                                ctypes.c_float]
     L.nis_sample_one.argtypes = [vp, vp, ctypes.c_int64, ctypes.POINTER(NisParams), vp,
@@ -265,6 +267,37 @@ class Sampler:
         _check(self._L, self._ctx, rc)
         return tokens
 
+    def _weights(self, H: int, fmt: int, data, V: int, scales, group_size: int, tensors):
+        """nis_weights for a [V, H] head, after checking every size the C ABI
+        will read (it sees bare pointers) and that all tensors share the
+        sampler's device."""
+        import torch
+        fmt, group_size = int(fmt), int(group_size)
+        if fmt == W_F32:
+            need, ddtype = V * H, torch.float32
+        elif fmt == W_INT8:
+            need, ddtype = V * H, torch.uint8
+        elif fmt == W_INT4:
+            need, ddtype = (V * H + 1) // 2, torch.uint8
+        else:
+            raise SamplerError(NIS_EINVAL, f"unknown weight format {fmt}")
+        if data.dtype != ddtype or not data.is_contiguous() or data.numel() < need:
+            raise SamplerError(NIS_EINVAL, f"weights must be contiguous {ddtype} with at least "
+                                           f"{need} elements (got {data.dtype}, {data.numel()})")
+        tensors = list(tensors) + [data]
+        if fmt != W_F32:
+            groups = H // group_size if group_size > 0 and H % group_size == 0 else 1
+            if scales is None or scales.dtype != torch.float32 or not scales.is_contiguous() or \
+                    scales.numel() < V * groups:
+                raise SamplerError(NIS_EINVAL, f"scales must be contiguous float32 with at least "
+                                               f"{V * groups} elements")
+            tensors.append(scales)
+        dev = torch.device("cuda", self.device)
+        if any(t.device != dev for t in tensors):
+            raise SamplerError(NIS_EINVAL, f"hidden, weights, scales and outputs must be on {dev}")
+        return NisWeights(fmt, group_size, data.data_ptr(),
+                          scales.data_ptr() if scales is not None else None)
+
     def lm_head_logits(self, hidden, fmt: int, data, V: int, scales=None, group_size: int = 0,
                        out=None):
         """Logits of B last-hidden rows (model.rs:317-325) on device tensors.
@@ -279,41 +312,45 @@ class Sampler:
         H = hidden.shape[1]
         if out is None:
             out = torch.empty((B, V), dtype=torch.float32, device=hidden.device)
-        # the C ABI sees bare pointers: every size it will read is checked here
         if out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1 or \
                 out.shape[0] < B or out.shape[1] < V:
             raise SamplerError(NIS_EINVAL, "out must be float32 [>= B, >= V] with unit column stride")
-        fmt, group_size = int(fmt), int(group_size)
-        if fmt == W_F32:
-            need, ddtype = V * H, torch.float32
-        elif fmt == W_INT8:
-            need, ddtype = V * H, torch.uint8
-        elif fmt == W_INT4:
-            need, ddtype = (V * H + 1) // 2, torch.uint8
-        else:
-            raise SamplerError(NIS_EINVAL, f"unknown weight format {fmt}")
-        if data.dtype != ddtype or not data.is_contiguous() or data.numel() < need:
-            raise SamplerError(NIS_EINVAL, f"weights must be contiguous {ddtype} with at least "
-                                           f"{need} elements (got {data.dtype}, {data.numel()})")
-        tensors = [hidden, data, out]
-        if fmt != W_F32:
-            groups = H // group_size if group_size > 0 and H % group_size == 0 else 1
-            if scales is None or scales.dtype != torch.float32 or not scales.is_contiguous() or \
-                    scales.numel() < V * groups:
-                raise SamplerError(NIS_EINVAL, f"scales must be contiguous float32 with at least "
-                                               f"{V * groups} elements")
-            tensors.append(scales)
-        dev = torch.device("cuda", self.device)
-        if any(t.device != dev for t in tensors):
-            raise SamplerError(NIS_EINVAL, f"hidden, weights, scales and out must be on {dev}")
-        w = NisWeights(int(fmt), int(group_size), data.data_ptr(),
-                       scales.data_ptr() if scales is not None else None)
+        w = self._weights(H, fmt, data, V, scales, group_size, [hidden, out])
         self._bind_stream()
         rc = self._L.nis_lm_head_logits(self._ctx, ctypes.c_void_p(hidden.data_ptr()),
                                         hidden.stride(0), B, H, ctypes.byref(w), V,
                                         ctypes.c_void_p(out.data_ptr()), out.stride(0))
         _check(self._L, self._ctx, rc)
         return out
+
+    def lm_head_greedy(self, hidden, fmt: int, data, V: int, scales=None, group_size: int = 0,
+                       logits=None, token=None):
+        """Greedy token of one last-hidden row (model.rs:317-325, then
+        sampler.rs:172-181) in one pass over the head (nis_lm_head_greedy).
+
+        hidden: float32 [H] or [1, H]; logits: optional float32 [>= V] that
+        also receives the logits; token: optional int32 [1].  Returns token."""
+        import torch
+        h = hidden.reshape(-1)
+        assert h.dtype == torch.float32 and h.is_contiguous()
+        H = h.numel()
+        if token is None:
+            token = torch.empty(1, dtype=torch.int32, device=h.device)
+        if token.dtype != torch.int32 or token.numel() < 1:
+            raise SamplerError(NIS_EINVAL, "token must be int32 with one element")
+        tensors = [h, token]
+        if logits is not None:
+            if logits.dtype != torch.float32 or not logits.is_contiguous() or logits.numel() < V:
+                raise SamplerError(NIS_EINVAL, "logits must be contiguous float32 [>= V]")
+            tensors.append(logits)
+        w = self._weights(H, fmt, data, V, scales, group_size, tensors)
+        self._bind_stream()
+        rc = self._L.nis_lm_head_greedy(
+            self._ctx, ctypes.c_void_p(h.data_ptr()), H, ctypes.byref(w), V,
+            ctypes.c_void_p(logits.data_ptr()) if logits is not None else None,
+            ctypes.c_void_p(token.data_ptr()))
+        _check(self._L, self._ctx, rc)
+        return token
 
     def argmax_batch(self, logits, V: Optional[int] = None, tokens=None):
         import torch

@@ -160,3 +160,89 @@ def test_bench_kernel_cli_checks_match_oracle():
         exact, absd = lh.lm_head_logits(x[None, :], fmt, data, ones, 1, 768)
         assert abs(check - exact[0, 0]) <= lh.f32_bound(absd[0, 0], 768) + 5e-5, (fmt, check, exact)
     assert all(res[f"{k}_gflops"] > 0 for k in ("f32", "int8", "int4"))
+
+
+# ---------------------------------------------------------------------------
+# nis_lm_head_greedy: the one-row GEMV with the greedy token fused into its
+# epilogue.  The token must be the reference's greedy answer (sampler.rs:172-
+# 181: first index of the maximum, a NaN at index 0 gives 0) on the logits
+# the same call writes, and equal nis_argmax_batch on them.
+
+def _greedy_ref(v):
+    best = 0
+    for i in range(1, len(v)):
+        if v[i] > v[best]:
+            best = i
+    return best
+
+
+def _greedy_case(sampler, fmt, H, V, group=None, seed=0, tweak=None, with_logits=True):
+    import torch
+    rnd = np.random.default_rng(seed)
+    x = rnd.standard_normal(H).astype(np.float32)
+    data, scales = _weights(fmt, V, H, group, rnd)
+    if tweak is not None:
+        data, scales, x = tweak(data, scales, x)
+    dev = torch.device("cuda:0")
+    d = torch.from_numpy(np.ascontiguousarray(data)).to(dev)
+    s = torch.from_numpy(scales).to(dev) if scales is not None else None
+    xt = torch.from_numpy(x).to(dev)
+    print(f"[lm_head greedy] fmt={fmt} H={H} V={V} group={group} seed={seed}", flush=True)
+    logits = torch.full((V,), float("nan"), dtype=torch.float32, device=dev) if with_logits else None
+    tok = sampler.lm_head_greedy(xt, fmt, d, V, scales=s, group_size=group or 0, logits=logits)
+    # the same head through the two-call path, for the logits and argmax_batch
+    out = sampler.lm_head_logits(xt.reshape(1, -1), fmt, d, V, scales=s, group_size=group or 0)
+    am = sampler.argmax_batch(out)
+    torch.cuda.synchronize()
+    lg = out.cpu().numpy()[0]
+    if with_logits:
+        assert np.array_equal(logits.cpu().numpy(), lg, equal_nan=True), "fused logits differ"
+    t = int(tok.cpu().numpy()[0])
+    assert t == _greedy_ref(lg) == int(am.cpu().numpy()[0]), (t, _greedy_ref(lg))
+    return t
+
+
+@pytest.mark.parametrize("fmt,H,V,group", [
+    (0, 768, 50257, None),    # GPT-2 head, 64 lanes per row
+    (8, 768, 50257, None),    # int8, 16 lanes per row
+    (8, 768, 50257, 64),      # int8 grouped
+    (4, 768, 50257, 64),      # int4 grouped
+    (4, 4096, 999, None),     # 64 lanes, 2 runs per lane
+    (0, 1024, 777, None),     # a grid of few workgroups, the last one partly past V
+    (0, 4096, 300, None),     # over the one-row kernel's cap: the two-launch form
+    (4, 40, 65, None),        # int4 H % 32 != 0: the two-launch form
+])
+def test_greedy_matches_argmax_of_the_logits(sampler, fmt, H, V, group):
+    for seed in range(3):
+        _greedy_case(sampler, fmt, H, V, group, seed=seed, with_logits=seed != 1)
+
+
+def test_greedy_ties_take_the_first_index(sampler):
+    # duplicated weight rows give bit-identical logits: the lowest index of
+    # the maximum must win, across waves and workgroups
+    H, V = 768, 50257
+
+    def tweak(data, scales, x):
+        w = data.reshape(V, H).copy()
+        top = int(np.argmax(w @ x))
+        for j in (7, 5000, top + 1 if top + 1 < V else 3, 49999):
+            w[j] = w[top]
+        w[2] = w[top]  # the lowest copy
+        return w.reshape(-1), scales, x
+    assert _greedy_case(sampler, 0, H, V, tweak=tweak) == 2
+
+
+def test_greedy_nan_rules(sampler):
+    # a NaN logit at index 0 gives 0 (every comparison fails); a NaN elsewhere
+    # never wins
+    H, V = 768, 20000
+
+    def nan_at(j):
+        def tweak(data, scales, x):
+            w = data.reshape(V, H).copy()
+            w[j, 5] = np.float32(np.nan)
+            return w.reshape(-1), scales, x
+        return tweak
+    assert _greedy_case(sampler, 0, H, V, tweak=nan_at(0)) == 0
+    t = _greedy_case(sampler, 0, H, V, tweak=nan_at(123))
+    assert t != 123
