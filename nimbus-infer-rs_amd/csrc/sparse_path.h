@@ -42,13 +42,16 @@
 // agree to the last bit and the inverse-CDF walk (sampler.rs:209-216)
 // always finds its crossing.
 //
-// Hand-offs after the stream: the last wave to finish its histogram adds
-// (an LDS counter) finds b_p; one barrier publishes it; every wave then sums
-// its kept mass above b_p per lane segment of its list and lists its members
-// of b_p; the last wave to finish that (a second counter) ranks the members
-// and walks waves -> the chosen wave's list segments -> elements.  Any step
-// that cannot prove its result returns a reject code before the barrier; the
-// caller then runs the general path on the row.
+// Hand-offs after the stream: once every wave's histogram adds are done (one
+// barrier), wave 0 finds b_p; a second barrier publishes it; every wave then
+// sums its kept mass above b_p per lane segment of its list and lists its
+// members of b_p; the last wave to finish that (an LDS counter) ranks the
+// members and walks waves -> the chosen wave's list segments -> elements.
+// Any step that cannot prove its result returns a reject code before the
+// second barrier; the caller then runs the general path on the row.
+// The octave histogram keeps 8 copies of each bin (lane & 7 picks one), so
+// the 64 lanes of one add round, whose candidates crowd into a few octaves,
+// hit up to 8 times as many addresses.
 #pragma once
 #include "fast_path.h"
 #include "penalty_bits.h"
@@ -67,8 +70,8 @@ constexpr int kSSeg = kSE / 64;             // list entries per lane segment (at
 constexpr int kSRes = 64;                   // histogram buckets per octave of x*c
 constexpr int kSLog = 6;                    // log2(kSRes)
 constexpr int kSHB = 32 * kSRes;            // bucket ring: 32 octaves
-constexpr int kSPer = kSHB / 64;            // search rounds (64 buckets each, at most)
 constexpr int kSMem = 64;                   // members of the cutoff bucket
+constexpr int kSOctC = 8;                   // copies of each octave bin (lane & 7 picks one)
 constexpr uint32_t kSNone = 0x80000000u;    // packed bucket of no candidate (below any b_p)
 // repetition penalty (sample_rows_sparse_pen_kernel)
 constexpr int kSSide = 48;                  // penalised elements per wave
@@ -147,7 +150,7 @@ struct WideShared {
     uint16_t epos[kSW][kSE + 64];  //   their chunk * 64 + lane
     uint32_t whist[kSW][256];      // each wave's sample histogram (1/8-octave bins)
     unsigned long long hist[kSHB]; // [b & (kSHB-1)]: count << 48 | sum of fm, buckets >= blo
-    unsigned long long oct[32];    // the same per octave
+    unsigned long long oct[32 * kSOctC]; // the same per octave, kSOctC copies each
     double seg[kSW][64];           // kept mass above b_p per lane segment of the entry lists
     double tw[kSW];                // per-wave kept mass (2^(R-40) units, integers)
     SMem mem[kSMem];               // members of b_p
@@ -155,7 +158,6 @@ struct WideShared {
     SCut cut;
     double u0;                     // the draw
     uint32_t nmem;
-    uint32_t cnt1;                 // waves done with their candidates
     uint32_t cnt2;                 // waves done with their kept sums
     // the waves' records reduced as they arrive (order-preserving keys)
     uint32_t kmax;                 // max logit
@@ -451,10 +453,9 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         if (tid == 0) sh.pover = hlong ? 1u : 0u;
     }
     *reinterpret_cast<u4v*>(&sh.hist[w * (kSHB / kSW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
-    if (l < 32 / kSW) sh.oct[w * (32 / kSW) + l] = 0ull;
+    if (l < 32 * kSOctC / kSW) sh.oct[w * (32 * kSOctC / kSW) + l] = 0ull;
     if (w == 0 && l == 0) {
         sh.nmem = 0u;
-        sh.cnt1 = 0u;
         sh.cnt2 = 0u;
         sh.kmax = 0u;
         sh.kxlo = 0u;
@@ -678,7 +679,8 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             if (cmk) {
                 const int b = s_bucket(ts);
                 lds_add2_u64_m(cmk, lds_addr(&sh.hist[0]) + 8 * ((uint32_t)b & (uint32_t)(kSHB - 1)),
-                               lds_addr(&sh.oct[0]) + 8 * ((uint32_t)(b >> kSLog) & 31u),
+                               lds_addr(&sh.oct[0]) + 8 * kSOctC * ((uint32_t)(b >> kSLog) & 31u) +
+                                   8 * ((uint32_t)l & (kSOctC - 1)),
                                (1ull << 48) | (uint64_t)s_pfm(yc, ts));
             }
             nsc = (uint32_t)__popcll(cmk);
@@ -713,7 +715,8 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     uint32_t cfm[kSRounds];  // its fm
     int nrd = 0;             // rounds (wave-uniform)
     {
-        const uint32_t hist0 = lds_addr(&sh.hist[0]), oct0 = lds_addr(&sh.oct[0]);
+        const uint32_t hist0 = lds_addr(&sh.hist[0]);
+        const uint32_t oct0 = lds_addr(&sh.oct[0]) + 8 * ((uint32_t)l & (kSOctC - 1));
         const float* const el = reinterpret_cast<const float*>(&sh.ent[w][0]) + 4 * e0;
 #pragma unroll
         for (int r = 0; r < kSRounds; ++r) {
@@ -733,7 +736,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const int b = s_bucket(tq);
             const uint32_t fm = s_fm(xq, c, tq);
             lds_add2_u64_m(am, hist0 + 8 * ((uint32_t)b & (uint32_t)(kSHB - 1)),
-                           oct0 + 8 * ((uint32_t)(b >> kSLog) & 31u), (1ull << 48) | (uint64_t)fm);
+                           oct0 + 8 * kSOctC * ((uint32_t)(b >> kSLog) & 31u), (1ull << 48) | (uint64_t)fm);
             cbk[r] = has ? (((uint32_t)b << 4) | bit) : kSNone;
             cfm[r] = fm;
         }
@@ -767,15 +770,11 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     }
     NIS_STS(2);
 
-    // ---- the last wave to finish its candidates runs the cutoff search ----
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    uint32_t done1 = 0u;
-    if (l == 0) done1 = atomicAdd(&sh.cnt1, 1u);
-    done1 = bcast_u32(done1, 0);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // ---- B1: every wave's candidates are in the histograms; wave 0 searches
     const int li = min(l, kSW - 1);
     const bool rv = l < kSW;
-    if (done1 == (uint32_t)(kSW - 1)) {
+    lds_barrier();
+    if (w == 0) {
         NIS_STS(3);
         __builtin_amdgcn_s_setprio(3);
         const u4v ra = *reinterpret_cast<const u4v*>(&sh.rec[li]);
@@ -799,7 +798,15 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const unsigned long long lv = (bl >= blo && bl <= bM) ? sh.hist[(uint32_t)bl & (kSHB - 1)] : 0ull;
         const int o = oM - l;
         const bool oin = l <= oM - olo;
-        const unsigned long long ovr = (oin && o != olo) ? sh.oct[(uint32_t)o & 31u] : 0ull;
+        unsigned long long ovr = 0ull;
+        if (oin && o != olo) {
+            const u4v* const oc = reinterpret_cast<const u4v*>(&sh.oct[kSOctC * ((uint32_t)o & 31u)]);
+#pragma unroll
+            for (int j = 0; j < kSOctC / 2; ++j) {
+                const u4v q = oc[j];
+                ovr += (((unsigned long long)q.y << 32) | q.x) + (((unsigned long long)q.w << 32) | q.z);
+            }
+        }
         const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
         // a wave whose reference sits far below the row max may have overflowed
         const bool range_ok = fmaf(M, c, -unkey32(sh.krwmin)) <= 120.0f;
