@@ -446,32 +446,43 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         xl_c = vl - fabsf(vl) * 1.0e-6f - 1.0e-30f;
         xh_c = vh + fabsf(vh) * 1.0e-6f + 1.0e-30f;
     }
+    // A side with more elements than the lists hold float4s (four elements
+    // each) cannot fit: such a row skips the listing and works in registers.
+    const uint32_t nside = kside ? nab0 + nsel0 : (uint32_t)V - nab0;
+    bool brute = nside > (uint32_t)(4 * kDL * kDW);
     uint32_t nq = 0u;  // wave-uniform list length
-    {
+    if (!brute) {
         const uint32_t ent0 = lds_addr(&sh.ent[w][0]), epos0 = lds_addr(&sh.epos[w][0]);
+        // lane k < kDN keeps chunk k's ballot and first list slot
+        uint32_t lm_lo = 0u, lm_hi = 0u, lb_l = 0u;
+        auto list_chunks = [&](auto&& pred) {
 #pragma unroll
-        for (int k = 0; k < kDN; ++k) {
-            uint64_t sk = 0ull;
-            if (k < Kw) {
-                const f4v x = xv[k];
-                sk = __ballot(kside ? (r_max4(x) >= xl_c) : (d_min4(x) <= xh_c));
-                if (sk) {
+            for (int k = 0; k < kDN; ++k) {
+                if (k < Kw) {
+                    const uint64_t sk = __ballot(pred(xv[k]));
                     const uint32_t s = min(nq + lane_rank(sk), (uint32_t)kDL - 1u);
-                    lds_put_x4_u16(sk, ent0 + 16 * s, x, epos0 + 2 * s, (uint32_t)(k * 64 + l));
+                    lds_put_x4_u16(sk, ent0 + 16 * s, xv[k], epos0 + 2 * s, (uint32_t)(k * 64 + l));
+                    if (l == k) {
+                        lm_lo = (uint32_t)sk;
+                        lm_hi = (uint32_t)(sk >> 32);
+                        lb_l = nq;
+                    }
+                    nq += (uint32_t)__popcll(sk);
                 }
             }
-            if (l == 0) {
-                sh.lmask[w][k] = sk;
-                sh.lbase[w][k] = nq;
-            }
-            nq += (uint32_t)__popcll(sk);
+        };
+        if (kside) list_chunks([&](const f4v& x) { return r_max4(x) >= xl_c; });
+        else list_chunks([&](const f4v& x) { return d_min4(x) <= xh_c; });
+        if (l < kDN) {
+            sh.lmask[w][l] = ((uint64_t)lm_hi << 32) | lm_lo;
+            sh.lbase[w][l] = lb_l;
         }
         if (l == 0 && nq > (uint32_t)kDL) atomicOr(&sh.over, 1u);
     }
     // ---- B4: lists complete ---------------------------------------------------
     lds_barrier();
     NIS_DTS(4);
-    const bool brute = sh.over != 0u;
+    brute = brute || sh.over != 0u;
 
     // ---- the cutoff bucket's members: refined while more than kDMem ----------
     // Every float4 holding a member of b_p is on the listed side (or, when a

@@ -89,9 +89,11 @@ constexpr double kS40 = 1099511627776.0;    // 2^40
 __device__ unsigned long long nis_sparse_ts[2048 * 256];
 #define NIS_TDECL                \
     uint32_t nis_tw_[8] = {};    \
+    uint32_t nis_tx_[4] = {};    \
     uint32_t nis_ts_[16] = {};
 #define NIS_STS(i) (nis_tw_[i] = (uint32_t)wall_clock64())
 #define NIS_STS1(j) (nis_ts_[j] = (uint32_t)wall_clock64())
+#define NIS_STX(i) (nis_tx_[i] = (uint32_t)wall_clock64())
 #define NIS_TFLUSH()                                                                        \
     do {                                                                                    \
         if (lane_id() == 0 && blockIdx.x < 2048) {                                          \
@@ -100,6 +102,8 @@ __device__ unsigned long long nis_sparse_ts[2048 * 256];
                 ts_[8 * wave_id() + i_] = nis_tw_[i_];                                      \
             _Pragma("unroll") for (int j_ = 0; j_ < 16; ++j_) if (nis_ts_[j_])             \
                 ts_[128 + j_] = nis_ts_[j_];                                                \
+            _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_) if (nis_tx_[i_])              \
+                ts_[144 + 4 * wave_id() + i_] = nis_tx_[i_];                                \
         }                                                                                   \
     } while (0)
 #else
@@ -109,6 +113,9 @@ __device__ unsigned long long nis_sparse_ts[2048 * 256];
     } while (0)
 #define NIS_STS1(j) \
     do {            \
+    } while (0)
+#define NIS_STX(i) \
+    do {           \
     } while (0)
 #define NIS_TFLUSH() \
     do {             \
@@ -908,6 +915,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         NIS_TFLUSH();
         return cut.reject;
     }
+    NIS_STX(0);
     if (w == 0 && l < 4) a.rng[4 * (int64_t)row + l] = rst;
     const int bp = cut.bp;
     const float M = cut.M, R = cut.R;
@@ -976,6 +984,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const double ssum = (double)isum;
         sh.seg[w][l] = ssum;
         const double tsum = wsum_f64(ssum);
+        NIS_STX(1);
         const uint32_t mcnt = (uint32_t)__popc(mb);
         const uint32_t mincl = wscan_u32(mcnt);
         const uint32_t mtot = (uint32_t)__builtin_amdgcn_readlane((int)mincl, 63);
@@ -996,6 +1005,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             }
         }
         if (l == 0) sh.tw[w] = tsum;
+        NIS_STX(2);
     }
     // ---- the last wave to finish its sums ranks the members and walks -------
     NIS_STS(6);
@@ -1003,6 +1013,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     uint32_t done2 = 0u;
     if (l == 0) done2 = atomicAdd(&sh.cnt2, 1u);
     done2 = bcast_u32(done2, 0);
+    NIS_STX(3);
     if (done2 != (uint32_t)(kSW - 1)) {
         NIS_TFLUSH();
         return NIS_REJECT_NONE;
