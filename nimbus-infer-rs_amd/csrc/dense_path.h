@@ -128,12 +128,11 @@ struct NucleusShared {
     unsigned long long ring[kDRing];  // [j & (kDRing - 1)]: count << 48 | sum of fm
     f4v ent[kDW][kDL];                // listed float4s of one side of the cutoff, per wave
     uint16_t epos[kDW][kDL];          //   chunk * 64 + lane
-    float ekept[kDW][kDL];            //   their kept mass (2^R_z units)
     RCand mem[kDMem];                 // members of the final bucket
     unsigned long long sub[64];       // refinement histogram of the cutoff bucket
     float walk[kDN][64];              // the chosen wave's per-float4 kept masses
-    unsigned long long lmask[kDW][kDN];  // chunk k's ballot of listed float4s
-    uint32_t lbase[kDW][kDN];         //   and its first list slot
+    float em4[kDW][kDN][64];          // each lane's float4 masses (2^R_z units), then
+                                      //   kept masses (listed rows, after the cutoff)
     DRec rec[kDW];
     unsigned long long wtm[kDW];      // search: each wave's bucket mass
     uint32_t wtc[kDW];                //   and count
@@ -294,7 +293,13 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // elements more than 64 octaves below the first reference share one bucket
     const float tflo = (Rw0 - (float)kDSpan) * 64.0f;
     float mx = -INFINITY;
-    double z = 0.0;  // the lane's mass total (2^R_z units); NaN if any element is NaN
+    // this lane's float4 masses go to sh.em4 chunk by chunk (2^R_z units):
+    // the walk and the kept sums take the same values; chunks before kfin
+    // were summed at an older reference and are summed again at the final
+    // one below; z is the lane's total of them
+    double z = 0.0;
+    int kfin = 0;
+    float* const em4w = &sh.em4[w][0][l];
     float czh = chi, czl = clo;
     asm volatile("" : "+v"(czh), "+v"(czl));
     float Rz = Rw0;
@@ -312,14 +317,19 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         if (__ballot(m4 * chi > Rz + 1.0f)) {
             const float Rn = ceilf(wmax_f32(mx) * chi);
             if (fabsf(Rn) < 1e30f) {
-                z = ldexp(z, (int)(Rz - Rn));
                 Rz = Rn;
+                kfin = k;
+                z = 0.0;
             }
         }
         const int Rs = (int)Rz + 24;
         const float e0 = r_mass(x.x, czh, czl, Rz), e1 = r_mass(x.y, czh, czl, Rz);
         const float e2 = r_mass(x.z, czh, czl, Rz), e3 = r_mass(x.w, czh, czl, Rz);
-        z += (double)((e0 + e1) + (e2 + e3));
+        {
+            const float s4 = (e0 + e1) + (e2 + e3);
+            em4w[64 * k] = s4;
+            z += (double)s4;
+        }
 #define NIS_DHIST(xq, eq)                                                                  \
         {                                                                                  \
             const int j_ = d_flr(d_vmax((xq) * chi64, tflo));                              \
@@ -336,6 +346,21 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     NIS_DTS(1);
     __builtin_amdgcn_s_setprio(0);
     mx = wmax_f32(mx);
+    // the masses of chunks summed before the reference last moved, again at
+    // the final reference (kfin is wave-uniform and usually 0); then the
+    // lane's total, NaN if any element is NaN
+    if (kfin > 0) {
+#pragma unroll
+        for (int k = 0; k < kDN; ++k) {
+            if (k < kfin) {
+                const f4v x = xv[k];
+                const float s4 = (r_mass(x.x, czh, czl, Rz) + r_mass(x.y, czh, czl, Rz)) +
+                                 (r_mass(x.z, czh, czl, Rz) + r_mass(x.w, czh, czl, Rz));
+                em4w[64 * k] = s4;
+                z += (double)s4;
+            }
+        }
+    }
     {
         const uint32_t nan_seen = (uint32_t)(__ballot(z != z) != 0ull);
         if (l == 0) sh.rec[w] = DRec{mx, Rz, Rw0, nan_seen | (Kw > 0 ? 2u : 0u)};
@@ -395,6 +420,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     }
     // ---- B2: the waves' bucket totals ---------------------------------------
     lds_barrier();
+    NIS_DTS(10);
     const unsigned long long wmi = rscan16_u64(rv ? sh.wtm[l] : 0ull);
     const uint32_t wci = rscan_u32(rv ? sh.wtc[l] : 0u);
     const unsigned long long Z = rbcast_u64(wmi, kDW - 1);  // 2^(R - 44) units
@@ -453,8 +479,6 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     uint32_t nq = 0u;  // wave-uniform list length
     if (!brute) {
         const uint32_t ent0 = lds_addr(&sh.ent[w][0]), epos0 = lds_addr(&sh.epos[w][0]);
-        // lane k < kDN keeps chunk k's ballot and first list slot
-        uint32_t lm_lo = 0u, lm_hi = 0u, lb_l = 0u;
         auto list_chunks = [&](auto&& pred) {
 #pragma unroll
             for (int k = 0; k < kDN; ++k) {
@@ -462,21 +486,12 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                     const uint64_t sk = __ballot(pred(xv[k]));
                     const uint32_t s = min(nq + lane_rank(sk), (uint32_t)kDL - 1u);
                     lds_put_x4_u16(sk, ent0 + 16 * s, xv[k], epos0 + 2 * s, (uint32_t)(k * 64 + l));
-                    if (l == k) {
-                        lm_lo = (uint32_t)sk;
-                        lm_hi = (uint32_t)(sk >> 32);
-                        lb_l = nq;
-                    }
                     nq += (uint32_t)__popcll(sk);
                 }
             }
         };
         if (kside) list_chunks([&](const f4v& x) { return r_max4(x) >= xl_c; });
         else list_chunks([&](const f4v& x) { return d_min4(x) <= xh_c; });
-        if (l < kDN) {
-            sh.lmask[w][l] = ((uint64_t)lm_hi << 32) | lm_lo;
-            sh.lbase[w][l] = lb_l;
-        }
         if (l == 0 && nq > (uint32_t)kDL) atomicOr(&sh.over, 1u);
     }
     // ---- B4: lists complete ---------------------------------------------------
@@ -575,6 +590,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         }
         chiL = chiS;
     }
+    NIS_DTS(11);
     // members of the final bucket B (at most kDMem) into sh.mem
     if (!all_out && ns > 0u) {
         const int o = B >> (6 * (lv + 1));
@@ -664,25 +680,40 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         return (k4[0] + k4[1]) + (k4[2] + k4[3]);
     };
     double tws = 0.0;  // this lane's part of the wave's kept mass (2^R_z units)
+    float kvb[kDN];    // brute: this lane's float4 kept masses
+#pragma unroll
+    for (int k = 0; k < kDN; ++k) kvb[k] = 0.0f;
     if (!brute) {
+        // The parked float4 masses ([chunk][lane] of this wave) become kept
+        // masses: a listed float4 takes its own; off the list every float4 is
+        // kept whole (listed removed side) or removed (listed kept side).
+        float* const esw = &sh.em4[w][0][0];
+        if (kside) {
+#pragma unroll
+            for (int k = 0; k < kDN; ++k) esw[64 * k + l] = 0.0f;
+            lds_wave_fence();
+        }
 #pragma unroll
         for (int r = 0; r < kDL / 64; ++r) {
             if (64 * r < ne) {
                 const int je = 64 * r + l;
                 const bool valid = je < ne;
                 float orig;
-                const float ks = kept4(sh.ent[w][je], (uint32_t)(4 * (wbase + (int)sh.epos[w][je]) - mis), orig);
-                if (valid) sh.ekept[w][je] = ks;
+                const int ep = (int)sh.epos[w][min(je, kDL - 1)];
+                const float ks = kept4(sh.ent[w][min(je, kDL - 1)], (uint32_t)(4 * (wbase + ep) - mis), orig);
+                if (valid) esw[ep] = ks;
                 tws += valid ? (kside ? (double)ks : (double)ks - (double)orig) : 0.0;
             }
         }
         if (!kside) tws += z;  // every float4 off the list is kept whole
     } else {
+        // (kept in registers: the chosen wave's walk takes them as they are)
 #pragma unroll
         for (int k = 0; k < kDN; ++k) {
             if (k < Kw) {
                 float orig;
-                tws += (double)kept4(xv[k], (uint32_t)NIS_RIDXD(k), orig);
+                kvb[k] = kept4(xv[k], (uint32_t)NIS_RIDXD(k), orig);
+                tws += (double)kvb[k];
             }
         }
     }
@@ -712,32 +743,19 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     const double rw_ = ldexp(r - bcast_f64(Tincl - T, ws), (int)(R - Rz));
     // this lane's per-float4 kept masses (2^R_z units), transposed into chunk
     // totals
-    bool lst[kDN];
+    // this lane's float4 kept masses: in registers (brute), else the parked
+    // array the kept sums left behind (one read each, all issued together)
     float kv[kDN];
-    uint64_t lmk[kDN];
-    uint32_t lbk[kDN];
+    {
+        const float* const esw = &sh.em4[w][0][l];
 #pragma unroll
-    for (int k = 0; k < kDN; ++k) {
-        lmk[k] = sh.lmask[w][k];
-        lbk[k] = sh.lbase[w][k];
+        for (int k = 0; k < kDN; ++k) kv[k] = esw[64 * k];
+#pragma unroll
+        for (int k = 0; k < kDN; ++k) kv[k] = brute ? kvb[k] : ((k < Kw) ? kv[k] : 0.0f);
     }
 #pragma unroll
-    for (int k = 0; k < kDN; ++k) {
-        const uint64_t mk = brute ? ~0ull : lmk[k];
-        lst[k] = (mk >> l) & 1ull;
-        float v = 0.0f;
-        if (k < Kw) {
-            float all;
-            if (brute) v = kept4(xv[k], (uint32_t)NIS_RIDXD(k), all);
-            else if (lst[k]) v = sh.ekept[w][min(lbk[k] + lane_rank(mk), (uint32_t)kDL - 1u)];
-            else if (!kside) {
-                kept4(xv[k], (uint32_t)NIS_RIDXD(k), all);
-                v = all;
-            }
-        }
-        kv[k] = v;
-        sh.walk[k][l] = v;
-    }
+    for (int k = 0; k < kDN; ++k) sh.walk[k][l] = kv[k];
+    NIS_DTS(14);
     lds_wave_fence();
     // lane j < 4 kDN: quarter j & 3 of chunk j >> 2
     double qs = 0.0;
@@ -765,17 +783,16 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     const uint64_t hk = __ballot((l < 16) & (cks > 0.0) & (cincl >= rw_));
     const uint64_t nzk = __ballot((l < 16) & (cks > 0.0));
     const int kc = hk ? (__ffsll((long long)hk) - 1) : (63 - __clzll((long long)(nzk | 1ull)));
+    NIS_DTS(15);
     const double rk_ = rw_ - bcast_f64(cincl - cks, kc);
     // the lanes of chunk kc in index order
     f4v xc = xv[0];
     float sc = kv[0];
-    bool lc_l = lst[0];
 #pragma unroll
     for (int k = 1; k < kDN; ++k)
         if (k == kc) {
             xc = xv[k];
             sc = kv[k];
-            lc_l = lst[k];
         }
     const double sl = (double)sc;
     const double lincl = wscan_f64(sl);
@@ -792,7 +809,8 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             const float xq = elem(xc, q);
             // the same masses the float4's kept total was summed from
             const float eq = r_mass(xq, czh, czl, Rz);
-            ev[q] = lc_l ? (d_kept(xq, ib + (uint32_t)q, chiL, Bf, kcut) ? eq : 0.0f) : eq;
+            // (a float4 kept whole passes every test: its elements lie above b_p)
+            ev[q] = d_kept(xq, ib + (uint32_t)q, chiL, Bf, kcut) ? eq : 0.0f;
         }
         int q = -1, qlast = 0;
 #pragma unroll
