@@ -129,6 +129,8 @@ struct NucleusShared {
     f4v ent[kDW][kDL];                // listed float4s of one side of the cutoff, per wave
     uint16_t epos[kDW][kDL];          //   chunk * 64 + lane
     RCand mem[kDMem];                 // members of the final bucket
+    unsigned long long mkey[kDMem];   //   their stable-order keys (ranking)
+    unsigned long long mmass[kDMem];  //   and masses (2^(R - 44) units)
     unsigned long long sub[64];       // refinement histogram of the cutoff bucket
     float walk[kDN][64];              // the chosen wave's per-float4 kept masses
     float em4[kDW][kDN][64];          // each lane's float4 masses (2^R_z units), then
@@ -633,13 +635,26 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             const RCand mr = sh.mem[min(l, kDMem - 1)];
             const unsigned long long Km = valid ? r_key(mr.x, mr.idx) : 0ull;
             const unsigned long long em = valid ? d_u44(mr.fm, mr.b, Ri) : 0ull;
+            // every lane compares its key with all of them, read back from LDS
+            // (same address in every lane; eight reads in flight per step)
+            sh.mkey[l] = Km;
+            sh.mmass[l] = em;
+            lds_wave_fence();
             unsigned long long pre = 0ull;  // mass of the members ahead of this one
             uint32_t rk = 0u;
-            for (int j = 0; j < n; ++j) {
-                const unsigned long long Kj = rbcast_u64(Km, j);
-                const unsigned long long ej = rbcast_u64(em, j);
-                pre += (Kj > Km) ? ej : 0ull;
-                rk += (Kj > Km) ? 1u : 0u;
+            for (int j0 = 0; j0 < n; j0 += 8) {
+                unsigned long long kj[8], ej[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    kj[jj] = sh.mkey[min(j0 + jj, kDMem - 1)];
+                    ej[jj] = sh.mmass[min(j0 + jj, kDMem - 1)];
+                }
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const bool ahead = (j0 + jj < n) & (kj[jj] > Km);
+                    pre += ahead ? ej[jj] : 0ull;
+                    rk += ahead ? 1u : 0u;
+                }
             }
             // sampler.rs:150 in rank order: D = G + pre - e; the kept ones are
             // the longest prefix of ranks with D <= p Z
@@ -668,13 +683,24 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // ---- kept masses: this wave's listed float4s, or all of its float4s -----
     // kept mass of float4 x4 (elements 0..3 at row index i0) and its stream
     // mass, from the same per-element masses the stream summed
+    // (the stable-order key is compared only in a chunk holding an element
+    // of the final bucket: at most kDMem of them in the row)
     auto kept4 = [&](const f4v& x4, uint32_t i0, float& all) {
         float e[4], k4[4];
+        int F[4];
+        bool inb = false;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float x = elem(x4, q);
             e[q] = r_mass(x, czh, czl, Rz);
-            k4[q] = d_kept(x, i0 + (uint32_t)q, chiL, Bf, kcut) ? e[q] : 0.0f;
+            F[q] = d_flr(x * chiL);
+            k4[q] = (F[q] > Bf) ? e[q] : 0.0f;
+            inb |= F[q] == Bf;
+        }
+        if (__ballot(inb)) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if ((F[q] == Bf) && (r_key(elem(x4, q), i0 + (uint32_t)q) >= kcut)) k4[q] = e[q];
         }
         all = (e[0] + e[1]) + (e[2] + e[3]);
         return (k4[0] + k4[1]) + (k4[2] + k4[3]);
