@@ -474,10 +474,12 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         xl_c = vl - fabsf(vl) * 1.0e-6f - 1.0e-30f;
         xh_c = vh + fabsf(vh) * 1.0e-6f + 1.0e-30f;
     }
-    // A side with more elements than the lists hold float4s (four elements
-    // each) cannot fit: such a row skips the listing and works in registers.
+    // A side with more elements than the lists have slots rarely fits (its
+    // elements would have to share float4s; on c2's rows with 2-8 k of them
+    // the busiest wave needs 170-400 slots of 128): such a row skips the
+    // listing and works in registers.
     const uint32_t nside = kside ? nab0 + nsel0 : (uint32_t)V - nab0;
-    bool brute = nside > (uint32_t)(4 * kDL * kDW);
+    bool brute = nside > (uint32_t)(kDL * kDW);
     uint32_t nq = 0u;  // wave-uniform list length
     if (!brute) {
         const uint32_t ent0 = lds_addr(&sh.ent[w][0]), epos0 = lds_addr(&sh.epos[w][0]);

@@ -697,6 +697,34 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     mx = wmax_f32(mx);
     z = wsum_f64(z);
     NIS_STS(4);
+    // the wave's record, its keys and (wave 0) the row's draw go out before
+    // its histogram rounds, so that they overlap them
+    {
+        const uint64_t zb = (uint64_t)__double_as_longlong(z);
+        const uint32_t ra = lds_addr(&sh.rec[w]);
+        lds_put_b128_m(1ull, ra, u4v{(uint32_t)zb, (uint32_t)(zb >> 32), __float_as_uint(mx),
+                                     __float_as_uint(Rw)});
+        lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, nsw, 0u});
+    }
+    // the row's one draw (sampler.rs:209), made by wave 0 off the critical
+    // path; wave 0 stores the advanced state once the row cannot be declined
+    uint64_t rst = 0;  // wave 0, lane j < 4: word j of the advanced state
+    if (w == 0) {
+        uint64_t st[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
+        const double u0 = rng_next_f64(st);
+        if (l == 0) sh.u0 = u0;
+        rst = (l == 0) ? st[0] : (l == 1) ? st[1] : (l == 2) ? st[2] : st[3];
+    }
+    if (l == 0) {
+        const float thr = Kw > 0 ? thc : -INFINITY;
+        atomicMax(&sh.kmax, key32(mx));
+        if (nw > 0u || nsc > 0u) atomicMin(&sh.kthmin, key32(thr));
+        if (mx > -INFINITY) atomicMin(&sh.krwmin, key32(Rw));
+        atomicMax(&sh.nmax, nw);
+    }
     // every element of the wave's entries at or above thl (raised to the
     // thresholds published meanwhile) is a candidate; lane l holds entries
     // [l sg, l sg + sg).  The candidates join the shared histograms (bucket:
@@ -749,32 +777,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         }
     }
     NIS_STS(7);
-    {
-        const uint64_t zb = (uint64_t)__double_as_longlong(z);
-        const uint32_t ra = lds_addr(&sh.rec[w]);
-        lds_put_b128_m(1ull, ra, u4v{(uint32_t)zb, (uint32_t)(zb >> 32), __float_as_uint(mx),
-                                     __float_as_uint(Rw)});
-        lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, nsw, 0u});
-    }
-    // the row's one draw (sampler.rs:209), made by wave 0 off the critical
-    // path; wave 0 stores the advanced state once the row cannot be declined
-    uint64_t rst = 0;  // wave 0, lane j < 4: word j of the advanced state
-    if (w == 0) {
-        uint64_t st[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            st[j] = ((uint64_t)bcast_u32((uint32_t)(rsv >> 32), j) << 32) | bcast_u32((uint32_t)rsv, j);
-        const double u0 = rng_next_f64(st);
-        if (l == 0) sh.u0 = u0;
-        rst = (l == 0) ? st[0] : (l == 1) ? st[1] : (l == 2) ? st[2] : st[3];
-    }
-    if (l == 0) {
-        const float thr = Kw > 0 ? thc : -INFINITY;
-        atomicMax(&sh.kmax, key32(mx));
-        if (nw > 0u || nsc > 0u) atomicMin(&sh.kthmin, key32(thr));
-        if (mx > -INFINITY) atomicMin(&sh.krwmin, key32(Rw));
-        atomicMax(&sh.nmax, nw);
-    }
     NIS_STS(2);
 
     // ---- B1: every wave's candidates are in the histograms; wave 0 searches
