@@ -135,7 +135,9 @@ struct NucleusShared {
     float walk[kDN][64];              // the chosen wave's per-float4 kept masses
     float em4[kDW][kDN][64];          // each lane's float4 masses (2^R_z units), then
                                       //   kept masses (listed rows, after the cutoff)
-    DRec rec[kDW];
+    uint32_t kmax;                    // the waves' maxima, reduced as they arrive (key32)
+    uint32_t krw0;                    //   their first references (min, key32)
+    uint32_t fnan;                    //   a NaN seen
     unsigned long long wtm[kDW];      // search: each wave's bucket mass
     uint32_t wtc[kDW];                //   and count
     DCand cand[kDW];
@@ -242,6 +244,9 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     if (tid == 0) {
         sh.nmem = 0u;
         sh.over = 0u;
+        sh.kmax = 0u;
+        sh.krw0 = 0xFFFFFFFFu;
+        sh.fnan = 0u;
     }
     lds_barrier();
     const int voff = 16 * slot0;  // (chunks past the first never hold slot 0)
@@ -364,8 +369,14 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         }
     }
     {
-        const uint32_t nan_seen = (uint32_t)(__ballot(z != z) != 0ull);
-        if (l == 0) sh.rec[w] = DRec{mx, Rz, Rw0, nan_seen | (Kw > 0 ? 2u : 0u)};
+        const bool nan_seen = __ballot(z != z) != 0ull;
+        if (l == 0) {
+            if (Kw > 0) {
+                atomicMax(&sh.kmax, key32(mx == mx ? mx : -INFINITY));
+                atomicMin(&sh.krw0, key32(Rw0));
+            }
+            if (nan_seen) atomicOr(&sh.fnan, 1u);
+        }
     }
     // the row's one draw (sampler.rs:209), made by wave 0; the advanced state
     // is stored once the row cannot be declined any more
@@ -383,14 +394,12 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     lds_barrier();
     NIS_DTS(2);
     const bool rv = l < kDW;
-    const DRec rr = sh.rec[rv ? l : 0];
-    const bool has = rv && (rr.flags & 2u);
-    const float M = wmax_f32(has ? rr.mx : -INFINITY);
+    const float M = unkey32(sh.kmax);  // (NaN when no wave holds data: declined below)
     const float R = (M > -INFINITY && fabsf(M * chi) < 1e30f) ? ceilf(M * chi) : 0.0f;
     const int Ri = (int)R;
     {
-        const bool anynan = __ballot(rv && (rr.flags & 1u)) != 0ull;
-        const float rw0min = -wmax_f32(has ? -rr.rw0 : -INFINITY);
+        const bool anynan = sh.fnan != 0u;
+        const float rw0min = unkey32(sh.krw0);
         // |M c| < 4096 keeps the finest bucket index floor(64^3 x c) in range
         const bool ok = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
                         (R - rw0min < (float)kDSpan);
