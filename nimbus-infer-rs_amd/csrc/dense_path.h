@@ -3,10 +3,11 @@
 // (V <= 53245), for 0 < top_p < 1, T > 0, no top-k and no penalty history
 // (src/sampler.rs:118-160, 183-216).
 //
-// Layout and stream.  As in the resident path: wave w owns 64-slot chunks
-// [cpw w, cpw (w + 1)) of the row's float4 slots, lane l of chunk k holds
-// slot 64 (cpw w + k) + l, and every lane keeps kDD loads in flight ahead of
-// the chunk it works on.  As a chunk lands each lane computes its four
+// Layout and stream.  Wave w owns a contiguous run of Kw 64-slot chunks of
+// the row's float4 slots (the chunks split as evenly as they go over the
+// waves), lane l of chunk k holds slot wbase + 64 k + l, and every lane
+// keeps kDD loads in flight ahead of the chunk it works on.  As a chunk
+// lands each lane computes its four
 // masses e = 2^(x c - R_z) (c = log2(e) / T split as c_hi + c_lo, R_z the
 // wave's integer reference, raised with its running max so that the masses
 // near the max have small arguments) into the wave's f64 total, and adds
@@ -212,9 +213,13 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     const int f_lo = mis ? 1 : 0;          // first float4 slot lying fully inside the row
     const int f_hi = (V + mis - 4) >> 2;   // last one
     const int nsl = (V + mis + 3) >> 2;    // slots touching the row
-    const int cpw = (((nsl + 63) >> 6) + kDW - 1) / kDW;  // chunks per wave
-    const int wbase = 64 * cpw * w;
-    const int Kw = min(max((nsl - wbase + 63) >> 6, 0), cpw);
+    // the row's chunks split as evenly as they go: every wave nch / kDW of
+    // them, the first nch % kDW waves one more (the stream is bound by VALU
+    // issue, so each SIMD's share of chunks sets its length)
+    const int nch = (nsl + 63) >> 6;
+    const int cb = nch / kDW, cr = nch % kDW;
+    const int Kw = cb + (w < cr ? 1 : 0);  // <= kDN: V <= kDMaxV
+    const int wbase = 64 * (cb * w + min(w, cr));
     const int slot0 = wbase + l;
     // row index of element 0 of chunk k of this lane
 #define NIS_RIDXD(k) (4 * (slot0 + 64 * (k)) - mis)
