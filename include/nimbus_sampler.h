@@ -73,13 +73,12 @@ typedef struct nis_row_stats {
     uint64_t kept;  /* tokens surviving top-k / top-p */
     uint32_t path;  /* NIS_PATH_* */
     uint32_t token;
-    uint32_t kernel;/* 1 = register-resident fast path, 2 = general path */
-    uint32_t reject;/* NIS_REJECT_*: kernel 2 -> why the fast path handed the row on;
-                       kernel 1 -> why its sparse top-p route declined (the
-                       register-resident dense route then produced it); 0 if not */
+    uint32_t kernel;/* 1 = a row kernel (sparse, dense, resident, long-row), 2 = general path */
+    uint32_t reject;/* NIS_REJECT_*: kernel 2 -> why the row kernel handed the row on
+                       (SHAPE: no row kernel takes it); 0 if not */
 } nis_row_stats;
 
-/* nis_row_stats.reject: the fast path declines a row it cannot prove exact
+/* nis_row_stats.reject: a row kernel declines a row it cannot prove exact
  * and the general path recomputes it; the result is the same either way. */
 #define NIS_REJECT_NONE 0
 #define NIS_REJECT_SHAPE 1      /* V out of range, per-row penalty, top-k, top-p <= 0 */

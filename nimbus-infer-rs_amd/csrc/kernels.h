@@ -7,27 +7,14 @@
 
 namespace nis {
 
-// One workgroup per row: the register-resident fast path when the row fits
-// it, the general path otherwise (or when the fast path declines the row).
+// One 512-lane workgroup per row on the general path: the launches no
+// row kernel takes (top-k, V < 256, top-p <= 0, a penalty history on rows
+// longer than the registers hold).
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(RowArgs a) {
-    __shared__ union {
-        GeneralShared g;
-        FastShared f;
-    } sh;
+    __shared__ GeneralShared sh;
     const int row = (int)blockIdx.x;
     if (a.done != nullptr && a.done[row]) return;  // a finished sequence (decode step)
-    // every argument the fast path reads before its first load, fetched in
-    // one batch of scalar loads instead of a chain of them behind the
-    // eligibility tests
-    asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
-                 "s"(a.penalty), "s"(a.top_k), "s"(a.gen_ids), "s"(a.gen_off));
-    uint32_t reject = NIS_REJECT_SHAPE;
-    if (fast_eligible(a, row)) {
-        reject = fast_row(a, row, sh.f);
-        if (reject == NIS_REJECT_NONE) return;
-        __syncthreads();
-    }
-    general_row(a, row, sh.g, reject);
+    general_row(a, row, sh, NIS_REJECT_SHAPE);
 }
 
 // Sparse top-p rows: one 1024-lane workgroup per row.  A row the sparse

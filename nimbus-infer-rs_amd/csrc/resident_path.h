@@ -29,7 +29,7 @@
 // wide for f32 masses) returns a reject code before anything is written, and
 // the caller runs the general path on it.
 #pragma once
-#include "fast_path.h"
+#include "row_common.h"
 #include "penalty_bits.h"
 
 namespace nis {

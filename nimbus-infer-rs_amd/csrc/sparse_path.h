@@ -53,7 +53,7 @@
 // the 64 lanes of one add round, whose candidates crowd into a few octaves,
 // hit up to 8 times as many addresses.
 #pragma once
-#include "fast_path.h"
+#include "row_common.h"
 #include "penalty_bits.h"
 
 namespace nis {

@@ -365,9 +365,9 @@ def test_invalid_arguments_are_rejected(sampler):
 def test_penalty_launch_rows_take_the_register_kernels(sampler):
     # A top-p < 0.95 or top-p-off penalty launch runs the sparse or resident
     # kernel with the penalty applied in registers: every row stays on it
-    # (kernel == 1, reject 0).  At top-p 0.99 it runs the 512-lane kernel,
-    # whose routes may take the rows without a history; rows with a history
-    # run the general path there (kernel == 2).
+    # (kernel == 1, reject 0).  At top-p 0.99 it runs the dense kernel: the
+    # rows without a history stay on it, the rows with one run the general
+    # path inside it (kernel == 2).
     from nimbus_sampler import workloads
     B, V = 32, 50257
     rnd = np.random.Generator(np.random.PCG64(31))
@@ -387,3 +387,5 @@ def test_penalty_launch_rows_take_the_register_kernels(sampler):
             assert (st["kernel"] == 1).all() and (st["reject"] == 0).all(), st["reject"]
         else:
             assert (st["kernel"][~empty] == 2).all(), st["kernel"]
+            assert (st["kernel"][empty] == 1).all() and (st["reject"][empty] == 0).all(), \
+                (st["kernel"], st["reject"])
