@@ -152,8 +152,8 @@ nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_pa
 //   - greedy (T <= 0), 256 <= V <= 53245: the resident kernel's argmax;
 //   - top-p off (>= 1), no top-k: the resident kernel's all-kept walk;
 //   - 0.95 <= top-p < 1, no top-k: the 1024-lane dense kernel (a nucleus of
-//     any size: one exact histogram of the whole row built in the stream;
-//     with a penalty launch, the rows without a history);
+//     any size: one exact histogram of the whole row built in the stream),
+//     or its penalty variant for a launch with a penalty history;
 //   - 0 < top-p < 0.95, no top-k: the 1024-lane sparse kernel (few kept
 //     tokens, listed against a sampled threshold);
 //   - V > 53245 (rows longer than the registers hold), no top-k: the
@@ -162,8 +162,9 @@ nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_pa
 //     it declined;
 //   - anything else (top-k, V < 256, top-p <= 0, a penalty history on rows
 //     longer than the registers hold): the 512-lane general kernel.
-// A row with a repetition-penalty history, or one a kernel cannot prove,
-// runs the general path inside whichever kernel was launched.
+// A row one of these kernels cannot prove (non-finite values, capacity,
+// exact-tie overflow, a history past the bitmaps) runs the general path
+// inside whichever kernel was launched.
 int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
     const bool res_shape = a.V >= 256 && a.V <= nis::kRMaxV;
     const bool no_topk = a.top_k == 0 || a.top_k >= (uint64_t)a.V;
@@ -182,9 +183,12 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
             hipLaunchKernelGGL(nis::sample_rows_resident_kernel<nis::kResAll>, dim3((unsigned)B),
                                dim3(nis::kRB), 0, ctx->stream, a);
     } else if (res_shape && a.temperature > 0.0f && no_topk && a.top_p >= 0.95f && a.top_p < 1.0f) {
-        // (a row with a penalty history runs the general path inside it)
-        hipLaunchKernelGGL(nis::sample_rows_dense_kernel, dim3((unsigned)B), dim3(nis::kDB), 0,
-                           ctx->stream, a);
+        if (a.penalty != 1.0f && a.gen_ids != nullptr)  // the penalty applied in registers
+            hipLaunchKernelGGL(nis::sample_rows_dense_pen_kernel, dim3((unsigned)B), dim3(nis::kDB), 0,
+                               ctx->stream, a);
+        else
+            hipLaunchKernelGGL(nis::sample_rows_dense_kernel, dim3((unsigned)B), dim3(nis::kDB), 0,
+                               ctx->stream, a);
     } else if (a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f && a.top_p > 0.0f &&
                a.top_p < 0.95f && no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)) {
         hipLaunchKernelGGL(nis::sample_rows_sparse_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,

@@ -1,7 +1,8 @@
 // dense_path.h — top-p rows whatever the size of their nucleus: one row per
 // 1024-lane workgroup (16 wave64s, four per SIMD), the row held in VGPRs
-// (V <= 53245), for 0 < top_p < 1, T > 0, no top-k and no penalty history
-// (src/sampler.rs:118-160, 183-216).
+// (V <= 53245), for 0 < top_p < 1, T > 0 and no top-k (src/sampler.rs:118-160,
+// 183-216); the PEN form also applies a repetition-penalty history
+// (sampler.rs:83-101, described at the end of this comment).
 //
 // Layout and stream.  Wave w owns a contiguous run of Kw 64-slot chunks of
 // the row's float4 slots (the chunks split as evenly as they go over the
@@ -53,11 +54,29 @@
 // those per-float4 kept masses, and the drawn token's probability uses its
 // mass computed in f64.
 //
+// PEN: the history's ids go into LDS bitmaps before the stream (as for the
+// sparse kernel), so each wave holds one bit per chunk (pany) and each lane a
+// 4-bit mask per chunk of its own slot's penalised elements (pnl).  A
+// penalised element keeps its logit x in registers, but every register pass
+// skips it: the stream works on a copy of a flagged chunk with -inf in its
+// place, and the later passes test the mask.  After each pass, each lane
+// visits its own penalised elements one by one (few per lane; each_pen) with
+// y = pen(x) in f64: the mass 2^(y c - R_z) from the f64 argument, the bucket
+// functions floor(64^L T(y)) with T(v) = (float)(v c_hi) (for an f32 logit
+// T(x) = f32(x c_hi), so one monotone function orders plain and penalised
+// values alike), the max (y rounded up bounds every bucket, and moves the
+// wave's reference when it must; the exact f64 max serves the statistics),
+// the members, ranked on (key64(value), index) pairs, and the kept masses,
+// added to their float4s' entries.  Every float4 holding a penalised
+// element is listed on either side of the cutoff, so the unlisted float4s
+// are plain.
+//
 // Any row this path cannot prove returns a reject code before anything is
 // written, and the caller runs the general path on it.
 #pragma once
 #include "resident_path.h"
 #include "sparse_path.h"
+#include "penalty_bits.h"
 
 namespace nis {
 
@@ -123,15 +142,25 @@ struct alignas(16) DCut {
     uint32_t nkept;           // kept members
     uint32_t nsel;            // its members
     uint32_t rej;
+    uint32_t kidx;            // PEN: row index of the last kept member (kcut: key64 of its value)
+};
+// The listed float4s of one side of the cutoff; PEN reuses the space for the
+// history bitmaps, which are read before the stream.
+struct DList {
+    f4v ent[kDW][kDL];        // listed float4s, per wave
+    uint16_t epos[kDW][kDL];  //   chunk * 64 + lane | PEN: penalised-element mask << 12
 };
 
 struct NucleusShared {
     unsigned long long ring[kDRing];  // [j & (kDRing - 1)]: count << 48 | sum of fm
-    f4v ent[kDW][kDL];                // listed float4s of one side of the cutoff, per wave
-    uint16_t epos[kDW][kDL];          //   chunk * 64 + lane
-    RCand mem[kDMem];                 // members of the final bucket
-    unsigned long long mkey[kDMem];   //   their stable-order keys (ranking)
+    union {
+        DList l;                      // one side of the cutoff
+        PenBits pb;                   // PEN: the history (set-up only)
+    } u;
+    RCand mem[kDMem];                 // members of the final bucket (PEN: idx bit 31 = penalised)
+    unsigned long long mkey[kDMem];   //   their stable-order keys (ranking; PEN: key64 of the value)
     unsigned long long mmass[kDMem];  //   and masses (2^(R - 44) units)
+    uint32_t midx[kDMem];             //   PEN: their row indices
     unsigned long long sub[64];       // refinement histogram of the cutoff bucket
     float walk[kDN][64];              // the chosen wave's per-float4 kept masses
     float em4[kDW][kDN][64];          // each lane's float4 masses (2^R_z units), then
@@ -139,6 +168,10 @@ struct NucleusShared {
     uint32_t kmax;                    // the waves' maxima, reduced as they arrive (key32)
     uint32_t krw0;                    //   their first references (min, key32)
     uint32_t fnan;                    //   a NaN seen
+    uint32_t kpl;                     // PEN: the plain elements' max (key32; kmax also
+                                      //   holds the penalised values rounded up)
+    unsigned long long kymax;         // PEN: the penalised values' exact max (key64)
+    uint32_t pover;                   // PEN: the history is longer than the bitmaps take
     unsigned long long wtm[kDW];      // search: each wave's bucket mass
     uint32_t wtc[kDW];                //   and count
     DCand cand[kDW];
@@ -149,10 +182,13 @@ struct NucleusShared {
     uint32_t over;                    // a wave's side list overflowed
 };
 
+// PEN: the row may carry a penalty history (its length is checked inside).
+template <bool PEN>
 __device__ __forceinline__ bool dense_eligible(const RowArgs a, int row) {
     if (a.V < 256 || a.V > kDMaxV) return false;
     if (!(a.temperature > 0.0f) || !(a.top_p > 0.0f) || !(a.top_p < 1.0f)) return false;
     if (a.top_k > 0 && a.top_k < (uint64_t)a.V) return false;
+    if (PEN) return true;
     int64_t g0 = 0, g1 = 0;
     if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) return false;
     return true;
@@ -199,9 +235,30 @@ __device__ __forceinline__ bool d_kept(float x, uint32_t idx, float chiL, int B,
     const int F = d_flr(x * chiL);
     return (F > B) | ((F == B) & (r_key(x, idx) >= kcut));
 }
+// PEN: a float4 with its penalised elements (bits of nb) set to -inf
+__device__ __forceinline__ f4v d_mask4(const f4v& x, uint32_t nb) {
+    return f4v{(nb & 1u) ? -INFINITY : x.x, (nb & 2u) ? -INFINITY : x.y, (nb & 4u) ? -INFINITY : x.z,
+               (nb & 8u) ? -INFINITY : x.w};
+}
+// T(y) = (float)(y c_hi) of a penalised value: the f32 rounding of its f64
+// product, as f32(x c_hi) is for a logit (whose product is exact in f64).
+__device__ __forceinline__ float d_pt(double y, double chid) { return (float)(y * chid); }
+// Octave-relative fixed-point mass of a penalised value in octave o, as r_fm
+// for a logit: 2^(y c - o) * 2^24 rounded down (yc = y c in f64).
+__device__ __forceinline__ uint32_t d_pfm(double yc, int o) {
+    return (uint32_t)(__builtin_amdgcn_exp2f((float)(yc - (double)o)) * 16777216.0f);
+}
+// PEN: the stable order on f64 values: (key64(v), row index) pairs, larger
+// first; kept(v, i) <=> key > kcut or (key == kcut and i <= kidx).
+__device__ __forceinline__ bool d_pkeep(unsigned long long kv, uint32_t idx, unsigned long long kcut,
+                                        uint32_t kidx) {
+    return (kv > kcut) | ((kv == kcut) & (idx <= kidx));
+}
+
 // Returns NIS_REJECT_NONE when the row is done, else (uniformly across the
 // workgroup) why the general path must recompute it; nothing has been
 // written then.
+template <bool PEN>
 __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, NucleusShared& sh) {
     const int l = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -240,6 +297,13 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // until the CU has issued them all, which it does only as data arrives.
     xv[0] = nis_buffer_load_f4(rsrc, (Kw > 0) ? 16 * max(slot0, f_lo) : 0x7FFFFFF0, 0, 2);
     __builtin_amdgcn_sched_barrier(0);
+    // PEN: the raw history ids (behind chunk 0), and the bitmaps cleared
+    uint32_t hid[kPHist / kPB];
+    if constexpr (PEN) {
+        const bool hlong = pen_load_ids(a, row, tid, hid);  // too long: the row is declined
+        pen_clear(sh.u.pb, tid);
+        if (tid == 0) sh.pover = hlong ? 1u : 0u;
+    }
     {
         u4v* const rp = reinterpret_cast<u4v*>(&sh.ring[(kDRing / kDB) * tid]);
 #pragma unroll
@@ -252,6 +316,10 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         sh.kmax = 0u;
         sh.krw0 = 0xFFFFFFFFu;
         sh.fnan = 0u;
+        if (PEN) {
+            sh.kpl = 0u;
+            sh.kymax = 0ull;
+        }
     }
     lds_barrier();
     const int voff = 16 * slot0;  // (chunks past the first never hold slot 0)
@@ -268,6 +336,16 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     typedef const __attribute__((address_space(1))) uint64_t* gu64p;
     uint64_t rsv = 0;
     if (w == 0) rsv = ((gu64p)(a.rng + 4 * (int64_t)row))[l & 3];
+    // PEN: the bitmaps, then bit k of pany: chunk k of this wave has a slot
+    // holding a penalised element, and bits 4k..4k+3 of pnl: which elements
+    // of this lane's slot in chunk k are penalised
+    uint32_t pany = 0u;
+    uint64_t pnl = 0ull;
+    if constexpr (PEN) {
+        pen_set_bits(sh.u.pb, hid, V, mis);
+        lds_barrier();
+        pen_masks<kDN>(sh.u.pb, wbase, Kw, l, pany, pnl);
+    }
     // the CU serves the waves' loads in wave order: later waves run at a
     // higher priority until their stream ends
     __builtin_amdgcn_s_setprio(0);
@@ -297,14 +375,19 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     const float clo = (float)(c64 - (double)chi);
     const float chi64 = chi * 64.0f;  // exact: bucket j = floor(x * chi64) = floor(64 f32(x c_hi))
     const float p = a.top_p;
+    const double pen = (double)a.penalty;
+    const double chid = (double)chi;
 
     // ---- stream: chunk masses, max, and every element into the ring --------
     NIS_DFIX(0);
-    const float m0 = wmax_f32(r_max4(xv[0]));
+    // (PEN: of the plain elements; the stream leaves the penalised ones out)
+    const float m0 = wmax_f32(r_max4((PEN && (pany & 1u)) ? d_mask4(xv[0], (uint32_t)pnl & 15u) : xv[0]));
     const float Rw0 = (m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f;
     // elements more than 64 octaves below the first reference share one bucket
     const float tflo = (Rw0 - (float)kDSpan) * 64.0f;
-    float mx = -INFINITY;
+    float mx = -INFINITY;   // (PEN: of the plain elements)
+    float mxu = -INFINITY;  // PEN: of the penalised values rounded up
+    double ymx = -INFINITY; // PEN: of the penalised values
     // this lane's float4 masses go to sh.em4 chunk by chunk (2^R_z units):
     // the walk and the kept sums take the same values; chunks before kfin
     // were summed at an older reference and are summed again at the final
@@ -321,7 +404,17 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         __builtin_amdgcn_sched_barrier(0);
         if (k >= Kw) continue;
         if (k > 0) NIS_DFIX(k);
-        const f4v x = xv[k];
+        // PEN: the penalised elements are -inf in this copy (mass 0, count 1
+        // in the floor bucket, taken back with their own adds after the stream)
+        f4v x = xv[k];
+        if (PEN && ((pany >> k) & 1u)) x = d_mask4(x, (uint32_t)(pnl >> (4 * k)) & 15u);
+#define NIS_DHIST(jq, eq)                                                                  \
+        {                                                                                  \
+            const int j_ = d_flr(d_vmax((jq), tflo));                                      \
+            const uint32_t fm_ = (uint32_t)__builtin_amdgcn_ldexpf((eq), Rs - (j_ >> 6));   \
+            __hip_atomic_fetch_add(&sh.ring[j_ & (kDRing - 1)], (1ull << 48) | fm_,       \
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);        \
+        }
         const float m4 = r_max4(x);
         mx = fmaxf(mx, m4);
         // the reference follows the running max (the total moves by the exact
@@ -342,17 +435,10 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             em4w[64 * k] = s4;
             z += (double)s4;
         }
-#define NIS_DHIST(xq, eq)                                                                  \
-        {                                                                                  \
-            const int j_ = d_flr(d_vmax((xq) * chi64, tflo));                              \
-            const uint32_t fm_ = (uint32_t)__builtin_amdgcn_ldexpf((eq), Rs - (j_ >> 6));   \
-            __hip_atomic_fetch_add(&sh.ring[j_ & (kDRing - 1)], (1ull << 48) | fm_,       \
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);        \
-        }
-        NIS_DHIST(x.x, e0)
-        NIS_DHIST(x.y, e1)
-        NIS_DHIST(x.z, e2)
-        NIS_DHIST(x.w, e3)
+        NIS_DHIST(x.x * chi64, e0)
+        NIS_DHIST(x.y * chi64, e1)
+        NIS_DHIST(x.z * chi64, e2)
+        NIS_DHIST(x.w * chi64, e3)
 #undef NIS_DHIST
     }
     NIS_DTS(1);
@@ -365,13 +451,95 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
 #pragma unroll
         for (int k = 0; k < kDN; ++k) {
             if (k < kfin) {
-                const f4v x = xv[k];
+                f4v x = xv[k];
+                if (PEN && ((pany >> k) & 1u)) x = d_mask4(x, (uint32_t)(pnl >> (4 * k)) & 15u);
                 const float s4 = (r_mass(x.x, czh, czl, Rz) + r_mass(x.y, czh, czl, Rz)) +
                                  (r_mass(x.z, czh, czl, Rz) + r_mass(x.w, czh, czl, Rz));
                 em4w[64 * k] = s4;
                 z += (double)s4;
             }
         }
+    }
+    // PEN: fn(x, y, idx, k) for each penalised element of this lane's own
+    // slots (bit 4 k + q of pnl; few per lane): its logit x taken from the
+    // registers by a select over the chunks, y = pen(x) in f64, idx its row
+    // index, k its chunk.  One copy of the code, so the per-element f64 work
+    // is not repeated for every register chunk.
+    auto each_pen = [&](auto&& fn) {
+        if constexpr (PEN) {
+            uint64_t bits = pnl;
+            while (bits) {
+                const int i = __ffsll((long long)bits) - 1;
+                bits &= bits - 1ull;
+                const int k = i >> 2, q = i & 3;
+                // (a switch: a select loop over a runtime chunk index is
+                // turned into an indexed copy of xv in scratch memory, whose
+                // stores in the stream wait on every load in flight)
+                f4v c;
+                switch (k) {
+                    case 0: c = xv[0]; break;
+                    case 1: c = xv[1]; break;
+                    case 2: c = xv[2]; break;
+                    case 3: c = xv[3]; break;
+                    case 4: c = xv[4]; break;
+                    case 5: c = xv[5]; break;
+                    case 6: c = xv[6]; break;
+                    case 7: c = xv[7]; break;
+                    case 8: c = xv[8]; break;
+                    case 9: c = xv[9]; break;
+                    case 10: c = xv[10]; break;
+                    case 11: c = xv[11]; break;
+                    default: c = xv[12]; break;
+                }
+                static_assert(kDN == 13, "one case per register chunk");
+                const float x = elem(c, q);
+                fn(x, pen_value(x, pen), (uint32_t)(4 * (slot0 + 64 * k) - mis + q), k);
+            }
+        }
+    };
+    if constexpr (PEN) {
+        // The penalised elements the stream left out: their max (y rounded
+        // up bounds every bucket; the exact max serves the statistics), the
+        // reference raised past them if they need it (every float4 mass is
+        // then summed again), then their masses into their float4s' entries
+        // and Z, and their buckets, each taking back the floor bucket's count
+        // its -inf added.
+        each_pen([&](float, double y, uint32_t, int) {
+            ymx = fmax(ymx, y);
+            mxu = fmaxf(mxu, pen_f32_up(y));
+        });
+        const float mu = wmax_f32(mxu);
+        if (mu * chi > Rz + 1.0f) {
+            const float Rn = ceilf(fmaxf(mx, mu) * chi);
+            if (fabsf(Rn) < 1e30f) {
+                Rz = Rn;
+                z = 0.0;
+#pragma unroll
+                for (int k = 0; k < kDN; ++k) {
+                    if (k < Kw) {
+                        f4v x = xv[k];
+                        if ((pany >> k) & 1u) x = d_mask4(x, (uint32_t)(pnl >> (4 * k)) & 15u);
+                        const float s4 = (r_mass(x.x, czh, czl, Rz) + r_mass(x.y, czh, czl, Rz)) +
+                                         (r_mass(x.z, czh, czl, Rz) + r_mass(x.w, czh, czl, Rz));
+                        em4w[64 * k] = s4;
+                        z += (double)s4;
+                    }
+                }
+            }
+        }
+        const int Rs = (int)Rz + 24;
+        const int jflo = d_flr(tflo);
+        each_pen([&](float, double y, uint32_t, int k) {
+            const float ey = (float)pen_mass(y * c64, Rz);
+            em4w[64 * k] += ey;
+            z += (double)ey;
+            const int j = d_flr(d_vmax(d_pt(y, chid) * 64.0f, tflo));
+            const uint32_t fm = (uint32_t)__builtin_amdgcn_ldexpf(ey, Rs - (j >> 6));
+            __hip_atomic_fetch_add(&sh.ring[j & (kDRing - 1)], (1ull << 48) | fm, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(&sh.ring[jflo & (kDRing - 1)], 0ull - (1ull << 48), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        });
     }
     {
         const bool nan_seen = __ballot(z != z) != 0ull;
@@ -381,6 +549,11 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                 atomicMin(&sh.krw0, key32(Rw0));
             }
             if (nan_seen) atomicOr(&sh.fnan, 1u);
+            if (PEN && Kw > 0) atomicMax(&sh.kpl, key32(mx == mx ? mx : -INFINITY));
+        }
+        if (PEN) {  // (few lanes: those holding penalised elements)
+            if (mxu > -INFINITY) atomicMax(&sh.kmax, key32(mxu));
+            if (ymx > -INFINITY) atomicMax(&sh.kymax, key64(ymx));
         }
     }
     // the row's one draw (sampler.rs:209), made by wave 0; the advanced state
@@ -411,6 +584,10 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         if (!ok) {
             NIS_DTFLUSH();
             return NIS_REJECT_NONFINITE;
+        }
+        if (PEN && sh.pover != 0u) {
+            NIS_DTFLUSH();
+            return NIS_REJECT_CAPACITY;  // a history longer than the bitmaps take
         }
     }
 
@@ -496,14 +673,16 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     bool brute = nside > (uint32_t)(kDL * kDW);
     uint32_t nq = 0u;  // wave-uniform list length
     if (!brute) {
-        const uint32_t ent0 = lds_addr(&sh.ent[w][0]), epos0 = lds_addr(&sh.epos[w][0]);
+        const uint32_t ent0 = lds_addr(&sh.u.l.ent[w][0]), epos0 = lds_addr(&sh.u.l.epos[w][0]);
         auto list_chunks = [&](auto&& pred) {
 #pragma unroll
             for (int k = 0; k < kDN; ++k) {
                 if (k < Kw) {
-                    const uint64_t sk = __ballot(pred(xv[k]));
+                    // PEN: a float4 holding a penalised element is listed on either side
+                    const uint32_t pmk = PEN ? (uint32_t)(pnl >> (4 * k)) & 15u : 0u;
+                    const uint64_t sk = __ballot(pred(xv[k]) | (pmk != 0u));
                     const uint32_t s = min(nq + lane_rank(sk), (uint32_t)kDL - 1u);
-                    lds_put_x4_u16(sk, ent0 + 16 * s, xv[k], epos0 + 2 * s, (uint32_t)(k * 64 + l));
+                    lds_put_x4_u16(sk, ent0 + 16 * s, xv[k], epos0 + 2 * s, (uint32_t)(k * 64 + l) | (pmk << 12));
                     nq += (uint32_t)__popcll(sk);
                 }
             }
@@ -519,8 +698,9 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
 
     // ---- the cutoff bucket's members: refined while more than kDMem ----------
     // Every float4 holding a member of b_p is on the listed side (or, when a
-    // list overflowed, in this lane's registers); fn(x4, i0, valid) visits them,
-    // i0 the row index of element 0.
+    // list overflowed, in this lane's registers); fn(x4, i0, valid, pm) visits
+    // them, i0 the row index of element 0, pm (PEN) its penalised elements,
+    // which the callers skip: each_pen visits those instead.
     const int ne = (int)min(nq, (uint32_t)kDL);
     auto each_float4 = [&](auto&& fn) {
         if (!brute) {
@@ -528,19 +708,22 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             for (int r = 0; r < kDL / 64; ++r) {
                 if (64 * r < ne) {
                     const int je = 64 * r + l;
-                    fn(sh.ent[w][je], (uint32_t)(4 * (wbase + (int)sh.epos[w][je]) - mis), je < ne);
+                    const uint32_t ev = sh.u.l.epos[w][je];
+                    fn(sh.u.l.ent[w][je], (uint32_t)(4 * (wbase + (int)(ev & 0xFFFu)) - mis), je < ne,
+                       PEN ? ev >> 12 : 0u);
                 }
             }
         } else {
 #pragma unroll
             for (int k = 0; k < kDN; ++k)
-                if (k < Kw) fn(xv[k], (uint32_t)NIS_RIDXD(k), true);
+                if (k < Kw) fn(xv[k], (uint32_t)NIS_RIDXD(k), true, PEN ? (uint32_t)(pnl >> (4 * k)) & 15u : 0u);
         }
     };
     int lv = 0, B = bp;
     unsigned long long Gc = Gp;
     uint32_t ns = nsel0, nabv = nab0;
     float chiL = chi64;
+    float scL = 64.0f;  // 64^(lv + 1): the level's buckets of T(v)
     bool all_out = false;  // the whole bucket is removed (no sub-bucket passes)
     while (ns > (uint32_t)kDMem) {
         if (lv == kDLevels - 1) {
@@ -548,12 +731,12 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             return NIS_REJECT_CAPACITY;  // exact ties beyond kDMem members
         }
         const int o = B >> (6 * (lv + 1));  // the bucket's octave
-        const float chiS = chiL * 64.0f;
-        each_float4([&](const f4v& x4, uint32_t i0, bool valid) {
+        const float chiS = chiL * 64.0f, scS = scL * 64.0f;
+        each_float4([&](const f4v& x4, uint32_t i0, bool valid, uint32_t pm) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float x = elem(x4, q);
-                const bool mem = valid & (d_flr(x * chiL) == B);
+                const bool mem = valid & (d_flr(x * chiL) == B) & !(PEN && ((pm >> q) & 1u));
                 if (__ballot(mem)) {
                     const uint32_t fm = r_fm(x, chi, clo, o);
                     const uint32_t sb = (uint32_t)d_flr(x * chiS) & 63u;
@@ -562,6 +745,13 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             }
+        });
+        each_pen([&](float, double y, uint32_t, int) {
+            const float t = d_pt(y, chid);
+            if (d_flr(t * scL) == B)
+                __hip_atomic_fetch_add(&sh.sub[(uint32_t)d_flr(t * scS) & 63u],
+                                       (1ull << 48) | (unsigned long long)d_pfm(y * c64, o), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
         });
         lds_barrier();
         if (w == 0) {
@@ -575,6 +765,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             const uint64_t ps = __ballot((n != 0u) && ((double)Gs - d_mup(Fs, lv + 1, Ri) <= pz));
             DCut c;
             c.kcut = ~0ull;
+            c.kidx = 0u;
             c.rej = 0u;
             c.nkept = 0u;
             if (ps) {
@@ -607,24 +798,30 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             break;
         }
         chiL = chiS;
+        scL = scS;
     }
     NIS_DTS(11);
     // members of the final bucket B (at most kDMem) into sh.mem
     if (!all_out && ns > 0u) {
         const int o = B >> (6 * (lv + 1));
-        each_float4([&](const f4v& x4, uint32_t i0, bool valid) {
+        each_float4([&](const f4v& x4, uint32_t i0, bool valid, uint32_t pm) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float x = elem(x4, q);
-                const bool mem = valid & (d_flr(x * chiL) == B);
+                const bool mem = valid & (d_flr(x * chiL) == B) & !(PEN && ((pm >> q) & 1u));
                 const uint64_t mb = __ballot(mem);
                 if (mb) {
                     uint32_t b0 = 0u;
                     if (l == 0) b0 = atomicAdd(&sh.nmem, (uint32_t)__popcll(mb));
                     const uint32_t sm = bcast_u32(b0, 0) + lane_rank(mb);
-                    if (mem)
-                        sh.mem[min(sm, (uint32_t)kDMem - 1u)] = RCand{x, i0 + (uint32_t)q, o, r_fm(x, chi, clo, o)};
+                    if (mem) sh.mem[min(sm, (uint32_t)kDMem - 1u)] = RCand{x, i0 + (uint32_t)q, o, r_fm(x, chi, clo, o)};
                 }
+            }
+        });
+        each_pen([&](float x, double y, uint32_t idx, int) {
+            if (d_flr(d_pt(y, chid) * scL) == B) {
+                const uint32_t sm = atomicAdd(&sh.nmem, 1u);
+                sh.mem[min(sm, (uint32_t)kDMem - 1u)] = RCand{x, idx | 0x80000000u, o, d_pfm(y * c64, o)};
             }
         });
     }
@@ -644,30 +841,41 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         c.nsel = ns;
         c.rej = 0u;
         c.kcut = ~0ull;
+        c.kidx = 0u;
         c.nkept = 0u;
         if (!all_out) {
             const int n = (int)ns;
             const bool valid = l < n;
             const RCand mr = sh.mem[min(l, kDMem - 1)];
-            const unsigned long long Km = valid ? r_key(mr.x, mr.idx) : 0ull;
+            // PEN: (key64 of the value, row index) pairs
+            const uint32_t im = PEN ? (mr.idx & 0x7FFFFFFFu) : mr.idx;
+            unsigned long long Km;
+            if constexpr (PEN)
+                Km = valid ? key64((mr.idx >> 31) ? pen_value(mr.x, pen) : (double)mr.x) : 0ull;
+            else
+                Km = valid ? r_key(mr.x, mr.idx) : 0ull;
             const unsigned long long em = valid ? d_u44(mr.fm, mr.b, Ri) : 0ull;
             // every lane compares its key with all of them, read back from LDS
             // (same address in every lane; eight reads in flight per step)
             sh.mkey[l] = Km;
             sh.mmass[l] = em;
+            if (PEN) sh.midx[l] = im;
             lds_wave_fence();
             unsigned long long pre = 0ull;  // mass of the members ahead of this one
             uint32_t rk = 0u;
             for (int j0 = 0; j0 < n; j0 += 8) {
                 unsigned long long kj[8], ej[8];
+                uint32_t ij[8];
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
                     kj[jj] = sh.mkey[min(j0 + jj, kDMem - 1)];
                     ej[jj] = sh.mmass[min(j0 + jj, kDMem - 1)];
+                    ij[jj] = PEN ? sh.midx[min(j0 + jj, kDMem - 1)] : 0u;
                 }
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
-                    const bool ahead = (j0 + jj < n) & (kj[jj] > Km);
+                    const bool gt = PEN ? ((kj[jj] > Km) | ((kj[jj] == Km) & (ij[jj] < im))) : (kj[jj] > Km);
+                    const bool ahead = (j0 + jj < n) & gt;
                     pre += ahead ? ej[jj] : 0ull;
                     rk += ahead ? 1u : 0u;
                 }
@@ -679,6 +887,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             if (__ballot(valid & !pass)) nkept = wmin_u32((valid && !pass) ? rk : 0xFFFFFFFFu);
             const uint64_t lastm = __ballot(valid & (rk + 1u == nkept));
             c.kcut = lastm ? rbcast_u64(Km, __ffsll((long long)lastm) - 1) : ~0ull;
+            c.kidx = lastm ? bcast_u32(im, __ffsll((long long)lastm) - 1) : 0u;
             c.nkept = nkept;
         }
         if (l == 0) sh.cut = c;
@@ -689,11 +898,16 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     const DCut cut = sh.cut;
     const int Bf = cut.bj;
     const unsigned long long kcut = cut.kcut;
+    const uint32_t kidx = cut.kidx;
     {
         // chi at the final level's resolution (exact powers of two)
-        float cl = chi64;
-        for (int i = 0; i < cut.lv; ++i) cl *= 64.0f;
+        float cl = chi64, sl = 64.0f;
+        for (int i = 0; i < cut.lv; ++i) {
+            cl *= 64.0f;
+            sl *= 64.0f;
+        }
         chiL = cl;
+        scL = sl;
     }
 
     // ---- kept masses: this wave's listed float4s, or all of its float4s -----
@@ -701,7 +915,9 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // mass, from the same per-element masses the stream summed
     // (the stable-order key is compared only in a chunk holding an element
     // of the final bucket: at most kDMem of them in the row)
-    auto kept4 = [&](const f4v& x4, uint32_t i0, float& all) {
+    // (PEN: the penalised elements, marked in pm, count 0 here: each_pen adds
+    // their kept masses after)
+    auto kept4 = [&](const f4v& x4, uint32_t i0, uint32_t pm, float& all) {
         float e[4], k4[4];
         int F[4];
         bool inb = false;
@@ -709,14 +925,23 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         for (int q = 0; q < 4; ++q) {
             const float x = elem(x4, q);
             e[q] = r_mass(x, czh, czl, Rz);
+            if (PEN && ((pm >> q) & 1u)) e[q] = 0.0f;
             F[q] = d_flr(x * chiL);
             k4[q] = (F[q] > Bf) ? e[q] : 0.0f;
             inb |= F[q] == Bf;
         }
         if (__ballot(inb)) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if ((F[q] == Bf) && (r_key(elem(x4, q), i0 + (uint32_t)q) >= kcut)) k4[q] = e[q];
+            for (int q = 0; q < 4; ++q) {
+                if (F[q] != Bf) continue;
+                bool kq;
+                if constexpr (PEN) {
+                    kq = d_pkeep(key64((double)elem(x4, q)), i0 + (uint32_t)q, kcut, kidx);
+                } else {
+                    kq = r_key(elem(x4, q), i0 + (uint32_t)q) >= kcut;
+                }
+                if (kq) k4[q] = e[q];
+            }
         }
         all = (e[0] + e[1]) + (e[2] + e[3]);
         return (k4[0] + k4[1]) + (k4[2] + k4[3]);
@@ -741,8 +966,10 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                 const int je = 64 * r + l;
                 const bool valid = je < ne;
                 float orig;
-                const int ep = (int)sh.epos[w][min(je, kDL - 1)];
-                const float ks = kept4(sh.ent[w][min(je, kDL - 1)], (uint32_t)(4 * (wbase + ep) - mis), orig);
+                const uint32_t ev = sh.u.l.epos[w][min(je, kDL - 1)];
+                const int ep = (int)(ev & 0xFFFu);
+                const float ks = kept4(sh.u.l.ent[w][min(je, kDL - 1)], (uint32_t)(4 * (wbase + ep) - mis),
+                                       PEN ? ev >> 12 : 0u, orig);
                 if (valid) esw[ep] = ks;
                 tws += valid ? (kside ? (double)ks : (double)ks - (double)orig) : 0.0;
             }
@@ -754,10 +981,29 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         for (int k = 0; k < kDN; ++k) {
             if (k < Kw) {
                 float orig;
-                kvb[k] = kept4(xv[k], (uint32_t)NIS_RIDXD(k), orig);
+                kvb[k] = kept4(xv[k], (uint32_t)NIS_RIDXD(k), PEN ? (uint32_t)(pnl >> (4 * k)) & 15u : 0u,
+                               orig);
                 tws += (double)kvb[k];
             }
         }
+    }
+    if constexpr (PEN) {
+        // the penalised elements' kept masses join their float4s' entries (a
+        // brute row's register masses are parked there first) and the total
+        float* const esw = &sh.em4[w][0][0];
+        if (brute) {
+#pragma unroll
+            for (int k = 0; k < kDN; ++k) esw[64 * k + l] = kvb[k];
+        }
+        lds_wave_fence();
+        const bool off_kept = !brute && !kside;  // their stream masses are already in tws
+        each_pen([&](float, double y, uint32_t idx, int k) {
+            const float ey = (float)pen_mass(y * c64, Rz);
+            const int F = d_flr(d_pt(y, chid) * scL);
+            const float ky = ((F > Bf) | ((F == Bf) & d_pkeep(key64(y), idx, kcut, kidx))) ? ey : 0.0f;
+            esw[64 * k + l] += ky;
+            tws += (double)ky - (off_kept ? (double)ey : 0.0);
+        });
     }
     {
         const double Tw = wsum_f64(tws);
@@ -793,7 +1039,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
 #pragma unroll
         for (int k = 0; k < kDN; ++k) kv[k] = esw[64 * k];
 #pragma unroll
-        for (int k = 0; k < kDN; ++k) kv[k] = brute ? kvb[k] : ((k < Kw) ? kv[k] : 0.0f);
+        for (int k = 0; k < kDN; ++k) kv[k] = (brute && !PEN) ? kvb[k] : ((k < Kw) ? kv[k] : 0.0f);
     }
 #pragma unroll
     for (int k = 0; k < kDN; ++k) sh.walk[k][l] = kv[k];
@@ -845,14 +1091,23 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     if (l == lc) {
         double run = rk_ - (lincl - sl);
         const uint32_t ib = (uint32_t)NIS_RIDXD(kc);
+        const uint32_t pmc = PEN ? (uint32_t)(pnl >> (4 * kc)) & 15u : 0u;
         float ev[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float xq = elem(xc, q);
             // the same masses the float4's kept total was summed from
-            const float eq = r_mass(xq, czh, czl, Rz);
             // (a float4 kept whole passes every test: its elements lie above b_p)
-            ev[q] = d_kept(xq, ib + (uint32_t)q, chiL, Bf, kcut) ? eq : 0.0f;
+            if constexpr (PEN) {
+                const bool pq = (pmc >> q) & 1u;
+                const double v = pq ? pen_value(xq, pen) : (double)xq;
+                const float eq = pq ? (float)pen_mass(v * c64, Rz) : r_mass(xq, czh, czl, Rz);
+                const int F = pq ? d_flr(d_pt(v, chid) * scL) : d_flr(xq * chiL);
+                ev[q] = ((F > Bf) | ((F == Bf) & d_pkeep(key64(v), ib + (uint32_t)q, kcut, kidx))) ? eq : 0.0f;
+            } else {
+                const float eq = r_mass(xq, czh, czl, Rz);
+                ev[q] = d_kept(xq, ib + (uint32_t)q, chiL, Bf, kcut) ? eq : 0.0f;
+            }
         }
         int q = -1, qlast = 0;
 #pragma unroll
@@ -871,11 +1126,15 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         if (u == 0.0) tok = 0u;  // r == 0 stops the reference's walk at index 0
         emit_token(a, row, tok);
         if (a.stats) {
+            // PEN: the exact max over the plain and the penalised values, and
+            // the drawn token's value after the penalty
+            const double Mx = PEN ? fmax((double)unkey32(sh.kpl), unkey64(sh.kymax)) : (double)M;
+            const double vq = (PEN && ((pmc >> q) & 1u)) ? pen_value(xq, pen) : (double)xq;
             // 2^(R - M c): units of 2^R -> units of the max element's mass
-            const double rho = exp2((double)R - (double)M * c64);
-            const double em = exp2((double)xq * c64 - (double)M * c64);
+            const double rho = exp2((double)R - Mx * c64);
+            const double em = exp2(vq * c64 - Mx * c64);
             const double zM = Zk * rho;
-            write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)M / temp, zM,
+            write_row_stats(a, row, tok, NIS_PATH_DRAW, Mx / temp, zM,
                             (double)Z / 17592186044416.0 * rho, u, (u == 0.0) ? 0.0 : em / zM,
                             (uint64_t)(cut.nab + cut.nkept), 1);
         }
@@ -888,25 +1147,38 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
 #undef NIS_RIDXD
 }
 
+union DenseKernelShared {
+    GeneralShared g;
+    NucleusShared d;
+};
+
 // One 1024-lane workgroup per row: the dense path, or the general path (on
 // the first 512 lanes) for a row it declines or cannot take.
-__global__ __launch_bounds__(kDB) void sample_rows_dense_kernel(RowArgs a) {
-    __shared__ union {
-        GeneralShared g;
-        NucleusShared d;
-    } sh;
+template <bool PEN>
+__device__ __forceinline__ void dense_kernel(const RowArgs a, DenseKernelShared& sh) {
     const int row = (int)blockIdx.x;
     if (a.done != nullptr && a.done[row]) return;  // a finished sequence (decode step)
     asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
                  "s"(a.penalty), "s"(a.gen_ids), "s"(a.gen_off));
     uint32_t reject = NIS_REJECT_SHAPE;
-    if (dense_eligible(a, row)) {
-        reject = dense_row(a, row, sh.d);
+    if (dense_eligible<PEN>(a, row)) {
+        reject = dense_row<PEN>(a, row, sh.d);
         if (reject == NIS_REJECT_NONE) return;
     }
     if (threadIdx.x >= kBlock) return;
     __syncthreads();
     general_row<1>(a, row, sh.g, reject);
+}
+
+__global__ __launch_bounds__(kDB) void sample_rows_dense_kernel(RowArgs a) {
+    __shared__ DenseKernelShared sh;
+    dense_kernel<false>(a, sh);
+}
+
+// The same with a repetition-penalty history applied in registers.
+__global__ __launch_bounds__(kDB) void sample_rows_dense_pen_kernel(RowArgs a) {
+    __shared__ DenseKernelShared sh;
+    dense_kernel<true>(a, sh);
 }
 
 }  // namespace nis

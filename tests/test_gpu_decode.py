@@ -129,12 +129,12 @@ def test_decode_steps_match_oracle_loop(sampler, V, kw, cap):
 
 
 @pytest.mark.parametrize("pen,T,p", [(1.3, 0.8, 0.9), (0.8, 0.8, 0.9), (1.2, 0.0, 0.9),
-                                     (1.2, 0.8, 1.0)])
+                                     (1.2, 0.8, 1.0), (1.3, 0.8, 0.97)])
 def test_penalised_decode_stays_on_the_register_kernels(sampler, pen, T, p):
-    # V = 50257, top-p 0.9 (or greedy) with a penalty, logits of the
-    # headline's spread (N(0, 3^2): nuclei of a few hundred tokens): every
-    # step of every sequence runs in the sparse (resident) kernel with its
-    # history applied in registers
+    # V = 50257, top-p 0.9 / 0.97 (or greedy, or top-p off) with a penalty,
+    # logits of the headline's spread (N(0, 3^2)): every step of every
+    # sequence runs in the sparse, dense or resident kernel with its history
+    # applied in registers
     kernels = []
     kw = dict(temperature=T, top_p=p, repetition_penalty=pen)
     diverged, n_done, n_started, _ = _run(sampler, B=24, V=50257, steps=7, cap=8, params_kw=kw,

@@ -363,11 +363,10 @@ def test_invalid_arguments_are_rejected(sampler):
 
 
 def test_penalty_launch_rows_take_the_register_kernels(sampler):
-    # A top-p < 0.95 or top-p-off penalty launch runs the sparse or resident
-    # kernel with the penalty applied in registers: every row stays on it
-    # (kernel == 1, reject 0).  At top-p 0.99 it runs the dense kernel: the
-    # rows without a history stay on it, the rows with one run the general
-    # path inside it (kernel == 2).
+    # A penalty launch runs the sparse (top-p < 0.95), dense (0.95 <= top-p
+    # < 1) or resident (top-p off) kernel's penalised form, with the penalty
+    # applied in registers: every row, with a history or without one, stays
+    # on it (kernel == 1, reject 0).
     from nimbus_sampler import workloads
     B, V = 32, 50257
     rnd = np.random.Generator(np.random.PCG64(31))
@@ -376,16 +375,10 @@ def test_penalty_launch_rows_take_the_register_kernels(sampler):
     off = np.zeros(B + 1, np.int64)
     off[1:] = np.cumsum([len(g) for g in gen])
     ids = np.concatenate(gen).astype(np.uint32)
-    empty = np.array([len(g) == 0 for g in gen])
     for p in (0.9, 0.99, 1.0):
         params = _params(temperature=0.8, top_p=p, repetition_penalty=1.2)
         gpu = run_gpu(sampler, x, V, params, list(range(B)), ids, off)
         ref = run_oracle(x, V, params, list(range(B)), ids, off)
         compare(gpu, ref, greedy=False)
         st = gpu[1]
-        if p != 0.99:
-            assert (st["kernel"] == 1).all() and (st["reject"] == 0).all(), st["reject"]
-        else:
-            assert (st["kernel"][~empty] == 2).all(), st["kernel"]
-            assert (st["kernel"][empty] == 1).all() and (st["reject"][empty] == 0).all(), \
-                (st["kernel"], st["reject"])
+        assert (st["kernel"] == 1).all() and (st["reject"] == 0).all(), (p, st["kernel"], st["reject"])

@@ -1,12 +1,14 @@
-"""GPU parity of the repetition penalty inside the sparse (headline) kernel.
+"""GPU parity of the repetition penalty inside the register-resident kernels.
 
-A top-p launch with a penalty history runs sample_rows_sparse_pen_kernel,
-which applies apply_repetition_penalty (src/sampler.rs:83-101) in f64 to the
-row it holds in registers: penalised logits leave the register path as the
-chunk lands and rejoin the histogram, the member ranking and the walk from a
-side list.  Every row must match the oracle's sample() and stay on that
-kernel (stats kernel == 1, reject == 0): none may fall back to the general
-path.
+A top-p launch with a penalty history runs sample_rows_sparse_pen_kernel
+(top-p < 0.95) or sample_rows_dense_pen_kernel (0.95 <= top-p < 1), which
+apply apply_repetition_penalty (src/sampler.rs:83-101) in f64 to the row they
+hold in registers.  The sparse kernel moves penalised logits to a side list
+as the chunk lands; the dense kernel keeps them in registers and gives the
+flagged chunks an f64 form of each step.  Greedy and top-p-off launches run
+the resident kernel's penalised modes.  Every row must match the oracle's
+sample() and stay on its kernel (stats kernel == 1, reject == 0): none may
+fall back to the general path.
 """
 import numpy as np
 import pytest
@@ -211,11 +213,11 @@ def test_greedy_ties_between_penalised_and_plain_values(sampler):
     assert all(int(gpu[0][r]) == 0 for r in range(0, B, 4))
 
 
-@pytest.mark.parametrize("T,p", [(0.0, 1.0), (0.8, 1.0), (0.8, 0.9)])
+@pytest.mark.parametrize("T,p", [(0.0, 1.0), (0.8, 1.0), (0.8, 0.9), (0.8, 0.97)])
 def test_non_finite_and_long_histories_fall_back(sampler, T, p):
     # NaN among the penalised logits, and histories past 4096 ids: declined,
     # recomputed by the general path (kernel == 2), same answers; greedy,
-    # top-p off and sparse top-p
+    # top-p off, sparse and dense top-p
     from nimbus_sampler import workloads
     B, V = 4, 50257
     x = workloads.headline(B)
@@ -264,3 +266,94 @@ def test_top_p_off_histories_on_the_top(sampler, pen):
     drew = sum(int(gpu[0][r]) in set(gen[r].tolist()) for r in range(B))
     print(f"[penalty] top-p off rows that drew a penalised token: {drew}/{B}", flush=True)
     assert drew > B // 4
+
+
+# ---------------------------------------------------------------------------
+# 0.95 <= top-p < 1: the dense kernel's penalised form
+
+def _rows(kind, B, V=50257):
+    from nimbus_sampler import workloads
+    if kind == "normal":
+        return workloads.headline(B, V)  # N(0, 3^2)
+    if kind == "flat":
+        return workloads.c5(B, V)        # U(-0.5, 0.5): nearly every token kept
+    return workloads.c2(B, V)            # peaks over N(0, 1): cutoff in the noise
+
+
+@pytest.mark.parametrize("kind,p,pen,T", [
+    ("normal", 0.97, 1.3, 0.8), ("normal", 0.99, 0.8, 0.8), ("normal", 0.95, 2.0, 1.0),
+    ("flat", 0.99, 1.3, 1.3), ("flat", 0.99, 0.8, 1.0),
+    ("peaks", 0.95, 1.3, 1.0), ("peaks", 0.97, 0.8, 1.0),
+])
+def test_dense_random_histories(sampler, kind, p, pen, T):
+    # histories of 0..400 ids with repeats, some past V; the flat rows list
+    # their removed side, the peaks rows (cutoff inside the noise) work in
+    # registers without a list
+    B, V = 64, 50257
+    rnd = np.random.Generator(np.random.PCG64(int(pen * 100) + int(p * 1000)))
+    x = _rows(kind, B)
+    gen = []
+    for r in range(B):
+        n = int(rnd.integers(0, 401))
+        g = rnd.integers(0, V + 8, size=n)
+        if n > 4:
+            g[: n // 4] = g[n // 4: 2 * (n // 4)]  # repeats
+        gen.append(g)
+    _check(sampler, x, V, _params(temperature=T, top_p=p, repetition_penalty=pen), gen,
+           f"dense {kind} pen={pen} p={p}")
+
+
+@pytest.mark.parametrize("kind,pen,p", [("normal", 1.3, 0.97), ("normal", 0.8, 0.99),
+                                        ("peaks", 1.5, 0.95), ("flat", 2.0, 0.99)])
+def test_dense_histories_on_the_head(sampler, kind, pen, p):
+    # the history holds each row's top tokens (up to 1500 of them), so
+    # penalised values are kept, fall into the cutoff's bucket, are ranked
+    # and drawn; with penalty < 1 they also set the row max
+    B, V = 64, 50257
+    rnd = np.random.Generator(np.random.PCG64(31 + int(pen * 100)))
+    x = _rows(kind, B)
+    order = np.argsort(-x, axis=1, kind="stable")
+    gen = [order[r, : int(rnd.integers(1, 1500))] for r in range(B)]
+    gpu, _ = _check(sampler, x, V, _params(temperature=1.0, top_p=p, repetition_penalty=pen), gen,
+                    f"dense head {kind} pen={pen} p={p}")
+    drew = sum(int(gpu[0][r]) in set(gen[r].tolist()) for r in range(B))
+    print(f"[penalty] dense rows that drew a penalised token: {drew}/{B}", flush=True)
+    assert drew > 0
+
+
+def test_dense_ties_between_penalised_and_plain_values(sampler):
+    # logits on a 1/1024 lattice (a few elements per value); penalty 2 maps
+    # a penalised 2v (or v/2 for v <= 0) to exactly v, so penalised and plain
+    # values tie in f64 across the whole row and the stable order (value,
+    # then index) decides at the cutoff
+    B, V = 48, 50257
+    rnd = np.random.Generator(np.random.PCG64(13))
+    base = np.round(rnd.standard_normal((B, V)) * 1536.0).astype(np.float32) / np.float32(1024.0)
+    gen = []
+    for r in range(B):
+        idx = rnd.choice(V, size=int(rnd.integers(200, 3000)), replace=False)
+        pos = base[r, idx] > 0
+        base[r, idx[pos]] *= np.float32(2.0)
+        base[r, idx[~pos]] *= np.float32(0.5)
+        gen.append(idx)
+    for p in (0.95, 0.99):
+        _check(sampler, base, V, _params(temperature=0.8, top_p=p, repetition_penalty=2.0),
+               gen, f"dense ties p={p}")
+
+
+def test_dense_padded_rows_and_short_vocabularies(sampler):
+    # misaligned rows put penalised ids in the partial head and tail slots
+    rnd = np.random.Generator(np.random.PCG64(9))
+    for V, ld in ((50257, 50261), (256, 259), (1000, 1000), (53245, 53248)):
+        B = 16
+        x = _rows("normal", B, V)
+        gen = [np.concatenate([[0, 1, 2, V - 1, V - 2, V - 3],
+                               rnd.integers(0, V, size=int(rnd.integers(0, 40)))])
+               for _ in range(B)]
+        ids, off = _csr(gen)
+        params = _params(temperature=0.8, top_p=0.97, repetition_penalty=1.4)
+        print(f"[penalty] dense padded V={V} ld={ld}", flush=True)
+        gpu = run_gpu(sampler, x, V, params, list(range(B)), ids, off, ld=ld)
+        ref = run_oracle(x, V, params, list(range(B)), ids, off)
+        compare(gpu, ref, greedy=False)
+        assert (gpu[1]["kernel"] == 1).all() and (gpu[1]["reject"] == 0).all(), (V, ld)
