@@ -56,12 +56,13 @@
 //
 // PEN: the history's ids go into LDS bitmaps before the stream (as for the
 // sparse kernel), so each wave holds one bit per chunk (pany) and each lane a
-// 4-bit mask per chunk of its own slot's penalised elements (pnl).  A
-// penalised element keeps its logit x in registers, but every register pass
-// skips it: the stream works on a copy of a flagged chunk with -inf in its
-// place, and the later passes test the mask.  After each pass, each lane
-// visits its own penalised elements one by one (few per lane; each_pen) with
-// y = pen(x) in f64: the mass 2^(y c - R_z) from the f64 argument, the bucket
+// 4-bit mask per chunk of its own slot's penalised elements (pnl).  Every
+// register pass skips a penalised element: the stream works on a copy of a
+// flagged chunk with -inf in its place, and after the cutoff search each
+// lane parks its penalised logits in the (then free) histogram ring and puts
+// -inf in their register places.  After each pass, each lane visits its own
+// penalised elements one by one (few per lane; each_pen) with y = pen(x) in
+// f64: the mass 2^(y c - R_z) from the f64 argument, the bucket
 // functions floor(64^L T(y)) with T(v) = (float)(v c_hi) (for an f32 logit
 // T(x) = f32(x c_hi), so one monotone function orders plain and penalised
 // values alike), the max (y rounded up bounds every bucket, and moves the
@@ -90,6 +91,7 @@ constexpr int kDSpan = 64;                 // octaves searched below R
 constexpr int kDL = 128;                   // listed float4s per wave (one side of the cutoff)
 constexpr int kDMem = 64;                  // members ranked exactly
 constexpr int kDLevels = 3;                // bucket resolutions: 64, 64^2, 64^3 per octave
+constexpr int kDPenLane = 2 * kDRing / kDB;  // PEN: penalised elements one lane's slots may hold
 
 enum { kDKeptSide = 0, kDRemovedSide = 1, kDBrute = 2 };
 
@@ -171,7 +173,10 @@ struct NucleusShared {
     uint32_t kpl;                     // PEN: the plain elements' max (key32; kmax also
                                       //   holds the penalised values rounded up)
     unsigned long long kymax;         // PEN: the penalised values' exact max (key64)
-    uint32_t pover;                   // PEN: the history is longer than the bitmaps take
+    uint32_t pover;                   // PEN: bit 0: the history is longer than the bitmaps
+                                      //   take; bit 1: a lane holds more than kDPenLane
+                                      //   penalised elements
+    double my[kDMem];                 // PEN: the penalised members' values
     unsigned long long wtm[kDW];      // search: each wave's bucket mass
     uint32_t wtc[kDW];                //   and count
     DCand cand[kDW];
@@ -460,12 +465,12 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             }
         }
     }
-    // PEN: fn(x, y, idx, k) for each penalised element of this lane's own
-    // slots (bit 4 k + q of pnl; few per lane): its logit x taken from the
-    // registers by a select over the chunks, y = pen(x) in f64, idx its row
-    // index, k its chunk.  One copy of the code, so the per-element f64 work
-    // is not repeated for every register chunk.
-    auto each_pen = [&](auto&& fn) {
+    // PEN: fn(y, k) for each penalised element of this lane's own slots
+    // (bit 4 k + q of pnl, in that order; few per lane): its logit taken from
+    // the registers, y = pen(x) in f64, k its chunk.  One copy of the code,
+    // so the per-element f64 work is not repeated for every register chunk.
+    // (Until the cutoff search; after it each_pen reads the parked values.)
+    auto each_pen_x = [&](auto&& fn) {
         if constexpr (PEN) {
             uint64_t bits = pnl;
             while (bits) {
@@ -492,8 +497,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                     default: c = xv[12]; break;
                 }
                 static_assert(kDN == 13, "one case per register chunk");
-                const float x = elem(c, q);
-                fn(x, pen_value(x, pen), (uint32_t)(4 * (slot0 + 64 * k) - mis + q), k);
+                fn(pen_value(elem(c, q), pen), k);
             }
         }
     };
@@ -504,10 +508,13 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         // then summed again), then their masses into their float4s' entries
         // and Z, and their buckets, each taking back the floor bucket's count
         // its -inf added.
-        each_pen([&](float, double y, uint32_t, int) {
+        each_pen_x([&](double y, int) {
             ymx = fmax(ymx, y);
             mxu = fmaxf(mxu, pen_f32_up(y));
         });
+        // (each lane parks its penalised values after the search: at most
+        // kDPenLane of them)
+        if (__popcll(pnl) > kDPenLane) atomicOr(&sh.pover, 2u);
         const float mu = wmax_f32(mxu);
         if (mu * chi > Rz + 1.0f) {
             const float Rn = ceilf(fmaxf(mx, mu) * chi);
@@ -529,7 +536,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         }
         const int Rs = (int)Rz + 24;
         const int jflo = d_flr(tflo);
-        each_pen([&](float, double y, uint32_t, int k) {
+        each_pen_x([&](double y, int k) {
             const float ey = (float)pen_mass(y * c64, Rz);
             em4w[64 * k] += ey;
             z += (double)ey;
@@ -587,7 +594,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         }
         if (PEN && sh.pover != 0u) {
             NIS_DTFLUSH();
-            return NIS_REJECT_CAPACITY;  // a history longer than the bitmaps take
+            return NIS_REJECT_CAPACITY;  // a history past the bitmaps, or a crowded lane
         }
     }
 
@@ -614,6 +621,53 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // ---- B2: the waves' bucket totals ---------------------------------------
     lds_barrier();
     NIS_DTS(10);
+    // PEN: the ring has been read; each lane parks its penalised logits in
+    // its own kDPenLane words of it, in pnl's bit order, and puts -inf in
+    // their register places, so every later register pass skips them
+    float* const ppark = reinterpret_cast<float*>(&sh.ring[0]) + kDPenLane * tid;
+    if constexpr (PEN) {
+        uint64_t bits = pnl;
+        int jp = 0;
+        while (bits) {  // (the same select as each_pen_x)
+            const int i = __ffsll((long long)bits) - 1;
+            bits &= bits - 1ull;
+            const int k = i >> 2, q = i & 3;
+            f4v c;
+            switch (k) {
+                case 0: c = xv[0]; break;
+                case 1: c = xv[1]; break;
+                case 2: c = xv[2]; break;
+                case 3: c = xv[3]; break;
+                case 4: c = xv[4]; break;
+                case 5: c = xv[5]; break;
+                case 6: c = xv[6]; break;
+                case 7: c = xv[7]; break;
+                case 8: c = xv[8]; break;
+                case 9: c = xv[9]; break;
+                case 10: c = xv[10]; break;
+                case 11: c = xv[11]; break;
+                default: c = xv[12]; break;
+            }
+            ppark[jp++] = elem(c, q);
+        }
+#pragma unroll
+        for (int k = 0; k < kDN; ++k)
+            if ((pany >> k) & 1u) xv[k] = d_mask4(xv[k], (uint32_t)(pnl >> (4 * k)) & 15u);
+    }
+    // PEN: fn(y, idx, k) for each penalised element of this lane's own slots,
+    // y = pen(x) of its parked logit, idx its row index, k its chunk
+    auto each_pen = [&](auto&& fn) {
+        if constexpr (PEN) {
+            uint64_t bits = pnl;
+            int jp = 0;
+            while (bits) {
+                const int i = __ffsll((long long)bits) - 1;
+                bits &= bits - 1ull;
+                const int k = i >> 2, q = i & 3;
+                fn(pen_value(ppark[jp++], pen), (uint32_t)(4 * (slot0 + 64 * k) - mis + q), k);
+            }
+        }
+    };
     const unsigned long long wmi = rscan16_u64(rv ? sh.wtm[l] : 0ull);
     const uint32_t wci = rscan_u32(rv ? sh.wtc[l] : 0u);
     const unsigned long long Z = rbcast_u64(wmi, kDW - 1);  // 2^(R - 44) units
@@ -698,9 +752,9 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
 
     // ---- the cutoff bucket's members: refined while more than kDMem ----------
     // Every float4 holding a member of b_p is on the listed side (or, when a
-    // list overflowed, in this lane's registers); fn(x4, i0, valid, pm) visits
-    // them, i0 the row index of element 0, pm (PEN) its penalised elements,
-    // which the callers skip: each_pen visits those instead.
+    // list overflowed, in this lane's registers); fn(x4, i0, valid) visits
+    // them, i0 the row index of element 0 (PEN: the penalised elements are
+    // -inf there; each_pen visits them).
     const int ne = (int)min(nq, (uint32_t)kDL);
     auto each_float4 = [&](auto&& fn) {
         if (!brute) {
@@ -708,15 +762,14 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             for (int r = 0; r < kDL / 64; ++r) {
                 if (64 * r < ne) {
                     const int je = 64 * r + l;
-                    const uint32_t ev = sh.u.l.epos[w][je];
-                    fn(sh.u.l.ent[w][je], (uint32_t)(4 * (wbase + (int)(ev & 0xFFFu)) - mis), je < ne,
-                       PEN ? ev >> 12 : 0u);
+                    fn(sh.u.l.ent[w][je], (uint32_t)(4 * (wbase + (int)(sh.u.l.epos[w][je] & 0xFFFu)) - mis),
+                       je < ne);
                 }
             }
         } else {
 #pragma unroll
             for (int k = 0; k < kDN; ++k)
-                if (k < Kw) fn(xv[k], (uint32_t)NIS_RIDXD(k), true, PEN ? (uint32_t)(pnl >> (4 * k)) & 15u : 0u);
+                if (k < Kw) fn(xv[k], (uint32_t)NIS_RIDXD(k), true);
         }
     };
     int lv = 0, B = bp;
@@ -732,11 +785,11 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         }
         const int o = B >> (6 * (lv + 1));  // the bucket's octave
         const float chiS = chiL * 64.0f, scS = scL * 64.0f;
-        each_float4([&](const f4v& x4, uint32_t i0, bool valid, uint32_t pm) {
+        each_float4([&](const f4v& x4, uint32_t i0, bool valid) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float x = elem(x4, q);
-                const bool mem = valid & (d_flr(x * chiL) == B) & !(PEN && ((pm >> q) & 1u));
+                const bool mem = valid & (d_flr(x * chiL) == B);
                 if (__ballot(mem)) {
                     const uint32_t fm = r_fm(x, chi, clo, o);
                     const uint32_t sb = (uint32_t)d_flr(x * chiS) & 63u;
@@ -746,7 +799,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                 }
             }
         });
-        each_pen([&](float, double y, uint32_t, int) {
+        each_pen([&](double y, uint32_t, int) {
             const float t = d_pt(y, chid);
             if (d_flr(t * scL) == B)
                 __hip_atomic_fetch_add(&sh.sub[(uint32_t)d_flr(t * scS) & 63u],
@@ -804,11 +857,11 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // members of the final bucket B (at most kDMem) into sh.mem
     if (!all_out && ns > 0u) {
         const int o = B >> (6 * (lv + 1));
-        each_float4([&](const f4v& x4, uint32_t i0, bool valid, uint32_t pm) {
+        each_float4([&](const f4v& x4, uint32_t i0, bool valid) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float x = elem(x4, q);
-                const bool mem = valid & (d_flr(x * chiL) == B) & !(PEN && ((pm >> q) & 1u));
+                const bool mem = valid & (d_flr(x * chiL) == B);
                 const uint64_t mb = __ballot(mem);
                 if (mb) {
                     uint32_t b0 = 0u;
@@ -818,10 +871,11 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                 }
             }
         });
-        each_pen([&](float x, double y, uint32_t idx, int) {
+        each_pen([&](double y, uint32_t idx, int) {
             if (d_flr(d_pt(y, chid) * scL) == B) {
-                const uint32_t sm = atomicAdd(&sh.nmem, 1u);
-                sh.mem[min(sm, (uint32_t)kDMem - 1u)] = RCand{x, idx | 0x80000000u, o, d_pfm(y * c64, o)};
+                const uint32_t sm = min(atomicAdd(&sh.nmem, 1u), (uint32_t)kDMem - 1u);
+                sh.mem[sm] = RCand{0.0f, idx | 0x80000000u, o, d_pfm(y * c64, o)};
+                sh.my[sm] = y;
             }
         });
     }
@@ -851,7 +905,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             const uint32_t im = PEN ? (mr.idx & 0x7FFFFFFFu) : mr.idx;
             unsigned long long Km;
             if constexpr (PEN)
-                Km = valid ? key64((mr.idx >> 31) ? pen_value(mr.x, pen) : (double)mr.x) : 0ull;
+                Km = valid ? key64((mr.idx >> 31) ? sh.my[min(l, kDMem - 1)] : (double)mr.x) : 0ull;
             else
                 Km = valid ? r_key(mr.x, mr.idx) : 0ull;
             const unsigned long long em = valid ? d_u44(mr.fm, mr.b, Ri) : 0ull;
@@ -915,9 +969,9 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // mass, from the same per-element masses the stream summed
     // (the stable-order key is compared only in a chunk holding an element
     // of the final bucket: at most kDMem of them in the row)
-    // (PEN: the penalised elements, marked in pm, count 0 here: each_pen adds
-    // their kept masses after)
-    auto kept4 = [&](const f4v& x4, uint32_t i0, uint32_t pm, float& all) {
+    // (PEN: the penalised elements, -inf here, count 0: each_pen adds their
+    // kept masses after)
+    auto kept4 = [&](const f4v& x4, uint32_t i0, float& all) {
         float e[4], k4[4];
         int F[4];
         bool inb = false;
@@ -925,7 +979,6 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         for (int q = 0; q < 4; ++q) {
             const float x = elem(x4, q);
             e[q] = r_mass(x, czh, czl, Rz);
-            if (PEN && ((pm >> q) & 1u)) e[q] = 0.0f;
             F[q] = d_flr(x * chiL);
             k4[q] = (F[q] > Bf) ? e[q] : 0.0f;
             inb |= F[q] == Bf;
@@ -968,8 +1021,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                 float orig;
                 const uint32_t ev = sh.u.l.epos[w][min(je, kDL - 1)];
                 const int ep = (int)(ev & 0xFFFu);
-                const float ks = kept4(sh.u.l.ent[w][min(je, kDL - 1)], (uint32_t)(4 * (wbase + ep) - mis),
-                                       PEN ? ev >> 12 : 0u, orig);
+                const float ks = kept4(sh.u.l.ent[w][min(je, kDL - 1)], (uint32_t)(4 * (wbase + ep) - mis), orig);
                 if (valid) esw[ep] = ks;
                 tws += valid ? (kside ? (double)ks : (double)ks - (double)orig) : 0.0;
             }
@@ -981,8 +1033,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         for (int k = 0; k < kDN; ++k) {
             if (k < Kw) {
                 float orig;
-                kvb[k] = kept4(xv[k], (uint32_t)NIS_RIDXD(k), PEN ? (uint32_t)(pnl >> (4 * k)) & 15u : 0u,
-                               orig);
+                kvb[k] = kept4(xv[k], (uint32_t)NIS_RIDXD(k), orig);
                 tws += (double)kvb[k];
             }
         }
@@ -997,7 +1048,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         }
         lds_wave_fence();
         const bool off_kept = !brute && !kside;  // their stream masses are already in tws
-        each_pen([&](float, double y, uint32_t idx, int k) {
+        each_pen([&](double y, uint32_t idx, int k) {
             const float ey = (float)pen_mass(y * c64, Rz);
             const int F = d_flr(d_pt(y, chid) * scL);
             const float ky = ((F > Bf) | ((F == Bf) & d_pkeep(key64(y), idx, kcut, kidx))) ? ey : 0.0f;
@@ -1099,8 +1150,10 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             // the same masses the float4's kept total was summed from
             // (a float4 kept whole passes every test: its elements lie above b_p)
             if constexpr (PEN) {
+                // (a penalised element's logit is parked: the j-th set bit of pnl)
                 const bool pq = (pmc >> q) & 1u;
-                const double v = pq ? pen_value(xq, pen) : (double)xq;
+                const double v =
+                    pq ? pen_value(ppark[__popcll(pnl & ((1ull << (4 * kc + q)) - 1ull))], pen) : (double)xq;
                 const float eq = pq ? (float)pen_mass(v * c64, Rz) : r_mass(xq, czh, czl, Rz);
                 const int F = pq ? d_flr(d_pt(v, chid) * scL) : d_flr(xq * chiL);
                 ev[q] = ((F > Bf) | ((F == Bf) & d_pkeep(key64(v), ib + (uint32_t)q, kcut, kidx))) ? eq : 0.0f;
@@ -1129,7 +1182,9 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             // PEN: the exact max over the plain and the penalised values, and
             // the drawn token's value after the penalty
             const double Mx = PEN ? fmax((double)unkey32(sh.kpl), unkey64(sh.kymax)) : (double)M;
-            const double vq = (PEN && ((pmc >> q) & 1u)) ? pen_value(xq, pen) : (double)xq;
+            const double vq = (PEN && ((pmc >> q) & 1u))
+                                  ? pen_value(ppark[__popcll(pnl & ((1ull << (4 * kc + q)) - 1ull))], pen)
+                                  : (double)xq;
             // 2^(R - M c): units of 2^R -> units of the max element's mass
             const double rho = exp2((double)R - Mx * c64);
             const double em = exp2(vq * c64 - Mx * c64);

@@ -357,3 +357,19 @@ def test_dense_padded_rows_and_short_vocabularies(sampler):
         ref = run_oracle(x, V, params, list(range(B)), ids, off)
         compare(gpu, ref, greedy=False)
         assert (gpu[1]["kernel"] == 1).all() and (gpu[1]["reject"] == 0).all(), (V, ld)
+
+
+def test_dense_crowded_lane_falls_back_to_the_general_path(sampler):
+    # the dense kernel parks each lane's penalised logits (at most 16 per
+    # lane, the lane's slots being 4 (64 k + l) .. + 3 of its wave's range): a
+    # history covering every element of one lane's slots declines the row,
+    # and the general path recomputes it with the same result
+    B, V = 8, 50257
+    x = _rows("normal", B)
+    crowded = np.array([256 * k + q for k in range(13) for q in range(4)])
+    gen = [crowded if r % 2 else np.arange(40000, 40016) for r in range(B)]
+    gpu, _ = _check(sampler, x, V, _params(temperature=0.8, top_p=0.97, repetition_penalty=1.3),
+                    gen, "dense crowded", on_kernel=False)
+    st = gpu[1]
+    assert (st["kernel"][0::2] == 1).all() and (st["reject"][0::2] == 0).all()
+    assert (st["kernel"][1::2] == 2).all()
