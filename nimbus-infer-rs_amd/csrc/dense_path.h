@@ -150,7 +150,7 @@ struct alignas(16) DCut {
 // history bitmaps, which are read before the stream.
 struct DList {
     f4v ent[kDW][kDL];        // listed float4s, per wave
-    uint16_t epos[kDW][kDL];  //   chunk * 64 + lane | PEN: penalised-element mask << 12
+    uint16_t epos[kDW][kDL];  //   chunk * 64 + lane
 };
 
 struct NucleusShared {
@@ -736,7 +736,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                     const uint32_t pmk = PEN ? (uint32_t)(pnl >> (4 * k)) & 15u : 0u;
                     const uint64_t sk = __ballot(pred(xv[k]) | (pmk != 0u));
                     const uint32_t s = min(nq + lane_rank(sk), (uint32_t)kDL - 1u);
-                    lds_put_x4_u16(sk, ent0 + 16 * s, xv[k], epos0 + 2 * s, (uint32_t)(k * 64 + l) | (pmk << 12));
+                    lds_put_x4_u16(sk, ent0 + 16 * s, xv[k], epos0 + 2 * s, (uint32_t)(k * 64 + l));
                     nq += (uint32_t)__popcll(sk);
                 }
             }
@@ -762,7 +762,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             for (int r = 0; r < kDL / 64; ++r) {
                 if (64 * r < ne) {
                     const int je = 64 * r + l;
-                    fn(sh.u.l.ent[w][je], (uint32_t)(4 * (wbase + (int)(sh.u.l.epos[w][je] & 0xFFFu)) - mis),
+                    fn(sh.u.l.ent[w][je], (uint32_t)(4 * (wbase + (int)sh.u.l.epos[w][je]) - mis),
                        je < ne);
                 }
             }
@@ -1019,8 +1019,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                 const int je = 64 * r + l;
                 const bool valid = je < ne;
                 float orig;
-                const uint32_t ev = sh.u.l.epos[w][min(je, kDL - 1)];
-                const int ep = (int)(ev & 0xFFFu);
+                const int ep = (int)sh.u.l.epos[w][min(je, kDL - 1)];
                 const float ks = kept4(sh.u.l.ent[w][min(je, kDL - 1)], (uint32_t)(4 * (wbase + ep) - mis), orig);
                 if (valid) esw[ep] = ks;
                 tws += valid ? (kside ? (double)ks : (double)ks - (double)orig) : 0.0;
