@@ -19,6 +19,10 @@
 #ifndef NIS_LH_NB
 #define NIS_LH_NB 4
 #endif
+// parts of h summed by separate waves at 4 tiles per wave (1, 2 or 4)
+#ifndef NIS_LH_KS
+#define NIS_LH_KS 2
+#endif
 #include "nimbus_sampler.h"
 #include "rng.h"
 
@@ -222,12 +226,12 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
 
 template <int FMT, bool VEC, bool GROUPED>
 void launch_lm_head_t(const nis::LmHeadArgs& a, int nb, dim3 grid, dim3 block, hipStream_t st) {
-    if (nb == 4)
-        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 4>), grid, block, 0, st, a);
+    if (nb == 4)  // (h split in NIS_LH_KS parts: see lm_head_kernel)
+        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 4, NIS_LH_KS>), grid, block, 0, st, a);
     else if (nb == 2)
-        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 2>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 2, 1>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 1>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((nis::lm_head_kernel<FMT, VEC, GROUPED, 1, 1>), grid, block, 0, st, a);
 }
 
 template <int FMT>
@@ -502,12 +506,16 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
     {
     // a wave: 64 vocab rows x 16*nb hidden rows; workgroups of 1 wave for
     // small batches (spread over every CU), else 4 waves split along b first
+    // (nb = 4: 4 / NIS_LH_KS tiles along b, each summed by NIS_LH_KS waves
+    // over parts of h, whole 32-wide chunks)
     const int nb = B > 16 ? NIS_LH_NB : 1;
     const int64_t nbt = ((int64_t)B + 16 * nb - 1) / (16 * nb);
-    a.wb = nb == 1 ? 1 : (nbt >= 4 ? 4 : (nbt >= 2 ? 2 : 1));
-    a.wv = nb == 1 ? 1 : 4 / a.wb;
+    const int ks = nb == 4 ? NIS_LH_KS : 1;
+    a.wb = nb == 1 ? 1 : (nbt >= 4 / ks ? 4 / ks : (nbt >= 2 ? 2 : 1));
+    a.wv = nb == 1 ? 1 : 4 / ks / a.wb;
+    a.hs = ((H / ks + 31) / 32) * 32;
     dim3 grid((unsigned)((nbt + a.wb - 1) / a.wb), (unsigned)((V + 64 * a.wv - 1) / (64 * a.wv)));
-    dim3 block((unsigned)(64 * a.wv * a.wb));
+    dim3 block((unsigned)(64 * a.wv * a.wb * ks));
     if (fmt == NIS_W_F32) launch_lm_head_f<nis::kLhF32>(a, vec, false, nb, grid, block, ctx->stream);
     else if (fmt == NIS_W_INT8) launch_lm_head_f<nis::kLhInt8>(a, vec, grouped, nb, grid, block, ctx->stream);
     else launch_lm_head_f<nis::kLhInt4>(a, vec, grouped, nb, grid, block, ctx->stream);

@@ -26,8 +26,11 @@
 //     more rounding per term, inside the f32 error bound of the sum).
 //   - Stores: accumulator r of a tile is 4 hidden rows x 16 consecutive
 //     vocab entries, 64 contiguous bytes per row.
-// No LDS, no barriers: waves outside the problem return at once; every load
-// index is clamped into the operands and every store is masked.
+// The split form (KS > 1, at 4 hidden tiles per wave) passes partial sums
+// through LDS behind one barrier; otherwise no LDS and no barriers.  Waves
+// outside the problem do no work (and, in the split form, still reach the
+// barrier); every load index is clamped into the operands and every store
+// is masked.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -51,6 +54,7 @@ struct LmHeadArgs {
     uint32_t gmagic;       // ceil(2^32 / group); 0 for group 1 (2^32 does not fit)
     int32_t wv;            // waves of a workgroup along v (wv * wb waves)
     int32_t wb;            // waves of a workgroup along b
+    int32_t hs;            // KS = 2: length of the first half of h (whole chunks)
     int64_t V;
     float* out;            // logits [B][ld] (greedy form: may be null)
     int64_t ld;
@@ -160,19 +164,29 @@ __device__ __forceinline__ lh_f4 lh_values(const LhRun& r) {
     return w;
 }
 
-template <int FMT, bool VEC, bool GROUPED, int NB>
+// KS > 1: KS waves of a workgroup share each tile, each summing one part of
+// h (a.hs long, a whole number of chunks; the last part takes the rest);
+// the accumulators of parts 1..KS-1 go through LDS and the part-0 wave adds
+// them in that fixed order as it stores.  Finer work items spread
+// the launch evenly over the SIMDs: at B = 256, V = 50257, 3144 whole tiles
+// fill 3 waves per SIMD and leave 72 over, which run on after the rest.
+template <int FMT, bool VEC, bool GROUPED, int NB, int KS>
 __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
     // runs of 4 h per lane per chunk: one for f32 (100 VGPRs, 3 waves per
     // SIMD: 260 us at B = 256 against 281 with two), two for packed codes
     // (their loads are narrower; one run was 4 % slower for int4)
     constexpr int kLhRuns = FMT == kLhF32 ? 1 : 2;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = (threadIdx.x >> 6) % (a.wv * a.wb);  // the tile's wave
+    const int ks = (threadIdx.x >> 6) / (a.wv * a.wb);    // KS > 1: its part of h
     const int r16 = lane & 15;
     const int kq = lane >> 4;
     const int64_t b0 = ((int64_t)blockIdx.x * a.wb + wave / a.wv) * (16 * NB);
     const int64_t v0 = ((int64_t)blockIdx.y * a.wv + wave % a.wv) * 64;
-    if (b0 >= a.B || v0 >= a.V) return;
+    const bool live = b0 < a.B && v0 < a.V;
+    if (KS == 1 && !live) return;
+    const int hbeg = KS == 1 ? 0 : ks * a.hs;
+    const int hend = (KS == 1 || ks == KS - 1) ? a.H : min(a.H, (ks + 1) * a.hs);
 
     int64_t vrow[4], brow[NB];
 #pragma unroll
@@ -186,27 +200,33 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = lh_f4{0.f, 0.f, 0.f, 0.f};
 
+    // KS = 1: the next chunk's loads go out before this chunk's MFMAs.  KS > 1
+    // loads each chunk as it starts it (the prefetch's registers would take
+    // the third wave per SIMD; the other waves cover the loads' latency).
+    constexpr bool kPF = KS == 1;
     lh_f4 xc[NB][kLhRuns];
     LhRun wc[4][kLhRuns];
 #pragma unroll
     for (int s = 0; s < kLhRuns; ++s) {
 #pragma unroll
-        for (int i = 0; i < NB; ++i) xc[i][s] = lh_load_x<VEC>(a, brow[i], 16 * s + 4 * kq);
+        for (int i = 0; i < NB; ++i) xc[i][s] = lh_load_x<VEC>(a, brow[i], hbeg + 16 * s + 4 * kq);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            wc[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], 16 * s + 4 * kq);
+            wc[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hbeg + 16 * s + 4 * kq);
     }
-    for (int h0 = 0; h0 < a.H; h0 += 16 * kLhRuns) {
+    for (int h0 = hbeg; live && h0 < hend; h0 += 16 * kLhRuns) {
         lh_f4 xn[NB][kLhRuns];
         LhRun wn[4][kLhRuns];
         const int hn = h0 + 16 * kLhRuns;  // past H the loads return zeros / zero codes
+        if constexpr (kPF) {
 #pragma unroll
-        for (int s = 0; s < kLhRuns; ++s) {
+            for (int s = 0; s < kLhRuns; ++s) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i) xn[i][s] = lh_load_x<VEC>(a, brow[i], hn + 16 * s + 4 * kq);
+                for (int i = 0; i < NB; ++i) xn[i][s] = lh_load_x<VEC>(a, brow[i], hn + 16 * s + 4 * kq);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                wn[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hn + 16 * s + 4 * kq);
+                for (int j = 0; j < 4; ++j)
+                    wn[j][s] = lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hn + 16 * s + 4 * kq);
+            }
         }
 #pragma unroll
         for (int s = 0; s < kLhRuns; ++s) {
@@ -225,12 +245,32 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
 #pragma unroll
         for (int s = 0; s < kLhRuns; ++s) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i) xc[i][s] = xn[i][s];
+            for (int i = 0; i < NB; ++i)
+                xc[i][s] = kPF ? xn[i][s] : lh_load_x<VEC>(a, brow[i], hn + 16 * s + 4 * kq);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) wc[j][s] = wn[j][s];
+            for (int j = 0; j < 4; ++j)
+                wc[j][s] = kPF ? wn[j][s] : lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hn + 16 * s + 4 * kq);
         }
     }
 
+    // [part - 1][tile wave][accumulator][lane]: the sums of parts 1..KS-1
+    // (KS > 1: a workgroup holds 4 / KS tile waves)
+    constexpr int kTw = KS > 1 ? 4 / KS : 1;
+    __shared__ float part[KS > 1 ? KS - 1 : 1][kTw][KS > 1 ? NB * 16 : 1][64];
+    if constexpr (KS > 1) {
+        if (ks > 0) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) part[ks - 1][wave][16 * i + 4 * j + r][lane] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (ks > 0 || !live) return;
+    }
+    // (KS > 1: the other parts are added, in order, as each value is stored)
+    const float* const pw = KS > 1 ? &part[0][wave][0][lane] : nullptr;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t v = v0 + 16 * j + r16;
@@ -243,6 +283,9 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
                 const int64_t b = b0 + 16 * i + 4 * kq + r;
                 if (b < a.B) {
                     float y = acc[i][j][r];
+#pragma unroll
+                    for (int p = 1; p < KS; ++p)  // ((part 0 + part 1) + part 2) + ...
+                        y += pw[64 * ((p - 1) * kTw * NB * 16 + 16 * i + 4 * j + r)];
                     if (FMT != kLhF32 && !GROUPED) y *= sc;  // dot * scale (quant.rs:128)
                     a.out[b * a.ld + v] = y;
                 }
