@@ -465,11 +465,11 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             }
         }
     }
-    // PEN: fn(y, k) for each penalised element of this lane's own slots
-    // (bit 4 k + q of pnl, in that order; few per lane): its logit taken from
-    // the registers, y = pen(x) in f64, k its chunk.  One copy of the code,
-    // so the per-element f64 work is not repeated for every register chunk.
-    // (Until the cutoff search; after it each_pen reads the parked values.)
+    // PEN: fn(x, k) for each penalised element of this lane's own slots
+    // (bit 4 k + q of pnl, in that order; few per lane): its logit x taken
+    // from the registers, k its chunk.  One copy of the code, so the
+    // per-element f64 work is not repeated for every register chunk.
+    // (Until the cutoff search; after it each_pen reads the parked logits.)
     auto each_pen_x = [&](auto&& fn) {
         if constexpr (PEN) {
             uint64_t bits = pnl;
@@ -497,7 +497,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
                     default: c = xv[12]; break;
                 }
                 static_assert(kDN == 13, "one case per register chunk");
-                fn(pen_value(elem(c, q), pen), k);
+                fn(elem(c, q), k);
             }
         }
     };
@@ -508,7 +508,8 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         // then summed again), then their masses into their float4s' entries
         // and Z, and their buckets, each taking back the floor bucket's count
         // its -inf added.
-        each_pen_x([&](double y, int) {
+        each_pen_x([&](float x, int) {
+            const double y = pen_value(x, pen);
             ymx = fmax(ymx, y);
             mxu = fmaxf(mxu, pen_f32_up(y));
         });
@@ -536,7 +537,8 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         }
         const int Rs = (int)Rz + 24;
         const int jflo = d_flr(tflo);
-        each_pen_x([&](double y, int k) {
+        each_pen_x([&](float x, int k) {
+            const double y = pen_value(x, pen);
             const float ey = (float)pen_mass(y * c64, Rz);
             em4w[64 * k] += ey;
             z += (double)ey;
@@ -626,30 +628,8 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // their register places, so every later register pass skips them
     float* const ppark = reinterpret_cast<float*>(&sh.ring[0]) + kDPenLane * tid;
     if constexpr (PEN) {
-        uint64_t bits = pnl;
         int jp = 0;
-        while (bits) {  // (the same select as each_pen_x)
-            const int i = __ffsll((long long)bits) - 1;
-            bits &= bits - 1ull;
-            const int k = i >> 2, q = i & 3;
-            f4v c;
-            switch (k) {
-                case 0: c = xv[0]; break;
-                case 1: c = xv[1]; break;
-                case 2: c = xv[2]; break;
-                case 3: c = xv[3]; break;
-                case 4: c = xv[4]; break;
-                case 5: c = xv[5]; break;
-                case 6: c = xv[6]; break;
-                case 7: c = xv[7]; break;
-                case 8: c = xv[8]; break;
-                case 9: c = xv[9]; break;
-                case 10: c = xv[10]; break;
-                case 11: c = xv[11]; break;
-                default: c = xv[12]; break;
-            }
-            ppark[jp++] = elem(c, q);
-        }
+        each_pen_x([&](float x, int) { ppark[jp++] = x; });
 #pragma unroll
         for (int k = 0; k < kDN; ++k)
             if ((pany >> k) & 1u) xv[k] = d_mask4(xv[k], (uint32_t)(pnl >> (4 * k)) & 15u);
