@@ -304,10 +304,13 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     __builtin_amdgcn_sched_barrier(0);
     // PEN: the raw history ids (behind chunk 0), and the bitmaps cleared
     uint32_t hid[kPHist / kPB];
+    // (too long a history declines the row; the flag is stored once the
+    // first barrier is behind, so that no wave waits for the history's
+    // length before the row's next loads go out)
+    bool hlong = false;
     if constexpr (PEN) {
-        const bool hlong = pen_load_ids(a, row, tid, hid);  // too long: the row is declined
+        hlong = pen_load_ids(a, row, tid, hid);
         pen_clear(sh.u.pb, tid);
-        if (tid == 0) sh.pover = hlong ? 1u : 0u;
     }
     {
         u4v* const rp = reinterpret_cast<u4v*>(&sh.ring[(kDRing / kDB) * tid]);
@@ -324,6 +327,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         if (PEN) {
             sh.kpl = 0u;
             sh.kymax = 0ull;
+            sh.pover = 0u;
         }
     }
     lds_barrier();
@@ -348,6 +352,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     uint64_t pnl = 0ull;
     if constexpr (PEN) {
         pen_set_bits(sh.u.pb, hid, V, mis);
+        if (tid == 0 && hlong) atomicOr(&sh.pover, 1u);
         lds_barrier();
         pen_masks<kDN>(sh.u.pb, wbase, Kw, l, pany, pnl);
     }

@@ -454,10 +454,13 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     // PEN: the raw history ids (behind chunk 0), and the bitmaps cleared
     const int tid = (int)threadIdx.x;
     uint32_t hid[kPHist / kPB];
+    // (too long a history declines the row; the flag is stored once the
+    // first barrier is behind, so that no wave waits for the history's
+    // length before the row's next loads go out)
+    bool hlong = false;
     if constexpr (PEN) {
-        const bool hlong = pen_load_ids(a, row, tid, hid);  // too long: the row is declined
+        hlong = pen_load_ids(a, row, tid, hid);
         pen_clear(sh.pb, tid);
-        if (tid == 0) sh.pover = hlong ? 1u : 0u;
     }
     *reinterpret_cast<u4v*>(&sh.hist[w * (kSHB / kSW) + 2 * l]) = u4v{0u, 0u, 0u, 0u};
     if (l < 32 * kSOctC / kSW) sh.oct[w * (32 * kSOctC / kSW) + l] = 0ull;
@@ -471,6 +474,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         sh.nmax = 0u;
         if (PEN) {
             sh.kymax = 0ull;
+            sh.pover = 0u;
             sh.kmaxp = 0u;
         }
     }
@@ -496,6 +500,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     uint64_t pnl = 0ull;
     if constexpr (PEN) {
         pen_set_bits(sh.pb, hid, V, mis);
+        if (tid == 0 && hlong) atomicOr(&sh.pover, 1u);
         lds_barrier();
         pen_masks<kSN>(sh.pb, wbase, Kw, l, pany, pnl);
     }
