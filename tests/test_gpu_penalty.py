@@ -373,3 +373,30 @@ def test_dense_crowded_lane_falls_back_to_the_general_path(sampler):
     st = gpu[1]
     assert (st["kernel"][0::2] == 1).all() and (st["reject"][0::2] == 0).all()
     assert (st["kernel"][1::2] == 2).all()
+
+
+@pytest.mark.parametrize("pen,T,p,on", [(0.5, 0.3, 0.99, False), (5.0, 1.7, 0.95, True),
+                                        (0.25, 1.0, 0.97, False), (0.8, 0.5, 0.99, True)])
+def test_dense_strong_penalties(sampler, pen, T, p, on):
+    # penalties far from 1 at low and high temperature: with penalty < 1 the
+    # penalised head rises octaves above the unpenalised max (the wave's
+    # reference moves past it after the stream), with 5 it sinks into the
+    # tail; each row's history mixes its top tokens and random ones.  At
+    # penalty 0.5 and T = 0.3 (and in some rows at 0.25 and T = 1) the head
+    # rises more than 64 octaves above a wave's first reference (at T = 0.3
+    # a logit of 12 is 58 octaves, its penalised value 115): the histogram
+    # ring cannot span that, so such a row is declined (NIS_REJECT_NONFINITE)
+    # and the general path gives the same answer.
+    B, V = 64, 50257
+    rnd = np.random.Generator(np.random.PCG64(int(pen * 100) + int(T * 10)))
+    x = _rows("normal", B)
+    order = np.argsort(-x, axis=1, kind="stable")
+    gen = [np.concatenate([order[r, : int(rnd.integers(1, 200))], rnd.integers(0, V, size=100)])
+           for r in range(B)]
+    gpu, _ = _check(sampler, x, V, _params(temperature=T, top_p=p, repetition_penalty=pen), gen,
+                    f"dense strong pen={pen} T={T} p={p}", on_kernel=on)
+    if not on:
+        st = gpu[1]
+        assert ((st["kernel"] == 1) | (st["reject"] == 2)).all(), (st["kernel"].tolist(), st["reject"].tolist())
+    drew = sum(int(gpu[0][r]) in set(gen[r].tolist()) for r in range(B))
+    print(f"[penalty] dense strong pen={pen}: rows that drew a penalised token {drew}/{B}", flush=True)
