@@ -515,6 +515,10 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
     a.wv = nb == 1 ? 1 : 4 / ks / a.wb;
     a.hs = ((H / ks + 31) / 32) * 32;
     dim3 grid((unsigned)((nbt + a.wb - 1) / a.wb), (unsigned)((V + 64 * a.wv - 1) / (64 * a.wv)));
+    if (ks > 1) {  // 1-D, the vocab tiles rounded up to whole groups of 8 (see lm_head_kernel)
+        a.gx = (int32_t)grid.x;
+        grid = dim3((unsigned)(grid.x * ((grid.y + 7) / 8) * 8), 1u);
+    }
     dim3 block((unsigned)(64 * a.wv * a.wb * ks));
     if (fmt == NIS_W_F32) launch_lm_head_f<nis::kLhF32>(a, vec, false, nb, grid, block, ctx->stream);
     else if (fmt == NIS_W_INT8) launch_lm_head_f<nis::kLhInt8>(a, vec, grouped, nb, grid, block, ctx->stream);

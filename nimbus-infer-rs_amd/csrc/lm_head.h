@@ -54,7 +54,8 @@ struct LmHeadArgs {
     uint32_t gmagic;       // ceil(2^32 / group); 0 for group 1 (2^32 does not fit)
     int32_t wv;            // waves of a workgroup along v (wv * wb waves)
     int32_t wb;            // waves of a workgroup along b
-    int32_t hs;            // KS = 2: length of the first half of h (whole chunks)
+    int32_t hs;            // KS > 1: length of each part of h but the last (whole chunks)
+    int32_t gx;            // KS > 1: workgroups along b
     int64_t V;
     float* out;            // logits [B][ld] (greedy form: may be null)
     int64_t ld;
@@ -181,8 +182,17 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
     const int ks = (threadIdx.x >> 6) / (a.wv * a.wb);    // KS > 1: its part of h
     const int r16 = lane & 15;
     const int kq = lane >> 4;
-    const int64_t b0 = ((int64_t)blockIdx.x * a.wb + wave / a.wv) * (16 * NB);
-    const int64_t v0 = ((int64_t)blockIdx.y * a.wv + wave % a.wv) * 64;
+    // KS > 1: a 1-D grid, mapped so that the a.gx workgroups of one vocab
+    // tile get ids 8 apart: the dispatcher deals ids round-robin over the 8
+    // XCDs, so they share one L2 and the tile's weights are fetched once
+    int64_t bx = blockIdx.x, by = blockIdx.y;
+    if constexpr (KS > 1) {
+        const int64_t id = blockIdx.x, k = id >> 3;
+        bx = k % a.gx;
+        by = 8 * (k / a.gx) + (id & 7);
+    }
+    const int64_t b0 = (bx * a.wb + wave / a.wv) * (16 * NB);
+    const int64_t v0 = (by * a.wv + wave % a.wv) * 64;
     const bool live = b0 < a.B && v0 < a.V;
     if (KS == 1 && !live) return;
     const int hbeg = KS == 1 ? 0 : ks * a.hs;
