@@ -340,7 +340,8 @@ def main():
     ap.add_argument("--buffers", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
-                    help="oracle worker threads (0: NIMBUS_THREADS, else min(16, cores))")
+                    help="oracle worker threads (0: threads.rs worker_count(): NIMBUS_THREADS, "
+                         "else every logical core this process may run on)")
     ap.add_argument("--decode", action="store_true",
                     help="time nis_decode_step (sample + on-device history / stop / budget "
                          "update) on the workload instead, and print that line")
@@ -531,7 +532,11 @@ def main():
                      "traffic_source": (f"{traffic_src}: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE "
                                         "per dispatch, scaled by a plain copy's reading")
                      if traffic_src else None,
-                     "kernel": kernel, "kernel_mean_us": mean_ms * 1e3,
+                     "kernel": kernel,
+                     # HIP-event interval over the timed replays / launches: the
+                     # kernel's duration plus the gap between graph nodes (the
+                     # rocprofv3 kernel durations are in profiles/)
+                     "launch_interval_us": mean_ms * 1e3,
                      "alg_bytes_per_launch": alg_bytes},
         "cpu_baseline": cpu,
         "parity": parity,

@@ -252,14 +252,18 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[i][s][c], wv[j][c],
                                                                          acc[i][j], 0, 0, 0);
         }
+        // (without prefetch the next chunk is loaded only while one is left in
+        // this part's range: the last iteration issues no loads past hend)
+        if (kPF || hn < hend) {
 #pragma unroll
-        for (int s = 0; s < kLhRuns; ++s) {
+            for (int s = 0; s < kLhRuns; ++s) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i)
-                xc[i][s] = kPF ? xn[i][s] : lh_load_x<VEC>(a, brow[i], hn + 16 * s + 4 * kq);
+                for (int i = 0; i < NB; ++i)
+                    xc[i][s] = kPF ? xn[i][s] : lh_load_x<VEC>(a, brow[i], hn + 16 * s + 4 * kq);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                wc[j][s] = kPF ? wn[j][s] : lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hn + 16 * s + 4 * kq);
+                for (int j = 0; j < 4; ++j)
+                    wc[j][s] = kPF ? wn[j][s] : lh_load_w<FMT, VEC, GROUPED>(a, vrow[j], hn + 16 * s + 4 * kq);
+            }
         }
     }
 

@@ -1,5 +1,5 @@
 // long_path.h — rows too long for the registers (53245 < V <= 2^20): one row
-// per 1024-lane workgroup (16 wave64s, four per SIMD), streamed once from
+// per 512-lane workgroup (8 wave64s, two workgroups per CU), streamed once from
 // HBM; the passes after the stream read the row again (it was just read, so
 // from L2 / the memory-side cache) instead of holding it (src/sampler.rs:163-
 // 216).

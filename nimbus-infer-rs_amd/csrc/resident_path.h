@@ -340,7 +340,10 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
                             const double y = pen_value(xv[k][q], pen);
                             const int idx = NIS_RIDX(k, q);
                             if (y != y) fs = NAN;
-                            if (y > py || (y == py && idx < pi)) {
+                            // a -inf value is never recorded: like a plain
+                            // -inf it exceeds nothing (sampler.rs:176), so an
+                            // all -inf row still returns index 0
+                            if (y > py || (y == py && y > -INFINITY && idx < pi)) {
                                 py = y;
                                 pi = idx;
                             }

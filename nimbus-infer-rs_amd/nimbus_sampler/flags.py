@@ -21,9 +21,11 @@ import numpy as np
 
 DEFAULT_SEED = 0x5DEECE66D  # engine.rs:271
 
-_FLOAT_RE = re.compile(r"^[+-]?(?:(\d+\.?\d*|\.\d+)([eE][+-]?\d+)?)$")
-_SPECIAL_RE = re.compile(r"^([+-]?)(inf|infinity|nan)$", re.IGNORECASE)
-_UINT_RE = re.compile(r"^\+?\d+$")
+# ASCII digits only, matched over the whole text (a trailing newline or a
+# non-ASCII digit is a bad number, as for Rust's str::parse)
+_FLOAT_RE = re.compile(r"[+-]?(?:(\d+\.?\d*|\.\d+)([eE][+-]?\d+)?)", re.ASCII)
+_SPECIAL_RE = re.compile(r"([+-]?)(inf|infinity|nan)", re.IGNORECASE | re.ASCII)
+_UINT_RE = re.compile(r"\+?\d+", re.ASCII)
 
 
 class FlagError(ValueError):
@@ -33,11 +35,11 @@ class FlagError(ValueError):
 def parse_f32(text: str) -> np.float32:
     """Rust's `f32::from_str`: the decimal rounded once, to nearest, ties to
     even; "inf", "infinity" and "nan" in any case, with an optional sign."""
-    m = _SPECIAL_RE.match(text)
+    m = _SPECIAL_RE.fullmatch(text)
     if m:
         sign = -1.0 if m.group(1) == "-" else 1.0
         return np.float32(np.nan) if m.group(2).lower() == "nan" else np.float32(sign * np.inf)
-    if not _FLOAT_RE.match(text):
+    if not _FLOAT_RE.fullmatch(text):
         raise FlagError(f"bad number {text!r}")
     exact = fractions.Fraction(text)
     mag = abs(exact)
@@ -63,7 +65,7 @@ def parse_f32(text: str) -> np.float32:
 
 def parse_uint(text: str, bits: int = 64) -> int:
     """Rust's `usize` / `u64` `from_str`: optional '+', decimal digits, in range."""
-    if not _UINT_RE.match(text):
+    if not _UINT_RE.fullmatch(text):
         raise FlagError(f"bad number {text!r}")
     v = int(text.lstrip("+"))
     if v >= 1 << bits:

@@ -75,9 +75,17 @@ def test_f32_parse_is_correctly_rounded():
     assert float(parse_f32("1e-45")) == float(np.float32(1e-45))  # the smallest subnormal
     for ok in (".5", "5.", "+3", "1E+2", "infinity"):
         parse_f32(ok)
-    for bad in ("", " 1", "1 ", "1e", "e5", ".", "0x10", "1_0", "--1", "in"):
+    for bad in ("", " 1", "1 ", "1e", "e5", ".", "0x10", "1_0", "--1", "in",
+                "1.5\n", "inf\n", "\u0663", "1\u0663.5"):
         with pytest.raises(FlagError):
             parse_f32(bad)
+    # usize: ASCII digits only, the whole text (str::parse rejects a trailing
+    # newline and non-ASCII digits such as ARABIC-INDIC DIGIT THREE)
+    from nimbus_sampler.flags import parse_uint
+    assert parse_uint("+5") == 5 and parse_uint("0") == 0
+    for bad in ("5\n", "\u0663", "1\u0663", "", "+", "-1", " 5"):
+        with pytest.raises(FlagError):
+            parse_uint(bad)
     # random decimals: the nearest f32, checked against exact rationals
     import fractions
     rnd = random.Random(5)

@@ -213,6 +213,23 @@ def test_greedy_ties_between_penalised_and_plain_values(sampler):
     assert all(int(gpu[0][r]) == 0 for r in range(0, B, 4))
 
 
+def test_greedy_penalised_rows_of_minus_infinity(sampler):
+    # Rows of -inf with a history (sampler.rs:172-181): nothing exceeds
+    # work[0], so the answer is index 0 whatever the history holds, also
+    # when the row is all -inf but one finite element past the history, and
+    # when a penalised -inf sits below an unpenalised finite max.
+    B, V = 6, 50257
+    x = np.full((B, V), -np.inf, np.float32)
+    x[2, 9000] = np.float32(-3.0)     # the only finite value, not penalised
+    x[3, 5] = np.float32(4.0)         # the only finite value, penalised
+    x[4, 40000] = np.float32(1.0)     # finite, and a penalised -inf before it
+    gen = [np.array([5]), np.array([5, 17, 50000]), np.array([5]), np.array([5]),
+           np.array([3, 7]), np.array([], np.int64)]
+    gpu, _ = _check(sampler, x, V, _params(temperature=0.0, repetition_penalty=1.5), gen,
+                    "greedy all -inf")
+    assert gpu[0].tolist() == [0, 0, 9000, 5, 40000, 0], gpu[0].tolist()
+
+
 @pytest.mark.parametrize("T,p", [(0.0, 1.0), (0.8, 1.0), (0.8, 0.9), (0.8, 0.97)])
 def test_non_finite_and_long_histories_fall_back(sampler, T, p):
     # NaN among the penalised logits, and histories past 4096 ids: declined,
