@@ -6,12 +6,16 @@
 // the register-resident fast path does not take (penalty, top-k, non-finite
 // input, V above its capacity) or hands on.
 //
-// Masses: without a penalty a row's masses are 2^(x*c - R) in f32 (c =
-// log2(e)/T, R = ceil(M*c)), the same values as the fast path's; with a
-// penalty the f64 value w = v/T gives 2^((w - M/T) * log2 e), evaluated as an
-// f32 exp2 of the leading part times a first-order correction for the rest
-// (relative error ~1e-7).  Sums are f64; histogram masses are 2^-40 fixed
-// point (exact and order-independent).
+// Masses: without a penalty a row's masses are 2^(x*c - R) (c = log2(e)/T
+// split as c_hi + c_lo, R = ceil(M*c_hi)), evaluated octave by octave: with
+// o = floor(x*c_hi), f32 exp2 of the small argument x*c_lo + (x*c_hi - o),
+// scaled by 2^(o - R) in f64.  The argument's rounding then costs 2^-24 of
+// an octave at any depth below the max (relative error ~1.6e-7 with exp2's
+// own), where one f32 argument x*c - R would lose 2^-24 of its depth.  With
+// a penalty the f64 value w = v/T gives 2^((w - M/T) * log2 e), evaluated as
+// an f32 exp2 of the leading part times a first-order correction for the
+// rest (relative error ~1e-7).  Sums are f64; histogram masses are 2^-40
+// fixed point (exact and order-independent).
 //
 // Sort-free top-p (sampler.rs:118-160): the reference keeps sorted position
 // pos iff D(pos) = cum_excl(pos) - q(pos) <= p (normalised).  D is
@@ -363,29 +367,50 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     };
     const uint64_t kmax = keyof(M);
 
-    // Masses (see the header): f32 2^(x*c - R) when the row has no penalty
-    // and a finite reference; otherwise relative to the max, 2^((w - M_w)
-    // log2 e).  `rho` turns the first form into units of the max element.
-    const float cf = (float)(1.4426950408889634 / temp);
+    // Masses (see the header): 2^(x*c - R) octave by octave when the row has
+    // no penalty and a finite reference; otherwise relative to the max,
+    // 2^((w - M_w) log2 e).  `rho` turns the first form into units of the
+    // max element.
+    const double c64 = 1.4426950408889634 / temp;
+    // c_hi rounded toward zero, so c_lo >= 0
+    float cf = (float)c64;
+    if ((double)cf > c64) cf = __uint_as_float(__float_as_uint(cf) - 1u);
+    const float clo = (float)(c64 - (double)cf);
     const bool mf32 = !pen && fabsf((float)M * cf) < 1e30f;
     if (SIMPLE && !mf32) return false;  // nothing written yet
     const float Rf = mf32 ? ceilf((float)M * cf) : 0.0f;
-    const double rho = mf32 ? (double)__builtin_amdgcn_exp2f(-fmaf((float)M, cf, -Rf)) : 1.0;
+    const int Ri = (int)Rf;
+    // the position of x on the value grid: x*c - R in f32, monotone in x
+    // (the histogram bins; within 2^-24 of its magnitude of the exponent)
+    // (c_lo == 0 would turn x = -inf into NaN: then c_hi alone is c)
+    auto tpos = [&](float xr) -> float {
+        const float u = fmaf(xr, cf, -Rf);
+        return clo != 0.0f ? fmaf(xr, clo, u) : u;
+    };
+    // 2^(x*c - R) in f64: exp2 of the octave-relative argument, then the
+    // exact power of two (0 for x = -inf; x is never NaN or +inf here)
+    auto massx = [&](float xr) -> double {
+        const float of = fminf(fmaxf(floorf(xr * cf), Rf - 1100.0f), Rf + 2.0f);
+        const float f = fmaf(xr, clo, fmaf(xr, cf, -of));
+        const double m = ldexp((double)__builtin_amdgcn_exp2f(f), (int)of - Ri);
+        return xr > -INFINITY ? m : 0.0;
+    };
+    const double rho = mf32 ? 1.0 / massx((float)M) : 1.0;
     auto mass_w = [&](double wv) -> double {  // wv = value / T (penalised rows)
         const double t = (wv - M_w) * 1.4426950408889634;
         const float th = (float)t;
         return (double)__builtin_amdgcn_exp2f(th) * (1.0 + (t - (double)th) * 0.6931471805599453);
     };
     auto massv = [&](double v, float xr) -> double {
-        if constexpr (SIMPLE) return (double)__builtin_amdgcn_exp2f(fmaf(xr, cf, -Rf));
-        else return mf32 ? (double)__builtin_amdgcn_exp2f(fmaf(xr, cf, -Rf)) : mass_w(v / temp);
+        if constexpr (SIMPLE) return massx(xr);
+        else return mf32 ? massx(xr) : mass_w(v / temp);
     };
     auto mass_of_key = [&](uint64_t k) -> double {
         const float xk = unkey32((uint32_t)(k >> 32));
-        if constexpr (SIMPLE) return (double)__builtin_amdgcn_exp2f(fmaf(xk, cf, -Rf));
+        if constexpr (SIMPLE) return massx(xk);
         else {
             if (pen) return mass_w(unkey64(k));
-            return mf32 ? (double)__builtin_amdgcn_exp2f(fmaf(xk, cf, -Rf)) : mass_w((double)xk / temp);
+            return mf32 ? massx(xk) : mass_w((double)xk / temp);
         }
     };
 
@@ -459,13 +484,10 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
 #pragma unroll
         for (int e = 0; e < 8; ++e) xs[e] = x[min(j0 + 64 * e, V - 1)];
     };
-    // m * 2^40 as an exact integer, m an f32 mass <= 1 (high part m * 2^8,
-    // low part the rest: both exact in f32)
-    auto fix40 = [](float m) -> unsigned long long {
-        const float hi = floorf(m * 256.0f);
-        const uint32_t lo = (uint32_t)fmaf(-hi, 4294967296.0f, m * 1099511627776.0f);
-        return ((unsigned long long)(uint32_t)hi << 32) | lo;
-    };
+    // m * 2^40 rounded down to an integer (m <= 2: an f32 mantissa times a
+    // power of two, so the product is exact in f64 and only the bits below
+    // 2^-40 are dropped)
+    auto fix40 = [](double m) -> unsigned long long { return (unsigned long long)(m * kGFix); };
     bool sums_done = false;   // kept mass of every chunk already in csum[]
     int64_t kept_pre = 0;     // and the kept count of this thread
 
@@ -488,9 +510,9 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             };
             double zl = 0.0;
             NIS_G_EACH({
-                const float t = fmaf(xr, cf, -Rf);
-                const float e = __builtin_amdgcn_exp2f(t);
-                zl += (double)e;
+                const float t = tpos(xr);
+                const double e = massx(xr);
+                zl += e;
                 const uint32_t b = vbin(t);
                 atomicAdd(&sh.u.v.cnt[b], 1u);
                 atomicAdd(&sh.u.v.mass[b], fix40(e));
@@ -498,9 +520,11 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             z_all = block_sum(zl, sh.dscr);
             const double pZ = (double)p * z_all;
             // wave 0: the lowest bin b_a passing sampler.rs:150 with the bin's
-            // upper edge 2^(-b/kGVRes) for its first element.  That edge is at
-            // least the first element's mass, so the true cutoff bin is b_a or
-            // the nonempty bin b_p above it; their members are listed next.
+            // upper edge 2^(-b/kGVRes) for its first element, raised by 2^-17
+            // for the bin position's rounding (at most 2^-24 of 64 octaves).
+            // That edge is at least the first element's mass, so the true
+            // cutoff bin is b_a or the nonempty bin b_p above it; their
+            // members are listed next.
             if (w == 0) {
                 constexpr int per = kGVBins / 64;
                 unsigned long long ltot = 0;
@@ -514,7 +538,8 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                     const int b = per * l + i;
                     const uint32_t n = sh.u.v.cnt[b];
                     const double G = above / kGFix;
-                    const double edge = (double)__builtin_amdgcn_exp2f(-(float)b / kGVRes);
+                    const double edge =
+                        (double)__builtin_amdgcn_exp2f(-(float)b / kGVRes) * (1.0 + 0x1p-17);
                     const bool q = (n != 0) && (G - edge <= pZ);
                     ba = q ? b : ba;
                     above += (double)sh.u.v.mass[b];
@@ -567,10 +592,10 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                     for (int e = 0; e < 8; ++e) {
                         const int64_t j = cc * kGChunk + 64 * e + l;
                         const bool inr = j < V;
-                        const float t = fmaf(xs[e], cf, -Rf);
+                        const float t = tpos(xs[e]);
                         const int b = (int)vbin(t);
                         const bool sure = inr & (b < bTop);
-                        sl += sure ? (double)__builtin_amdgcn_exp2f(t) : 0.0;
+                        sl += sure ? massx(xs[e]) : 0.0;
                         nsure += sure ? 1 : 0;
                         const bool in = inr & ((b == bA) | (b == bP));
                         diff |= in ? ((uint64_t)(key32(xs[e]) ^ kref) << 32) : 0ull;
@@ -606,8 +631,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                                 if (in_prefix(k, shift, prefix)) {
                                     const int d = (int)((k >> shift) & 255);
                                     atomicAdd(&sh.hcnt[d], 1u);
-                                    atomicAdd(&sh.hmass[d],
-                                              (unsigned long long)((double)__builtin_amdgcn_exp2f(fmaf(xl, cf, -Rf)) * kGFix));
+                                    atomicAdd(&sh.hmass[d], fix40(massx(xl)));
                                     atomicMax(&sh.hkey[d], (unsigned long long)k);
                                 }
                             }
@@ -650,8 +674,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                             const uint64_t k = (uint64_t)key32(xl) << 32;
                             if (k >= kstar) {
                                 const uint32_t jl = sh.u.v.li[i][tid];
-                                atomicAdd(&sh.csum[jl / kGChunk],
-                                          fix40(__builtin_amdgcn_exp2f(fmaf(xl, cf, -Rf))));
+                                atomicAdd(&sh.csum[jl / kGChunk], fix40(massx(xl)));
                                 ++nkl;
                             }
                         }

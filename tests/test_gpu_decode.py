@@ -116,6 +116,11 @@ def _run(sampler, B, V, steps, cap, params_kw, seed, kernels=None, sigma=2.0):
     # histories smaller than the steps: a full history ends the sequence
     (4096, dict(temperature=0.9, top_p=0.9, repetition_penalty=1.3), 3),
     (50257, dict(temperature=0.8, top_p=0.9), 3),
+    # rows longer than the registers (the long-row kernel, whose penalised
+    # rows are finished by the general path through the pending launch)
+    (128256, dict(temperature=0.8, top_p=0.9, repetition_penalty=1.3), 8),
+    (128256, dict(temperature=0.0, repetition_penalty=1.2), 3),
+    (128256, dict(temperature=0.8, top_p=1.0, repetition_penalty=0.8), 8),
 ])
 def test_decode_steps_match_oracle_loop(sampler, V, kw, cap):
     diverged, n_done, n_started, n_full = _run(sampler, B=24, V=V, steps=7, cap=cap,

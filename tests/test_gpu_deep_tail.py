@@ -5,7 +5,9 @@ tail holds a large share of the mass and many rows draw a token 16-24 octaves
 below the maximum.  The mass 2^(t) of such a token must still match the
 oracle's exp(w - max) (sampler.rs:201-205) within 1e-6 relative: the
 probability of the drawn token and the kept mass are checked on every drawn
-row, at T = 1 and T = 0.3, with top-p off and at 0.99.
+row, at T = 1 and T = 0.3, with top-p off and at 0.99.  The same rows with
+top-k = V - 1 on rows longer than the register kernels hold run the general
+path (its octave-relative masses), which every declined row also takes.
 """
 import numpy as np
 import pytest
@@ -65,4 +67,31 @@ def test_deep_tail_probabilities(sampler, V, T, top_p, lo, hi, B):
     rep["deepest_draw_octaves"] = float(depth.max())
     print(f"[deep-tail] -> {rep}", flush=True)
     # the workload must actually exercise the deep tail
+    assert drawn_deep >= 4, rep
+
+
+@pytest.mark.parametrize("V,T,top_p,lo,hi,B", [
+    (60000, 0.3, 1.0, 11.0, 13.0, 96),
+    (60000, 0.3, 0.99, 11.0, 16.0, 96),
+    (128256, 1.0, 0.99, 13.5, 14.5, 96),
+])
+def test_deep_tail_probabilities_general_path(sampler, V, T, top_p, lo, hi, B):
+    # top-k = V - 1 (sampler.rs:103-116) removes the row minimum only; the
+    # rows run sample_rows_kernel (the general path), whose masses must meet
+    # the same 1e-6 bar 16-24 octaves below the max
+    import nimbus_sampler as ns
+    x = deep_tail_rows(B, V, T, lo, hi, seed=7 * V + int(100 * T) + int(100 * top_p))
+    params = ns.SamplingParams(temperature=T, top_p=top_p, top_k=V - 1)
+    seeds = list(range(4000, 4000 + B))
+    print(f"[deep-tail general] B={B} V={V} T={T} p={top_p} k={V - 1} depth [{lo},{hi}) nats",
+          flush=True)
+    gpu = run_gpu(sampler, x, V, params, seeds)
+    ref = run_oracle(x, V, params, seeds)
+    rep = compare(gpu, ref, greedy=False)
+    assert (gpu[1]["kernel"] == 2).all(), gpu[1]["kernel"].tolist()
+    depth = tail_depth_octaves(x, ref[0], T)
+    drawn_deep = int((depth >= 16.0).sum())
+    rep["rows_drawing_16_octaves_deep"] = drawn_deep
+    rep["deepest_draw_octaves"] = float(depth.max())
+    print(f"[deep-tail general] -> {rep}", flush=True)
     assert drawn_deep >= 4, rep
