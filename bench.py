@@ -53,6 +53,9 @@ def routed_kernel(V, temperature, top_k, top_p, penalty, history=False):
     if res_shape and temperature > 0.0 and no_topk and 0.95 <= top_p < 1.0 \
             and (penalty == 1.0 or not history):
         return "sample_rows_dense_kernel"
+    if 256 <= V <= SPARSE_MAX_V and temperature > 0.0 and top_p > 0.0 and not no_topk \
+            and not (penalty != 1.0 and history):
+        return "sample_rows_sparse_topk_kernel"
     if 256 <= V <= SPARSE_MAX_V and temperature > 0.0 and 0.0 < top_p < 0.95 and no_topk:
         if penalty != 1.0 and history:
             return "sample_rows_sparse_pen_kernel"
@@ -345,6 +348,9 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="time nis_decode_step (sample + on-device history / stop / budget "
                          "update) on the workload instead, and print that line")
+    ap.add_argument("--top-k", type=int, default=0,
+                    help="top-k of every row (sampler.rs:103-116) on top of the workload's "
+                         "temperature and top-p; the line's metric then names it")
     ap.add_argument("--penalty", type=float, default=1.0,
                     help="repetition penalty of --decode (sampler.rs:83-101; the histories "
                          "are the penalty lists)")
@@ -402,7 +408,7 @@ def main():
     sampler = ns.Sampler(0)
     temp = args.temperature if (args.decode and args.temperature is not None) else w.temperature
     top_p = args.top_p if (args.decode and args.top_p is not None) else w.top_p
-    params = ns.SamplingParams(temperature=temp, top_p=top_p,
+    params = ns.SamplingParams(temperature=temp, top_p=top_p, top_k=args.top_k,
                                repetition_penalty=args.penalty if args.decode else 1.0)
 
     host0 = w.make(B)
@@ -429,7 +435,8 @@ def main():
         g = sampler.argmax_batch(bufs[0])
         torch.cuda.synchronize()
         ref_states = oracle.rng_states(w.seeds)
-        rt, rs, _ = oracle.sample_batch(host0, V, oracle.make_params(w.temperature, w.top_p), ref_states)
+        rt, rs, _ = oracle.sample_batch(host0, V, oracle.make_params(w.temperature, w.top_p, args.top_k),
+                                        ref_states)
         gt, _, _ = oracle.sample_batch(host0, V, oracle.make_params(0.0), oracle.rng_states(w.seeds))
         got = tokens.cpu().numpy().astype(np.uint32)
         boundary = (rs["topp_margin"] <= 1e-6) | (rs["cdf_margin"] <= 1e-6)
@@ -486,14 +493,15 @@ def main():
 
     alg_bytes = B * (4 * V + 68)
     achieved = alg_bytes / (mean_ms * 1e-3) / 1e9
-    kernel = routed_kernel(V, w.temperature, 0, w.top_p, 1.0)
-    traffic, traffic_src = read_traffic(args.workload, kernel)
+    kernel = routed_kernel(V, w.temperature, args.top_k, w.top_p, 1.0)
+    traffic, traffic_src = read_traffic(
+        args.workload if not args.top_k else f"{args.workload}_topk{args.top_k}", kernel)
 
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import oracle
         nthreads = args.cpu_threads or reference_worker_count()
-        p = oracle.make_params(w.temperature, w.top_p)
+        p = oracle.make_params(w.temperature, w.top_p, args.top_k)
         times = []
         for rep in range(6):
             st = oracle.rng_states(w.seeds)
@@ -509,8 +517,11 @@ def main():
                          f"after 1 warm-up",
                "gbs": alg_bytes / med / 1e9, "host": host_cpu()}
 
+    metric = METRIC if (args.workload == "headline" and not args.top_k) else \
+        (f"sampled rows/s + HBM GB/s (% peak), B={B} x V={V} fp32, T={w.temperature} "
+         f"top-p={w.top_p}" + (f" top-k={args.top_k}" if args.top_k else ""))
     out = {
-        "metric": METRIC,
+        "metric": metric,
         "value": B * K / wall,
         "unit": "rows/s",
         "n_gpus": 1,
@@ -523,7 +534,7 @@ def main():
         "dtype": "fp32",
         "data": "synthetic: N(0,3^2) logits from PCG64 seed 7, 8 rotated batches resident in HBM",
         "config": {"workload": args.workload, "B": B, "V": V, "temperature": w.temperature,
-                   "top_p": w.top_p, "ld": V, "parallelism": "1 GPU",
+                   "top_p": w.top_p, "top_k": args.top_k, "ld": V, "parallelism": "1 GPU",
                    "launch": f"hipGraph replays: {K // G} x {G} + {K % G} nis_sample_batch "
                              f"launches",
                    "eager_rows_per_s": eager_rows_s},

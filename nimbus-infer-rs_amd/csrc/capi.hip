@@ -160,12 +160,16 @@ nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_pa
 //     or its penalty variant for a launch with a penalty history;
 //   - 0 < top-p < 0.95, no top-k: the 1024-lane sparse kernel (few kept
 //     tokens, listed against a sampled threshold);
+//   - 0 < top-k < V with any top-p > 0 and no penalty history: the sparse
+//     kernel's top-k form (the k-th largest found by count in the same
+//     histograms, top-p searched on the top-k mass);
 //   - V > 53245 (rows longer than the registers hold), no top-k: the
 //     512-lane long-row kernel (greedy, top-p off or top-p, the row read
 //     again from cache after its stream), then the general path on the rows
 //     it declined;
-//   - anything else (top-k, V < 256, top-p <= 0, a penalty history on rows
-//     longer than the registers hold): the 512-lane general kernel.
+//   - anything else (V < 256, top-p <= 0, top-k with a penalty history or
+//     past 53245, a penalty history on rows longer than the registers hold):
+//     the 512-lane general kernel.
 // A row one of these kernels cannot prove (non-finite values, capacity,
 // exact-tie overflow, a history past the bitmaps) runs the general path
 // inside whichever kernel was launched.
@@ -201,6 +205,11 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
                a.top_p < 0.95f && no_topk) {
         // a repetition-penalty history: applied inside the sparse path
         hipLaunchKernelGGL(nis::sample_rows_sparse_pen_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
+                           ctx->stream, a);
+    } else if (a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f && a.top_p > 0.0f && !no_topk &&
+               (a.penalty == 1.0f || a.gen_ids == nullptr)) {
+        // top-k (with top-p at any p > 0): found by count in the sparse path
+        hipLaunchKernelGGL(nis::sample_rows_sparse_topk_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
                            ctx->stream, a);
     } else if (a.V > nis::kDMaxV &&
                (a.temperature <= 0.0f || (no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)))) {

@@ -8,8 +8,9 @@
 namespace nis {
 
 // One 512-lane workgroup per row on the general path: the launches no
-// row kernel takes (top-k, V < 256, top-p <= 0, a penalty history on rows
-// longer than the registers hold).
+// row kernel takes (V < 256, top-p <= 0, top-k with a penalty history or on
+// rows longer than the registers hold, a penalty history on rows longer
+// than the registers hold).
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(RowArgs a) {
     __shared__ GeneralShared sh;
     const int row = (int)blockIdx.x;
@@ -21,8 +22,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(RowArgs a) {
 // path declines (or cannot take) runs the general path on the first 512
 // lanes; the other waves leave first, so the general path's barriers count
 // only its own eight waves.  PEN: the launch carries a repetition-penalty
-// history, applied inside the sparse path.
-template <bool PEN>
+// history, applied inside the sparse path.  TOPK: the launch carries a top-k
+// (sampler.rs:103-116), applied inside the sparse path.
+template <bool PEN, bool TOPK = false>
 __device__ __forceinline__ void sparse_rows_body(const RowArgs& a) {
     __shared__ union {
         GeneralShared g;
@@ -33,8 +35,8 @@ __device__ __forceinline__ void sparse_rows_body(const RowArgs& a) {
     asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
                  "s"(a.penalty), "s"(a.top_k), "s"(a.gen_ids), "s"(a.gen_off));
     uint32_t reject = NIS_REJECT_SHAPE;
-    if (sparse_eligible<PEN>(a, row)) {
-        reject = sparse_row<PEN>(a, row, sh.s);
+    if (sparse_eligible<PEN, TOPK>(a, row)) {
+        reject = sparse_row<PEN, TOPK>(a, row, sh.s);
         if (reject == NIS_REJECT_NONE) return;
     }
     if (threadIdx.x >= kBlock) return;
@@ -46,6 +48,9 @@ __global__ __launch_bounds__(kSB) void sample_rows_sparse_kernel(RowArgs a) {
 }
 __global__ __launch_bounds__(kSB) void sample_rows_sparse_pen_kernel(RowArgs a) {
     sparse_rows_body<true>(a);
+}
+__global__ __launch_bounds__(kSB) void sample_rows_sparse_topk_kernel(RowArgs a) {
+    sparse_rows_body<false, true>(a);
 }
 
 // General path only (used by tests to cross-check the two paths).

@@ -161,6 +161,8 @@ struct WideShared {
     double seg[kSW][64];           // kept mass above b_p per lane segment of the entry lists
     double tw[kSW];                // per-wave kept mass (2^(R-40) units, integers)
     SMem mem[kSMem];               // members of b_p
+    SMem kmem[kSMem];              // TOPK: members of b_k (when the k-th largest splits it)
+    uint32_t nkmem;
     SRec rec[kSW];
     SCut cut;
     double u0;                     // the draw
@@ -388,12 +390,18 @@ __device__ __forceinline__ void lds_put2_u32_m(uint64_t mask, uint32_t a, uint32
 }
 
 // PEN: the row may carry a penalty history (its length is checked inside,
-// so no load waits before the stream starts).
-template <bool PEN>
+// so no load waits before the stream starts).  TOPK: 0 < top_k < V, and any
+// top-p above 0 (at 1 or more, top-p is off and the k largest are kept).
+template <bool PEN, bool TOPK = false>
 __device__ __forceinline__ bool sparse_eligible(const RowArgs a, int row) {
+    static_assert(!(PEN && TOPK), "a penalty history with top-k runs the general path");
     if (a.V < 256 || a.V > kSMaxV) return false;
-    if (!(a.temperature > 0.0f) || !(a.top_p > 0.0f) || !(a.top_p < 1.0f)) return false;
-    if (a.top_k > 0 && a.top_k < (uint64_t)a.V) return false;
+    if (!(a.temperature > 0.0f) || !(a.top_p > 0.0f)) return false;
+    if (TOPK) {
+        if (!(a.top_k > 0 && a.top_k < (uint64_t)a.V)) return false;
+    } else {
+        if (!(a.top_p < 1.0f) || (a.top_k > 0 && a.top_k < (uint64_t)a.V)) return false;
+    }
     if (PEN) return true;
     int64_t g0 = 0, g1 = 0;
     if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) return false;
@@ -414,7 +422,17 @@ __device__ __forceinline__ bool sparse_eligible(const RowArgs a, int row) {
 // to the f32 bucket rule on unpenalised values).  After the cutoff they join
 // the segment sums, the members (ranked on f64 keys) and the final walk,
 // placed by row index.
-template <bool PEN>
+//
+// TOPK (top_k_filter, sampler.rs:103-116, then top-p on what it keeps): once
+// the histograms are complete every wave finds the bucket b_k holding the
+// k-th largest element by counting down from the top (the buckets are
+// monotone in x, so the k largest are the buckets above b_k and the largest
+// members of b_k).  When b_k's members straddle the k-th (two or more of
+// them, more than k in b_k and above), they are listed and ranked, and the
+// k-th largest value decides: members at or above it are kept (ties with it
+// included), the rest removed.  The top-p cutoff is then searched with
+// p Z_k, Z_k the mass kept by top-k, and never below b_k.
+template <bool PEN, bool TOPK = false>
 __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, WideShared& sh) {
     const int l = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -466,6 +484,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     if (l < 32 * kSOctC / kSW) sh.oct[w * (32 * kSOctC / kSW) + l] = 0ull;
     if (w == 0 && l == 0) {
         sh.nmem = 0u;
+        sh.nkmem = 0u;
         sh.cnt2 = 0u;
         sh.kmax = 0u;
         sh.kxlo = 0u;
@@ -788,6 +807,119 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const int li = min(l, kSW - 1);
     const bool rv = l < kSW;
     lds_barrier();
+    // ---- TOPK: b_k, the bucket of the k-th largest, by count (every wave) --
+    int bk = 0;             // its bucket
+    uint32_t kthk = 0u;     // key32 of the k-th largest value (0: all of b_k kept)
+    uint32_t ck = 0u;       // candidates above b_k
+    uint32_t nbk = 0u;      // candidates in b_k
+    double gk = 0.0;        // their mass above b_k, and b_k's kept mass (2^(R-40) units)
+    double zbk = 0.0;
+    uint32_t krej = NIS_REJECT_NONE;
+    if constexpr (TOPK) {
+        const uint64_t K = a.top_k;
+        const float M = unkey32(sh.kmax);
+        const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
+        const int Ri = (int)R;
+        const float xlo = unkey32(sh.kxlo);
+        const bool fin = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * c) < 1e6f);
+        const bool xfin = fin & (xlo < INFINITY) & (xlo <= M * c);
+        const int blo = xfin ? (int)(xlo * (float)kSRes) : 0;
+        const int bM = xfin ? s_bucket(M * c) : 0;
+        const int oM = bM >> kSLog, olo = blo >> kSLog;
+        if (!xfin || oM - olo > 30) {
+            krej = NIS_REJECT_CAPACITY;  // (wave 0's checks below decline the row too)
+        } else {
+            // lane l: octave oM - l; octave olo counts its buckets >= blo only
+            // (every candidate there is listed), as the cutoff search does
+            const int o = oM - l;
+            const bool oin = l <= oM - olo;
+            unsigned long long ovr = 0ull;
+            if (oin && o != olo) {
+                const u4v* const oc = reinterpret_cast<const u4v*>(&sh.oct[kSOctC * ((uint32_t)o & 31u)]);
+#pragma unroll
+                for (int j = 0; j < kSOctC / 2; ++j) {
+                    const u4v q = oc[j];
+                    ovr += (((unsigned long long)q.y << 32) | q.x) + (((unsigned long long)q.w << 32) | q.z);
+                }
+            }
+            const int bl = kSRes * olo + l;
+            const unsigned long long lv = (bl >= blo && bl <= bM) ? sh.hist[(uint32_t)bl & (kSHB - 1)] : 0ull;
+            const unsigned long long lsum = bcast_u64(wscan_u64(lv), 63);
+            const unsigned long long ov = (o == olo) ? lsum : ovr;
+            const uint32_t on = oin ? (uint32_t)(ov >> 48) : 0u;
+            const double om = oin ? s_m40(ov & 0xFFFFFFFFFFFFull, o, Ri) : 0.0;
+            const uint32_t cincl = wscan_u32(on);
+            const double mincl = wscan_f64(om);
+            const uint64_t hit = __ballot(oin & ((uint64_t)cincl >= K));
+            if (!hit) {
+                krej = NIS_REJECT_WINDOW;  // the k-th largest lies below the listed range
+            } else {
+                const int lk = __ffsll((long long)hit) - 1;
+                const uint32_t CO = bcast_u32(cincl - on, lk);
+                const double GO = bcast_f64(mincl - om, lk);
+                const int O = oM - lk;
+                // lane l: bucket 64 O + 63 - l (descending)
+                const int b = kSRes * O + (kSRes - 1) - l;
+                const bool bin = (b >= blo) & (b <= bM);
+                const unsigned long long bv = bin ? sh.hist[(uint32_t)b & (kSHB - 1)] : 0ull;
+                const uint32_t bn = (uint32_t)(bv >> 48);
+                const double bm = s_m40(bv & 0xFFFFFFFFFFFFull, O, Ri);
+                const uint32_t bci = wscan_u32(bn);
+                const double bmi = wscan_f64(bm);
+                const uint64_t hb = __ballot((uint64_t)(CO + bci) >= K);
+                if (!hb) {
+                    krej = NIS_REJECT_BUCKET;  // octave and bucket counts disagree (ring overlap)
+                } else {
+                    const int lb = __ffsll((long long)hb) - 1;
+                    bk = kSRes * O + (kSRes - 1) - lb;
+                    ck = CO + bcast_u32(bci - bn, lb);
+                    nbk = bcast_u32(bn, lb);
+                    gk = GO + bcast_f64(bmi - bm, lb);
+                    zbk = bcast_f64(bm, lb);
+                    // (b_k may lie more than 16 octaves below R: its masses and
+                    // those above it are then truncated to 2^(R-40) units in
+                    // Z_k, far below the cutoff's resolution; the kept range,
+                    // b_p and above, must still lie within those 16 octaves)
+                }
+            }
+        }
+        if (krej == NIS_REJECT_NONE && nbk >= 2u && (uint64_t)ck + nbk > K) {
+            // (uniform: every wave computed the same b_k) the k-th largest is
+            // inside b_k: every wave lists its members of b_k, then each wave
+            // ranks them (descending value, then ascending index)
+#pragma unroll
+            for (int r = 0; r < kSRounds; ++r) {
+                if (r < nrd && cbk[r] != kSNone && ((int)cbk[r] >> 4) == bk) {
+                    const uint32_t bit = cbk[r] & 15u;
+                    const int e = e0 + (int)(bit >> 2), q = (int)(bit & 3u);
+                    const float xq = reinterpret_cast<const float*>(&sh.ent[w][e])[q];
+                    const uint32_t iq = (uint32_t)(4 * (wbase + (int)sh.epos[w][e]) - mis + q);
+                    const uint32_t slot = atomicAdd(&sh.nkmem, 1u);
+                    if (slot < (uint32_t)kSMem) sh.kmem[slot] = SMem{xq, iq, cfm[r], 0u};
+                }
+            }
+            lds_barrier();
+            const uint32_t nk = sh.nkmem;
+            if (nk > (uint32_t)kSMem || nk != nbk) {
+                krej = NIS_REJECT_BUCKET;
+            } else {
+                const int n = (int)nk;
+                const bool valid = l < n;
+                const SMem mm = sh.kmem[min(l, kSMem - 1)];
+                const unsigned long long Km =
+                    valid ? (((unsigned long long)key32(mm.x) << 32) | (uint32_t)~mm.idx) : 0ull;
+                uint32_t rk = 0u;  // members ahead of this one
+                for (int j = 0; j < n; ++j) rk += (bcast_u64(Km, j) > Km) ? 1u : 0u;
+                // the k-th largest: rank k - ck - 1 among b_k's members
+                const uint64_t kl = __ballot(valid & ((uint64_t)rk + ck + 1u == K));
+                kthk = key32(bcast_f32(mm.x, kl ? __ffsll((long long)kl) - 1 : 0));
+                const float M = unkey32(sh.kmax);
+                const int Ri = (int)((M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f);
+                const bool live = valid & (key32(mm.x) >= kthk);
+                zbk = wsum_f64(live ? s_m40(mm.fm, (int)floorf(mm.x * c), Ri) : 0.0);
+            }
+        }
+    }
     if (w == 0) {
         NIS_STS(3);
         __builtin_amdgcn_s_setprio(3);
@@ -824,13 +956,15 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
         // a wave whose reference sits far below the row max may have overflowed
         const bool range_ok = fmaf(M, c, -unkey32(sh.krwmin)) <= 120.0f;
-        const double pz = (double)p * ZR * kS40;
+        // TOPK: top-p runs on the mass top-k keeps (off at p >= 1)
+        const double pz = TOPK ? (p >= 1.0f ? (double)INFINITY : (double)p * (gk + zbk))
+                               : (double)p * ZR * kS40;
         NIS_STS1(8);
         SCut cut;
         cut.reject = NIS_REJECT_NONE;
         cut.gp = 0.0;
         cut.pz = pz;
-        cut.zr = ZR;
+        cut.zr = TOPK ? (p >= 1.0f ? 0.0 : (gk + zbk) / kS40) : ZR;
         cut.bp = 0;
         cut.nabove = 0u;
         cut.M = M;
@@ -857,7 +991,8 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const uint64_t NEo = __ballot(oin & (on != 0u));
             // everything below blo is removed: G(blo - 1) - m_up(blo - 1) > p Z
             // (and every sum of kept masses stays an exact f64 integer: below 2^52)
-            const bool lo_ok = (gtot - s_mup(blo - 1, Ri) > pz) & (gtot < 4503599627370496.0);
+            // (TOPK: everything below b_k >= blo is removed by top-k)
+            const bool lo_ok = (TOPK || (gtot - s_mup(blo - 1, Ri) > pz)) & (gtot < 4503599627370496.0);
             if (!P || !lo_ok) {
                 cut.reject = NIS_REJECT_WINDOW;
             } else {
@@ -903,9 +1038,17 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                     cut.bp = (int32_t)bcast_u32((uint32_t)bsel, L);
                     cut.gp = bcast_f64(gsel, L);
                     cut.nabove = bcast_u32(csel, L);
+                    uint32_t nbp = bcast_u32(nsel, L);
+                    if (TOPK && cut.bp < bk) {  // no cutoff below the k-th largest
+                        cut.bp = bk;
+                        cut.gp = gk;
+                        cut.nabove = ck;
+                        nbp = nbk;
+                    }
                     // the kept range stays within 16 octaves of R (exact fixed point)
                     if ((cut.bp >> kSLog) < Ri - 16) cut.reject = NIS_REJECT_WINDOW;
-                    else if (bcast_u32(nsel, L) > (uint32_t)kSMem) cut.reject = NIS_REJECT_BUCKET;
+                    else if (nbp > (uint32_t)kSMem) cut.reject = NIS_REJECT_BUCKET;
+                    if (TOPK && krej != NIS_REJECT_NONE) cut.reject = krej;
                 }
             }
         }
@@ -1031,9 +1174,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
 
     const double pz = cut.pz, gp = cut.gp;
     const int n = (int)min(sh.nmem, (uint32_t)kSMem);
-    const bool valid = l < n;
     const u4v mr = *reinterpret_cast<const u4v*>(&sh.mem[min(l, kSMem - 1)]);
     const float xm = __uint_as_float(mr.x);
+    // (TOPK: members of b_k below the k-th largest value are removed)
+    const bool valid = (l < n) & (!TOPK || bp != bk || key32(xm) >= kthk);
     const uint32_t im = mr.y;
     double ym = 0.0;  // PEN: the member's value in f64
     if constexpr (PEN) ym = sh.memy[min(l, kSMem - 1)];

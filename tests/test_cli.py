@@ -71,7 +71,9 @@ def test_bench_routing_constants_match_the_library():
     assert b.routed_kernel(50257, 0.8, 0, 0.9, 1.0) == "sample_rows_sparse_kernel"
     assert b.routed_kernel(50257, 0.0, 0, 0.9, 1.0).endswith("<greedy>")
     assert b.routed_kernel(50257, 1.0, 0, 1.0, 1.0).endswith("<all>")
-    assert b.routed_kernel(50257, 0.7, 50, 1.0, 1.0) == "sample_rows_kernel"
+    assert b.routed_kernel(50257, 0.7, 50, 1.0, 1.0) == "sample_rows_sparse_topk_kernel"
+    assert b.routed_kernel(50257, 0.7, 50, 0.9, 1.3, history=True) == "sample_rows_kernel"
+    assert b.routed_kernel(128256, 0.7, 50, 0.9, 1.0) == "sample_rows_kernel"
 
 
 def test_bench_refuses_more_than_one_gpu():
