@@ -142,14 +142,21 @@ struct alignas(16) SMem {
 // Result of the cutoff search (written by wave 0 between barriers).
 struct alignas(16) SCut {
     double gp;        // mass of the buckets above b_p (2^(R-40) units, an integer)
-    double pz;        // p * Z (2^(R-40) units)
+    double pz;        // p * Z (2^(R-40) units; TOPK with split: p * its upper bound)
     double zr;        // Z (units of 2^R)
+    double gk;        // TOPK: mass of the buckets above b_k
     int32_t bp;       // b_p
     uint32_t nabove;  // candidates above b_p
     uint32_t reject;
     float M;          // row max logit
     float R;          // ceil(M c)
-    uint32_t pad[3];
+    int32_t bk;       // TOPK: bucket of the k-th largest
+    uint32_t ck;      //   candidates above it
+    uint32_t nbk;     //   candidates in it
+    uint32_t split;   //   1: its members straddle the k-th (ranked at the walk)
+    int32_t bpd;      // deepest bucket the cutoff may lie in (b_p otherwise; TOPK
+                      //   with split: [bpd, bp] covers the exact p Z_k)
+    uint32_t pad[2];
 };
 
 struct WideShared {
@@ -216,6 +223,15 @@ __device__ __forceinline__ double s_mup(int b, int R) {
     return ldexp((double)__builtin_amdgcn_exp2f((float)((b + 1) & (kSRes - 1)) * (1.0f / kSRes)) *
                      1.0001,
                  ((b + 1) >> kSLog) - R + 40);
+}
+// Lower bound of the 2^(R - 40)-unit mass of any element in bucket b (its
+// lower edge, deflated for the roundings of x*c and exp2 and, more than 16
+// octaves below R, for the truncation of s_m40).
+__device__ __forceinline__ double s_mdn(int b, int R) {
+    const double m = ldexp((double)__builtin_amdgcn_exp2f((float)(b & (kSRes - 1)) * (1.0f / kSRes)) /
+                               1.0001,
+                           (b >> kSLog) - R + 40);
+    return fmax(m - 1.0, 0.0);
 }
 // Octave-relative fixed-point mass of a penalised element: 2^(yc - floor(t))
 // * 2^24 with t = (float)yc, as s_fm is for an f32 logit.
@@ -807,119 +823,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const int li = min(l, kSW - 1);
     const bool rv = l < kSW;
     lds_barrier();
-    // ---- TOPK: b_k, the bucket of the k-th largest, by count (every wave) --
-    int bk = 0;             // its bucket
-    uint32_t kthk = 0u;     // key32 of the k-th largest value (0: all of b_k kept)
-    uint32_t ck = 0u;       // candidates above b_k
-    uint32_t nbk = 0u;      // candidates in b_k
-    double gk = 0.0;        // their mass above b_k, and b_k's kept mass (2^(R-40) units)
-    double zbk = 0.0;
-    uint32_t krej = NIS_REJECT_NONE;
-    if constexpr (TOPK) {
-        const uint64_t K = a.top_k;
-        const float M = unkey32(sh.kmax);
-        const float R = (M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f;
-        const int Ri = (int)R;
-        const float xlo = unkey32(sh.kxlo);
-        const bool fin = (M > -INFINITY) & (M < INFINITY) & (fabsf(M * c) < 1e6f);
-        const bool xfin = fin & (xlo < INFINITY) & (xlo <= M * c);
-        const int blo = xfin ? (int)(xlo * (float)kSRes) : 0;
-        const int bM = xfin ? s_bucket(M * c) : 0;
-        const int oM = bM >> kSLog, olo = blo >> kSLog;
-        if (!xfin || oM - olo > 30) {
-            krej = NIS_REJECT_CAPACITY;  // (wave 0's checks below decline the row too)
-        } else {
-            // lane l: octave oM - l; octave olo counts its buckets >= blo only
-            // (every candidate there is listed), as the cutoff search does
-            const int o = oM - l;
-            const bool oin = l <= oM - olo;
-            unsigned long long ovr = 0ull;
-            if (oin && o != olo) {
-                const u4v* const oc = reinterpret_cast<const u4v*>(&sh.oct[kSOctC * ((uint32_t)o & 31u)]);
-#pragma unroll
-                for (int j = 0; j < kSOctC / 2; ++j) {
-                    const u4v q = oc[j];
-                    ovr += (((unsigned long long)q.y << 32) | q.x) + (((unsigned long long)q.w << 32) | q.z);
-                }
-            }
-            const int bl = kSRes * olo + l;
-            const unsigned long long lv = (bl >= blo && bl <= bM) ? sh.hist[(uint32_t)bl & (kSHB - 1)] : 0ull;
-            const unsigned long long lsum = bcast_u64(wscan_u64(lv), 63);
-            const unsigned long long ov = (o == olo) ? lsum : ovr;
-            const uint32_t on = oin ? (uint32_t)(ov >> 48) : 0u;
-            const double om = oin ? s_m40(ov & 0xFFFFFFFFFFFFull, o, Ri) : 0.0;
-            const uint32_t cincl = wscan_u32(on);
-            const double mincl = wscan_f64(om);
-            const uint64_t hit = __ballot(oin & ((uint64_t)cincl >= K));
-            if (!hit) {
-                krej = NIS_REJECT_WINDOW;  // the k-th largest lies below the listed range
-            } else {
-                const int lk = __ffsll((long long)hit) - 1;
-                const uint32_t CO = bcast_u32(cincl - on, lk);
-                const double GO = bcast_f64(mincl - om, lk);
-                const int O = oM - lk;
-                // lane l: bucket 64 O + 63 - l (descending)
-                const int b = kSRes * O + (kSRes - 1) - l;
-                const bool bin = (b >= blo) & (b <= bM);
-                const unsigned long long bv = bin ? sh.hist[(uint32_t)b & (kSHB - 1)] : 0ull;
-                const uint32_t bn = (uint32_t)(bv >> 48);
-                const double bm = s_m40(bv & 0xFFFFFFFFFFFFull, O, Ri);
-                const uint32_t bci = wscan_u32(bn);
-                const double bmi = wscan_f64(bm);
-                const uint64_t hb = __ballot((uint64_t)(CO + bci) >= K);
-                if (!hb) {
-                    krej = NIS_REJECT_BUCKET;  // octave and bucket counts disagree (ring overlap)
-                } else {
-                    const int lb = __ffsll((long long)hb) - 1;
-                    bk = kSRes * O + (kSRes - 1) - lb;
-                    ck = CO + bcast_u32(bci - bn, lb);
-                    nbk = bcast_u32(bn, lb);
-                    gk = GO + bcast_f64(bmi - bm, lb);
-                    zbk = bcast_f64(bm, lb);
-                    // (b_k may lie more than 16 octaves below R: its masses and
-                    // those above it are then truncated to 2^(R-40) units in
-                    // Z_k, far below the cutoff's resolution; the kept range,
-                    // b_p and above, must still lie within those 16 octaves)
-                }
-            }
-        }
-        if (krej == NIS_REJECT_NONE && nbk >= 2u && (uint64_t)ck + nbk > K) {
-            // (uniform: every wave computed the same b_k) the k-th largest is
-            // inside b_k: every wave lists its members of b_k, then each wave
-            // ranks them (descending value, then ascending index)
-#pragma unroll
-            for (int r = 0; r < kSRounds; ++r) {
-                if (r < nrd && cbk[r] != kSNone && ((int)cbk[r] >> 4) == bk) {
-                    const uint32_t bit = cbk[r] & 15u;
-                    const int e = e0 + (int)(bit >> 2), q = (int)(bit & 3u);
-                    const float xq = reinterpret_cast<const float*>(&sh.ent[w][e])[q];
-                    const uint32_t iq = (uint32_t)(4 * (wbase + (int)sh.epos[w][e]) - mis + q);
-                    const uint32_t slot = atomicAdd(&sh.nkmem, 1u);
-                    if (slot < (uint32_t)kSMem) sh.kmem[slot] = SMem{xq, iq, cfm[r], 0u};
-                }
-            }
-            lds_barrier();
-            const uint32_t nk = sh.nkmem;
-            if (nk > (uint32_t)kSMem || nk != nbk) {
-                krej = NIS_REJECT_BUCKET;
-            } else {
-                const int n = (int)nk;
-                const bool valid = l < n;
-                const SMem mm = sh.kmem[min(l, kSMem - 1)];
-                const unsigned long long Km =
-                    valid ? (((unsigned long long)key32(mm.x) << 32) | (uint32_t)~mm.idx) : 0ull;
-                uint32_t rk = 0u;  // members ahead of this one
-                for (int j = 0; j < n; ++j) rk += (bcast_u64(Km, j) > Km) ? 1u : 0u;
-                // the k-th largest: rank k - ck - 1 among b_k's members
-                const uint64_t kl = __ballot(valid & ((uint64_t)rk + ck + 1u == K));
-                kthk = key32(bcast_f32(mm.x, kl ? __ffsll((long long)kl) - 1 : 0));
-                const float M = unkey32(sh.kmax);
-                const int Ri = (int)((M > -INFINITY && fabsf(M * c) < 1e30f) ? ceilf(M * c) : 0.0f);
-                const bool live = valid & (key32(mm.x) >= kthk);
-                zbk = wsum_f64(live ? s_m40(mm.fm, (int)floorf(mm.x * c), Ri) : 0.0);
-            }
-        }
-    }
     if (w == 0) {
         NIS_STS(3);
         __builtin_amdgcn_s_setprio(3);
@@ -956,15 +859,21 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
         // a wave whose reference sits far below the row max may have overflowed
         const bool range_ok = fmaf(M, c, -unkey32(sh.krwmin)) <= 120.0f;
-        // TOPK: top-p runs on the mass top-k keeps (off at p >= 1)
-        const double pz = TOPK ? (p >= 1.0f ? (double)INFINITY : (double)p * (gk + zbk))
-                               : (double)p * ZR * kS40;
+        // (TOPK: replaced below by p times the mass top-k keeps, or by its
+        // upper bound when b_k's members straddle the k-th; off at p >= 1)
+        double pz = (double)p * ZR * kS40;
         NIS_STS1(8);
         SCut cut;
         cut.reject = NIS_REJECT_NONE;
         cut.gp = 0.0;
         cut.pz = pz;
-        cut.zr = TOPK ? (p >= 1.0f ? 0.0 : (gk + zbk) / kS40) : ZR;
+        cut.zr = ZR;
+        cut.gk = 0.0;
+        cut.bk = 0;
+        cut.ck = 0u;
+        cut.nbk = 0u;
+        cut.split = 0u;
+        cut.bpd = 0;
         cut.bp = 0;
         cut.nabove = 0u;
         cut.M = M;
@@ -987,49 +896,128 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const double omlo = s_m40(lsum & 0xFFFFFFFFFFFFull, olo, Ri);
             const uint32_t on = (o == olo) ? (uint32_t)(lsum >> 48) : onr;
             const double gtot = bcast_f64(oincl, 63) + omlo;  // everything >= blo
+            // ---- TOPK: b_k, the bucket of the k-th largest, by count.  The
+            // buckets are monotone in x, so the k largest are the candidates
+            // above b_k and the largest of b_k's; all of b_k is kept unless
+            // its members straddle the k-th (two or more, more than k in b_k
+            // and above), when they are ranked at the walk and only the bounds
+            // Z_lo <= Z_k <= Z_hi are known here
+            int bk = 0;
+            uint32_t ck = 0u, nbk = 0u;
+            double gk = 0.0, pzlo = pz;
+            bool split = false;
+            uint32_t krej = NIS_REJECT_NONE;
+            if constexpr (TOPK) {
+                const uint64_t K = a.top_k;
+                const uint32_t oc = oin ? on : 0u;
+                const uint32_t cincl = wscan_u32(oc);
+                const uint64_t hit = __ballot(oin & ((uint64_t)cincl >= K));
+                if (!hit) {
+                    krej = NIS_REJECT_WINDOW;  // the k-th largest lies below the listed range
+                } else {
+                    const int lk = __ffsll((long long)hit) - 1;
+                    const uint32_t CO = bcast_u32(cincl - oc, lk);
+                    const double GO = bcast_f64(Go, lk);
+                    const int O = oM - lk;
+                    // lane l: bucket 64 O + 63 - l (descending)
+                    const int b = kSRes * O + (kSRes - 1) - l;
+                    const bool bin = (b >= blo) & (b <= bM);
+                    const unsigned long long bv = bin ? sh.hist[(uint32_t)b & (kSHB - 1)] : 0ull;
+                    const uint32_t bn = (uint32_t)(bv >> 48);
+                    const double bm = s_m40(bv & 0xFFFFFFFFFFFFull, O, Ri);
+                    const uint32_t bci = wscan_u32(bn);
+                    const double bmi = wscan_f64(bm);
+                    const uint64_t hb = __ballot((uint64_t)(CO + bci) >= K);
+                    if (!hb) {
+                        krej = NIS_REJECT_BUCKET;  // octave and bucket counts disagree
+                    } else {
+                        const int lb = __ffsll((long long)hb) - 1;
+                        bk = kSRes * O + (kSRes - 1) - lb;
+                        ck = CO + bcast_u32(bci - bn, lb);
+                        nbk = bcast_u32(bn, lb);
+                        gk = GO + bcast_f64(bmi - bm, lb);
+                        split = nbk >= 2u && (uint64_t)ck + nbk > K;
+                        // (b_k may lie more than 16 octaves below R: masses
+                        // there are truncated to 2^(R-40) units in Z_k, far
+                        // below the cutoff's resolution; only the kept range,
+                        // b_p and above, must lie within those 16 octaves)
+                        const double zhi = gk + bcast_f64(bm, lb);
+                        const double zlo = split ? gk + (double)(K - ck) * s_mdn(bk, Ri) : zhi;
+                        pz = p >= 1.0f ? (double)INFINITY : (double)p * zhi;
+                        pzlo = p >= 1.0f ? (double)INFINITY : (double)p * zlo;
+                        cut.zr = p >= 1.0f ? 0.0 : zhi / kS40;
+                    }
+                }
+                cut.pz = pz;
+            }
             const uint64_t P = __ballot(oin & (on != 0u) & (Go - ldexp(1.0001, o + 1 - Ri + 40) <= pz));
             const uint64_t NEo = __ballot(oin & (on != 0u));
             // everything below blo is removed: G(blo - 1) - m_up(blo - 1) > p Z
             // (and every sum of kept masses stays an exact f64 integer: below 2^52)
             // (TOPK: everything below b_k >= blo is removed by top-k)
             const bool lo_ok = (TOPK || (gtot - s_mup(blo - 1, Ri) > pz)) & (gtot < 4503599627370496.0);
-            if (!P || !lo_ok) {
+            if (TOPK && krej != NIS_REJECT_NONE) {
+                cut.reject = krej;
+            } else if (!P || !lo_ok) {
                 cut.reject = NIS_REJECT_WINDOW;
             } else {
-                const int lp = 63 - __clzll((long long)P);  // deepest passing octave
-                const uint64_t up = NEo & ((1ull << lp) - 1ull);
-                const int la = up ? 63 - __clzll((long long)up) : -1;  // next non-empty above
                 NIS_STS1(9);
-                // level 2: lane l takes bucket 64 O + 63 - l of O = Op (then Oa)
-                int L = -1, bsel = 0;
+                // level 2 for a threshold pzv whose passing octaves are Pm:
+                // lane l takes bucket 64 O + 63 - l of O = Op, the deepest
+                // passing octave, then (when Op has no passing bucket) of Oa,
+                // the next non-empty octave above it.  Returns the lane of the
+                // selected bucket (-1: none) and leaves its values on that lane.
+                auto level2 = [&](double pzv, uint64_t Pm, int& bs, double& gs, uint32_t& cs,
+                                  uint32_t& ns) -> int {
+                    const int lp = 63 - __clzll((long long)Pm);  // deepest passing octave
+                    const uint64_t up = NEo & ((1ull << lp) - 1ull);
+                    const int la = up ? 63 - __clzll((long long)up) : -1;  // next non-empty above
+                    int Ls = -1;
+#pragma unroll
+                    for (int pass2 = 0; pass2 < 2; ++pass2) {
+                        if (Ls < 0 && (pass2 == 0 || la >= 0)) {
+                            const int lo2 = pass2 == 0 ? lp : la;
+                            const int O = oM - lo2;
+                            const double GO = bcast_f64(Go, lo2);
+                            const uint32_t CO = bcast_u32(Co, lo2);
+                            const int b = kSRes * O + (kSRes - 1) - l;
+                            const bool bin = (b >= blo) & (b <= bM);
+                            const unsigned long long bv = bin ? sh.hist[(uint32_t)b & (kSHB - 1)] : 0ull;
+                            const uint32_t bn = (uint32_t)(bv >> 48);
+                            const double bm = s_m40(bv & 0xFFFFFFFFFFFFull, O, Ri);
+                            const double Gb = GO + (wscan_f64(bm) - bm);
+                            const uint32_t Cb = CO + (wscan_u32(bn) - bn);
+                            // Op: its deepest passing bucket; Oa (when Op has none):
+                            // its lowest non-empty bucket, which then passes
+                            const uint64_t sel = pass2 == 0
+                                                     ? __ballot((bn != 0u) & (Gb - s_mup(b, Ri) <= pzv))
+                                                     : __ballot(bn != 0u);
+                            if (sel) {
+                                Ls = 63 - __clzll((long long)sel);
+                                bs = b;
+                                gs = Gb;
+                                cs = Cb;
+                                ns = bn;
+                            }
+                        }
+                    }
+                    return Ls;
+                };
+                int bsel = 0;
                 double gsel = 0.0;
                 uint32_t csel = 0, nsel = 0;
-#pragma unroll
-                for (int pass2 = 0; pass2 < 2; ++pass2) {
-                    if (L < 0 && (pass2 == 0 || la >= 0)) {
-                        const int lo2 = pass2 == 0 ? lp : la;
-                        const int O = oM - lo2;
-                        const double GO = bcast_f64(Go, lo2);
-                        const uint32_t CO = bcast_u32(Co, lo2);
-                        const int b = kSRes * O + (kSRes - 1) - l;
-                        const bool bin = (b >= blo) & (b <= bM);
-                        const unsigned long long bv = bin ? sh.hist[(uint32_t)b & (kSHB - 1)] : 0ull;
-                        const uint32_t bn = (uint32_t)(bv >> 48);
-                        const double bm = s_m40(bv & 0xFFFFFFFFFFFFull, O, Ri);
-                        const double Gb = GO + (wscan_f64(bm) - bm);
-                        const uint32_t Cb = CO + (wscan_u32(bn) - bn);
-                        // Op: its deepest passing bucket; Oa (when Op has none):
-                        // its lowest non-empty bucket, which then passes
-                        const uint64_t sel = pass2 == 0
-                                                 ? __ballot((bn != 0u) & (Gb - s_mup(b, Ri) <= pz))
-                                                 : __ballot(bn != 0u);
-                        if (sel) {
-                            L = 63 - __clzll((long long)sel);
-                            bsel = b;
-                            gsel = Gb;
-                            csel = Cb;
-                            nsel = bn;
-                        }
+                const int L = level2(pz, P, bsel, gsel, csel, nsel);
+                // TOPK with b_k split: the same search with p Z_lo finds the
+                // shallowest bucket the cutoff may lie in (-1: none)
+                int Llo = -1, blsel = 0;
+                double glsel = 0.0;
+                uint32_t clsel = 0;
+                if constexpr (TOPK) {
+                    if (split && L >= 0) {
+                        const uint64_t Plo =
+                            __ballot(oin & (on != 0u) & (Go - ldexp(1.0001, o + 1 - Ri + 40) <= pzlo));
+                        uint32_t nlsel = 0;
+                        if (Plo) Llo = level2(pzlo, Plo, blsel, glsel, clsel, nlsel);
                     }
                 }
                 if (L < 0) {
@@ -1039,16 +1027,47 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                     cut.gp = bcast_f64(gsel, L);
                     cut.nabove = bcast_u32(csel, L);
                     uint32_t nbp = bcast_u32(nsel, L);
-                    if (TOPK && cut.bp < bk) {  // no cutoff below the k-th largest
-                        cut.bp = bk;
-                        cut.gp = gk;
-                        cut.nabove = ck;
-                        nbp = nbk;
+                    cut.bpd = cut.bp;
+                    if constexpr (TOPK) {
+                        // with b_k split, b_p was found with p Z_hi (the deepest
+                        // the cutoff may be); with p Z_lo it may be as shallow
+                        // as the deepest bucket passing then.  Every member of
+                        // [bpd, bp] is ranked at the walk with the exact p Z_k,
+                        // everything above bp is kept, everything below bpd is
+                        // removed.  Neither lies below b_k.
+                        const int bhi = cut.bp;  // b_p with p Z_hi (exact when not split)
+                        const int bdeep = max(bhi, bk);
+                        const uint32_t cdeep =  // candidates at or above bdeep
+                            bhi >= bk ? bcast_u32(csel + nsel, L) : ck + nbk;
+                        int bshal = bdeep;       // the shallow end
+                        if (split) {
+                            if (Llo < 0) {
+                                cut.reject = NIS_REJECT_WINDOW;  // b_lo in another octave: rare
+                            } else {
+                                bshal = max((int)bcast_u32((uint32_t)blsel, Llo), bk);
+                            }
+                        }
+                        if (bshal == bk) {
+                            cut.bp = bk;
+                            cut.gp = gk;
+                            cut.nabove = ck;
+                        } else if (split && Llo >= 0) {
+                            cut.bp = bshal;
+                            cut.gp = bcast_f64(glsel, Llo);
+                            cut.nabove = bcast_u32(clsel, Llo);
+                        }  // (else b_p = b_hi, as found)
+                        cut.bpd = bdeep;
+                        nbp = cdeep - cut.nabove;  // members of [bpd, bp]
+                        if (split && nbk > (uint32_t)kSMem) cut.reject = NIS_REJECT_BUCKET;
+                        cut.bk = bk;
+                        cut.ck = ck;
+                        cut.nbk = nbk;
+                        cut.gk = gk;
+                        cut.split = split ? 1u : 0u;
                     }
                     // the kept range stays within 16 octaves of R (exact fixed point)
-                    if ((cut.bp >> kSLog) < Ri - 16) cut.reject = NIS_REJECT_WINDOW;
+                    if ((cut.bpd >> kSLog) < Ri - 16) cut.reject = NIS_REJECT_WINDOW;
                     else if (nbp > (uint32_t)kSMem) cut.reject = NIS_REJECT_BUCKET;
-                    if (TOPK && krej != NIS_REJECT_NONE) cut.reject = krej;
                 }
             }
         }
@@ -1079,13 +1098,38 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         // of 0..16)
         unsigned long long isum = 0ull;
         uint32_t mb = 0u;  // bit 4 i + q: element q of entry i is a member
+        // TOPK: b_k split and below the cutoff range: its members are listed
+        // too (they fix Z_k); the members of the range [bpd, bp] are listed
+        const bool ksplit = TOPK && cut.split != 0u && cut.bk < cut.bpd;
+        const int bpd = TOPK ? cut.bpd : bp;
+        uint32_t mk = 0u;
 #pragma unroll
         for (int r = 0; r < kSRounds; ++r) {
             if (r < nrd) {
                 const int b = (int)cbk[r] >> 4;
                 const uint32_t fk = (b > bp) ? cfm[r] : 0u;
                 isum += (unsigned long long)fk << ((uint32_t)((b >> kSLog) - Ri + 16) & 63u);
-                mb |= (b == bp) ? (1u << (cbk[r] & 15u)) : 0u;
+                mb |= (b >= bpd && b <= bp) ? (1u << (cbk[r] & 15u)) : 0u;
+                if (TOPK) mk |= (ksplit && b == cut.bk) ? (1u << (cbk[r] & 15u)) : 0u;
+            }
+        }
+        if (TOPK && ksplit) {  // (uniform; at most kSMem members, checked above)
+            const uint32_t kc = (uint32_t)__popc(mk);
+            const uint32_t kincl = wscan_u32(kc);
+            const uint32_t ktot = (uint32_t)__builtin_amdgcn_readlane((int)kincl, 63);
+            if (ktot) {
+                uint32_t base = 0u;
+                if (l == 0) base = atomicAdd(&sh.nkmem, ktot);
+                uint32_t slot = bcast_u32(base, 0) + kincl - kc;
+                while (mk) {
+                    const int bit = __ffs(mk) - 1;
+                    mk &= mk - 1u;
+                    const int e = l * sg + (bit >> 2), q = bit & 3;
+                    const float x = reinterpret_cast<const float*>(&sh.ent[w][e])[q];
+                    const uint32_t idx = (uint32_t)(4 * (wbase + (int)sh.epos[w][e]) - mis + q);
+                    sh.kmem[min(slot, (uint32_t)kSMem - 1)] = SMem{x, idx, s_fm(x, c, x * c), 0u};
+                    ++slot;
+                }
             }
         }
         if (PEN && nsw != 0u) {
@@ -1172,13 +1216,40 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     NIS_STS1(3);
     __builtin_amdgcn_s_setprio(3);
 
-    const double pz = cut.pz, gp = cut.gp;
+    double pz = cut.pz;
+    const double gp = cut.gp;
+    double zrs = cut.zr;
     const int n = (int)min(sh.nmem, (uint32_t)kSMem);
     const u4v mr = *reinterpret_cast<const u4v*>(&sh.mem[min(l, kSMem - 1)]);
     const float xm = __uint_as_float(mr.x);
-    // (TOPK: members of b_k below the k-th largest value are removed)
-    const bool valid = (l < n) & (!TOPK || bp != bk || key32(xm) >= kthk);
     const uint32_t im = mr.y;
+    // TOPK with b_k split: its members (those of b_p when b_k = b_p) ranked
+    // by (value desc, index asc); the k-th largest value keeps every member
+    // at or above it, and Z_k, hence p Z_k, is now exact
+    uint32_t kthk = 0u;
+    if constexpr (TOPK) {
+        if (cut.split != 0u) {
+            const bool same = cut.bk >= cut.bpd;  // b_k is the deep end of the range
+            const int nk = same ? n : (int)min(sh.nkmem, (uint32_t)kSMem);
+            const SMem kq = sh.kmem[min(l, kSMem - 1)];
+            const float xk = same ? xm : kq.x;
+            const uint32_t ik = same ? im : kq.idx;
+            const uint32_t fk = same ? mr.z : kq.fm;
+            const bool kv = (l < nk) & (!same || s_bucket(xm * c) == cut.bk);
+            const unsigned long long Kk = kv ? (((unsigned long long)key32(xk) << 32) | (uint32_t)~ik) : 0ull;
+            uint32_t rk = 0u;
+            for (int j = 0; j < nk; ++j) rk += (bcast_u64(Kk, j) > Kk) ? 1u : 0u;
+            const uint64_t kl = __ballot(kv & ((uint64_t)rk + cut.ck + 1u == a.top_k));
+            kthk = key32(bcast_f32(xk, kl ? __ffsll((long long)kl) - 1 : 0));
+            const bool live = kv & (key32(xk) >= kthk);
+            const double zk_ = cut.gk + wsum_f64(live ? s_m40(fk, (int)floorf(xk * c), Ri) : 0.0);
+            pz = p >= 1.0f ? (double)INFINITY : (double)p * zk_;
+            zrs = p >= 1.0f ? 0.0 : zk_ / kS40;
+        }
+    }
+    // (TOPK: members below the k-th largest value are removed; kthk is 0
+    // unless b_k is split, and members above b_k lie above it)
+    const bool valid = (l < n) & (key32(xm) >= kthk);
     double ym = 0.0;  // PEN: the member's value in f64
     if constexpr (PEN) ym = sh.memy[min(l, kSMem - 1)];
     const float tm = PEN ? (float)(ym * (double)c) : xm * c;
@@ -1246,7 +1317,9 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     int le;              // the lane holding the drawn element
     if constexpr (!PEN) {
         const unsigned long long Ke = ((unsigned long long)key32(xe) << 32) | (uint32_t)~ide;
-        kje = (l < 4 * sgs) & (je < (int)nes) & ((be > bp) | ((be == bp) & (Ke >= Kcut)));
+        // (members: the cutoff range [bpd, bp], a single bucket but for TOPK)
+        kje = (l < 4 * sgs) & (je < (int)nes) &
+              ((be > bp) | ((be >= (TOPK ? cut.bpd : bp)) & (be <= bp) & (Ke >= Kcut)));
         ee = kje ? s_m40(s_fm(xe, c, te), (int)floorf(te), Ri) : 0.0;
         NIS_STS1(6);
         const double pe_incl = rscan_f64(ee);
@@ -1322,7 +1395,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
                 rho = (double)__builtin_amdgcn_exp2f(-(float)(Mx * (double)c - (double)R));
             }
             write_row_stats(a, row, tok, NIS_PATH_DRAW, Mx / temp, zk / kS40 * rho,
-                            cut.zr * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
+                            zrs * rho, u, prob, (uint64_t)(cut.nabove + nkept), 1);
         }
     }
     NIS_STS1(7);
