@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "sampled rows/s + HBM GB/s (% peak), B=256 x V=50257 fp32, T=0.8 top-p=0.9"
+GRAPH_MAX = 200          # launches per captured hipGraph in the timed region
 RESIDENT_MAX_V = 53245   # kRMaxV: the largest row one 1024-lane workgroup holds in registers
 SPARSE_MAX_V = 53245     # kSMaxV
 
@@ -457,15 +458,18 @@ def main():
         sampler.sample_batch(bufs[i % len(bufs)], params, states, tokens=tokens)
     torch.cuda.synchronize()
 
-    # Timed region: hipGraph replays of one launch per rotated buffer, so the
-    # GPU is not waiting on Python between launches.  HIP events bracket the
-    # whole region on the stream the launches run on; the mean launch
-    # duration is their elapsed time over the number of launches.
-    G = len(bufs)
+    # Timed region: hipGraph replays of launches over the rotated buffers
+    # (launch i reads buffer i mod 8), so the GPU is not waiting on Python
+    # between launches.  A graph holds up to GRAPH_MAX launches: each replay
+    # boundary costs about 5 us, so short graphs would add ~0.7 us per launch.
+    # HIP events bracket the whole region on the stream the launches run on;
+    # the launch interval is their elapsed time over the number of launches.
+    G = min(GRAPH_MAX, max(1, args.steps))
     K = max(1, args.steps)
+    nb = len(bufs)
 
     def launch(i):
-        sampler.sample_batch(bufs[i], params, states, tokens=tokens)
+        sampler.sample_batch(bufs[i % nb], params, states, tokens=tokens)
 
     g_full = capture(launch, G)
     g_tail = capture(launch, K % G)
@@ -487,7 +491,7 @@ def main():
     torch.cuda.synchronize()
     te0 = time.perf_counter()
     for i in range(min(K, 64)):
-        sampler.sample_batch(bufs[i % G], params, states, tokens=tokens)
+        sampler.sample_batch(bufs[i % nb], params, states, tokens=tokens)
     torch.cuda.synchronize()
     eager_rows_s = B * min(K, 64) / (time.perf_counter() - te0)
 
@@ -536,7 +540,7 @@ def main():
         "config": {"workload": args.workload, "B": B, "V": V, "temperature": w.temperature,
                    "top_p": w.top_p, "top_k": args.top_k, "ld": V, "parallelism": "1 GPU",
                    "launch": f"hipGraph replays: {K // G} x {G} + {K % G} nis_sample_batch "
-                             f"launches",
+                             f"launches over {nb} rotated batches",
                    "eager_rows_per_s": eager_rows_s},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
