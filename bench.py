@@ -202,6 +202,51 @@ def bench_decode(args, w, sampler, params, bufs, states, tokens):
                      "frac": alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS},
     }))
 
+def bench_floor(args, w, sampler, bufs):
+    """The stream floor (nis_stream_floor) on the workload's batches, timed
+    exactly as the sampler is: the same graph replays and events."""
+    import torch
+    B, V = w.B, w.V
+    out = torch.empty((B, 2), dtype=torch.float32, device=bufs[0].device)
+    nb = len(bufs)
+
+    def launch(i):
+        sampler.stream_floor(bufs[i % nb], w.temperature, out=out)
+
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    K = max(1, args.steps)
+    G = min(GRAPH_MAX, K)
+    g_full = capture(launch, G)
+    g_tail = capture(launch, K % G)
+    for _ in range(2):
+        g_full.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    replay_exact(g_full, g_tail, G, K)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / K
+    alg_bytes = B * 4 * V
+    print(json.dumps({
+        "metric": f"stream floor: rows/s + HBM GB/s (% peak), B={B} x V={V} fp32 read with the "
+                  f"sparse kernel's layout (max and exp-sum only, nothing sampled)",
+        "value": B / (us * 1e-6), "unit": "rows/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "us_per_step": us, "higher_is_better": True,
+        "data": "synthetic logits of the workload, 8 rotated batches resident in HBM",
+        "config": {"workload": args.workload, "B": B, "V": V,
+                   "launch": f"hipGraph replays of up to {G} nis_stream_floor launches"},
+        "roofline": {"bound": "hbm", "achieved": alg_bytes / (us * 1e-6) / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                     "kernel": "stream_floor_kernel", "launch_interval_us": us,
+                     "alg_bytes_per_launch": alg_bytes},
+    }))
+
+
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
@@ -370,6 +415,10 @@ def main():
                          "nis_argmax_batch")
     ap.add_argument("--lm-h", type=int, default=768, help="hidden size for --lm-head")
     ap.add_argument("--lm-group", type=int, default=0, help="group size for quantized --lm-head")
+    ap.add_argument("--floor", action="store_true",
+                    help="time nis_stream_floor instead: the sparse kernel's layout and load "
+                         "pipeline computing only each row's max and exp-sum (the bandwidth "
+                         "ceiling the sampler's roofline fraction is measured against)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 4 plain device copies of MIB MiB (reads MIB, writes MIB) "
                          "to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -420,6 +469,10 @@ def main():
     torch.cuda.synchronize()
     if args.decode:
         bench_decode(args, w, sampler, params, bufs, states, tokens)
+        sampler.close()
+        return
+    if args.floor:
+        bench_floor(args, w, sampler, bufs)
         sampler.close()
         return
 

@@ -225,6 +225,17 @@ int nis_lm_head_logits(nis_ctx* ctx, const float* d_hidden, int64_t ldh, int32_t
 int nis_lm_head_greedy(nis_ctx* ctx, const float* d_hidden, int32_t H, const nis_weights* w, int64_t V,
                        float* d_logits, uint32_t* d_token);
 
+/* Measurement only: the bandwidth floor of the sparse row kernel.  One
+ * 1024-lane workgroup per row reads it with that kernel's layout and load
+ * pipeline and computes only each row's max and sum of 2^(x c - R)
+ * (d_out[2 b] = max, d_out[2 b + 1] = the sum at R = ceil(max c),
+ * c = log2(e) / max(T, 1e-6)); it samples nothing.  No counterpart in the
+ * reference: bench.py --floor times it beside the sampler, so that the
+ * sampler's roofline fraction has a measured ceiling.  256 <= V <= 53245.
+ * Asynchronous on the context stream. */
+int nis_stream_floor(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     float temperature, float* d_out);
+
 /* Wait for all work queued on the context stream. */
 int nis_sync(nis_ctx* ctx);
 

@@ -13,6 +13,7 @@
 #include <string>
 
 #include "kernels.h"
+#include "floor_path.h"
 #include "lm_head.h"
 
 // 16-row hidden tiles per matrix-core wave when B > 16 (4 or 2)
@@ -588,6 +589,25 @@ int nis_lm_head_greedy(nis_ctx* ctx, const float* d_hidden, int32_t H, const nis
     rc = nis_lm_head_logits(ctx, d_hidden, H, 1, H, w, V, lg, V);
     if (rc != NIS_OK) return rc;
     return nis_argmax_batch(ctx, lg, V, 1, V, d_token);
+}
+
+int nis_stream_floor(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                     float temperature, float* d_out) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_logits || !d_out) return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (B <= 0 || V < 256 || V > nis::kSMaxV || ld < V)
+        return fail(ctx, NIS_EINVAL, "B must be positive, 256 <= V <= 53245 and ld >= V");
+    if (B > NIS_MAX_B) return fail(ctx, NIS_ERANGE, "B too large");
+    if (((uintptr_t)d_logits & 3u) || ((uintptr_t)d_out & 3u))
+        return fail(ctx, NIS_EALIGN, "logits and out must be 4-byte aligned");
+    if (!(temperature > 0.0f)) return fail(ctx, NIS_EINVAL, "temperature must be positive");
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+    const float c = (float)(1.4426950408889634 / fmax((double)temperature, 1e-6));
+    hipLaunchKernelGGL(nis::stream_floor_kernel, dim3((unsigned)B), dim3(nis::kSB), 0, ctx->stream,
+                       d_logits, ld, (int)V, c, d_out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "stream floor launch");
 }
 
 int nis_sync(nis_ctx* ctx) {

@@ -36,7 +36,7 @@ EXPORTED_SYMBOLS = (
     "nis_rng_next_f64", "nis_rng_seed_batch", "nis_sample_batch", "nis_argmax_batch",
     "nis_apply_repetition_penalty", "nis_sample_one", "nis_sample_one_noalloc", "nis_sync",
     "nis_decode_step",
-    "nis_lm_head_logits", "nis_lm_head_greedy",
+    "nis_lm_head_logits", "nis_lm_head_greedy", "nis_stream_floor",
 )
 
 
@@ -113,9 +113,11 @@ def load_library(path: str = LIB_PATH):
                                  ctypes.c_int64, u64p, ctypes.POINTER(ctypes.c_uint32)]
     L.nis_sample_one_noalloc.argtypes = L.nis_sample_one.argtypes
     L.nis_sync.argtypes = [vp]
+    L.nis_stream_floor.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                                   ctypes.c_float, vp]
     for name in ("nis_ctx_create", "nis_ctx_destroy", "nis_ctx_set_stream", "nis_rng_seed_batch",
                  "nis_sample_batch", "nis_argmax_batch", "nis_apply_repetition_penalty",
-                 "nis_sample_one", "nis_sample_one_noalloc", "nis_sync"):
+                 "nis_sample_one", "nis_sample_one_noalloc", "nis_sync", "nis_stream_floor"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -363,6 +365,22 @@ class Sampler:
                                       logits.stride(0), B, V, ctypes.c_void_p(tokens.data_ptr()))
         _check(self._L, self._ctx, rc)
         return tokens
+
+    def stream_floor(self, logits, temperature: float, V: Optional[int] = None, out=None):
+        """Measurement only (nis_stream_floor): each row's max and sum of
+        2^(x c - ceil(max c)) read with the sparse kernel's layout; out is a
+        [B, 2] float32 tensor.  Samples nothing."""
+        import torch
+        B = logits.shape[0]
+        V = logits.shape[1] if V is None else V
+        if out is None:
+            out = torch.empty((B, 2), dtype=torch.float32, device=logits.device)
+        self._bind_stream()
+        rc = self._L.nis_stream_floor(self._ctx, ctypes.c_void_p(logits.data_ptr()),
+                                      logits.stride(0), B, V, ctypes.c_float(temperature),
+                                      ctypes.c_void_p(out.data_ptr()))
+        _check(self._L, self._ctx, rc)
+        return out
 
     def rng_seed_batch(self, seeds, states):
         self._bind_stream()
