@@ -304,6 +304,29 @@ def bench_lm_head(args):
         sampler.lm_head_logits(x, fmt, d, V, scales=sc, group_size=group, out=out)
         sampler.argmax_batch(out, tokens=tok)
 
+    # --sample (B = 1): the decode step's sampled form, GEMV then
+    # nis_sample_batch on the logits it just wrote (T 0.8, top-p 0.9).  The
+    # hidden row is rescaled so the logits have c1's spread (standard
+    # deviation 3): the random heads' own logits are far narrower or wider,
+    # and a nucleus past the sparse kernel's lists would time the general
+    # path instead of the sampler the decode loop runs on real logits.
+    sparams = ns.SamplingParams(temperature=0.8, top_p=0.9)
+    sstate = torch.from_numpy(ns.rng_states([7]).view(np.int64)).to(dev)
+    xs = x
+    if args.sample and B == 1:
+        d0, sc0 = heads[0]
+        sampler.lm_head_logits(x, fmt, d0, V, scales=sc0, group_size=group, out=out)
+        torch.cuda.synchronize()
+        xs = x * float(3.0 / max(float(out[0].std()), 1e-30))
+
+    def run_sample(i):
+        d, sc = heads[i % ncopy]
+        sampler.lm_head_logits(xs, fmt, d, V, scales=sc, group_size=group, out=out)
+        sampler.sample_batch(out, sparams, sstate, tokens=tok)
+
+    def run_sample_only(i):
+        sampler.sample_batch(out, sparams, sstate, tokens=tok)
+
     for i in range(args.warmup):
         run(i)
     torch.cuda.synchronize()
@@ -318,6 +341,22 @@ def bench_lm_head(args):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / K
     split_us = None
+    sample_us = sample_only_us = None
+    if args.sample and B == 1:
+        for fn in (run_sample, run_sample_only):
+            for i in range(args.warmup):
+                fn(i)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for i in range(K):
+                fn(i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e3 / K
+            if fn is run_sample:
+                sample_us = t
+            else:
+                sample_only_us = t  # the sampler alone on the same (hot) logits
     if greedy:
         for i in range(args.warmup):
             run_split(i)
@@ -374,7 +413,9 @@ def bench_lm_head(args):
         "config": {"workload": f"lm_head_{args.lm_head}", "B": B, "H": H, "V": V,
                    "group_size": group, "alg_bytes": alg_bytes, "flops": flops,
                    "head_copies": ncopy,
-                   "split_logits_then_argmax_us": split_us},
+                   "split_logits_then_argmax_us": split_us,
+                   "logits_then_sample_us": sample_us,
+                   "sample_on_hot_logits_us": sample_only_us},
         "roofline": roof, "cpu_baseline": cpu,
     }))
     sampler.close()
@@ -413,6 +454,9 @@ def main():
                     help="with --lm-head and --lm-b 1: time nis_lm_head_greedy (GEMV with the "
                          "greedy token in its epilogue) and, beside it, nis_lm_head_logits + "
                          "nis_argmax_batch")
+    ap.add_argument("--sample", action="store_true",
+                    help="with --lm-head and --lm-b 1: also time nis_lm_head_logits followed by "
+                         "nis_sample_batch (T 0.8, top-p 0.9) on the logits it wrote")
     ap.add_argument("--lm-h", type=int, default=768, help="hidden size for --lm-head")
     ap.add_argument("--lm-group", type=int, default=0, help="group size for quantized --lm-head")
     ap.add_argument("--floor", action="store_true",
