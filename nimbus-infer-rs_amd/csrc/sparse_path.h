@@ -9,12 +9,14 @@
 // it works on, so each wave's data arrives spread over the whole stream and
 // the waves finish together.  As the chunks land each wave adds the masses
 // 2^(x c - R_w) to Z in f64 (c = log2(e)/T, R_w an integer reference from
-// the wave's first chunk), keeps its max, and appends every float4 holding
-// an element at or above its listing threshold to its LDS list (index order,
-// one ballot per chunk).  The threshold thc_w comes from the wave's first
-// four chunks: the lower edge of the 1/8-octave bins of x c holding at most
-// 44 of their 256 float4 maxima, raised to the running max of the thresholds
-// the other waves have published.
+// the wave's first chunk; an element more than 127 octaves above it makes Z
+// infinite and the row is declined), keeps its max, and appends every
+// float4 holding an element at or above its listing threshold to its LDS
+// list (index order, one ballot per chunk).  The threshold thc_w comes from the
+// wave's first four chunks: the lower edge of the 1/8-octave bins of x c
+// holding at most 44 of their 256 float4 maxima, raised to the running max
+// of the thresholds the other waves have published, and at the stream end
+// to kSDeep octaves below the largest max seen (nothing deeper is kept).
 //
 // Cutoff (src/sampler.rs:118-160) without a sort.  The reference keeps
 // sorted position pos iff D(pos) = cum_excl(pos) - q(pos) <= p*Z; D is
@@ -79,6 +81,15 @@ constexpr int kSSlot = 32;                  // float4 slots holding them, per wa
 static_assert(kSB == kPB && kSMaxV == kPMaxV, "penalty bitmaps sized for this layout");
 constexpr int kSRounds = 4 * kSSeg;         // candidates per lane (at most)
 constexpr double kS40 = 1099511627776.0;    // 2^40
+// Octaves below the row max past which nothing is kept for top-p < 0.95:
+// at most V 2^-22 Z <= 0.013 Z of mass lies there (V <= 53245), and the
+// removed mass is at least (1 - p) Z >= 0.05 Z, so every such element is
+// removed.  Listing thresholds are never set below (max seen) c - kSDeep.
+constexpr float kSDeep = 22.0f;
+// TOPK: the k-th largest may lie deeper than that (top-k keeps elements top-p
+// alone would remove, at any top-p): 30 octaves, still inside the 32-octave
+// histogram ring; a k-th below the listed range declines the row.
+constexpr float kSDeepK = 30.0f;
 
 // Optional phase timestamps (profiling builds only; compiled out unless
 // NIS_PHASE_TIMING is defined).  Each wave keeps the low 32 bits of the
@@ -179,7 +190,6 @@ struct WideShared {
     uint32_t kmax;                 // max logit
     uint32_t kxlo;                 // max listing threshold
     uint32_t kthmin;               // min listing threshold of a wave with entries
-    uint32_t krwmin;               // min R_w of a wave with data
     uint32_t nmax;                 // largest list
     // repetition penalty only (sparse_row<true>)
     PenBits pb;                        // the history's bitmaps
@@ -505,7 +515,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         sh.kmax = 0u;
         sh.kxlo = 0u;
         sh.kthmin = 0xFFFFFFFFu;
-        sh.krwmin = 0xFFFFFFFFu;
         sh.nmax = 0u;
         if (PEN) {
             sh.kymax = 0ull;
@@ -653,8 +662,15 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const int bw = (int)wsum_u32(nok) - 1; /* last bin whose cumulative count fits */ \
             thc = (bw < 0 || Kw == 0) ? INFINITY : RwH - (float)(bw + 1) * 0.125f;           \
             /* x_lo = max_w thc_w bounds the complete range, so nothing below the */         \
-            /* running max of the thresholds published so far is ever needed */            \
-            if (Kw > 0 && l == 0) atomicMax(&sh.kxlo, key32(thc));                           \
+            /* running max of the thresholds published so far is ever needed; the */         \
+            /* sample's max goes out too (the depth clamp at the stream end) */             \
+            {                                                                                \
+                const float msw = wmax_f32(mx);                                              \
+                if (l == 0) {                                                                \
+                    if (Kw > 0) atomicMax(&sh.kxlo, key32(thc));                             \
+                    atomicMax(&sh.kmax, key32(msw));                                         \
+                }                                                                            \
+            }                                                                                \
             lds_wave_fence();                                                                \
             thl = fmaxf(thc, unkey32(sh.kxlo));                                              \
             /* thl in logit units, rounded down: x >= thx whenever x * c >= thl */           \
@@ -679,6 +695,19 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     NIS_STS(1);
     __builtin_amdgcn_s_setprio(0);
     thl = fmaxf(thl, unkey32(sh.kxlo));
+    mx = wmax_f32(mx);
+    {
+        // nothing more than kSDeep octaves below the row max is kept (top-p
+        // < 0.95; TOPK: kSDeepK, and rows needing more are declined by the
+        // count search): the threshold rises to that depth below the largest
+        // max seen (this wave's, or one published), on the 1/8-octave grid,
+        // and the raised threshold is published (x_lo, the complete range,
+        // follows it)
+        const float mref = fmaxf(mx, unkey32(sh.kmax));
+        const float tcl = ceilf((mref * c - (TOPK ? kSDeepK : kSDeep)) * 8.0f) * 0.125f;
+        if (tcl > thl && tcl < INFINITY) thl = tcl;
+        if (l == 0 && Kw > 0 && thl < INFINITY) atomicMax(&sh.kxlo, key32(thl));
+    }
     // ---- PEN: this wave's penalised elements, in f64 ------------------------
     // One per lane (row order): the f64 value (sampler.rs:94-98) and its mass
     // into this lane's part of Z; its exact value and its f32 value rounded up
@@ -715,7 +744,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             const double yc = y * (double)c;
             const float ts = (float)yc;
             if (sv) {
-                z += pen_mass(yc, Rw);
+                z += pen_mass(yc, Rz);
                 if (y > -INFINITY) {
                     atomicMax(&sh.kymax, key64(y));
                     atomicMax(&sh.kmaxp, key32(pen_f32_up(y)));
@@ -734,8 +763,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             if (sv) srec[l] = SSide{y, rr.z, cand ? 1u : 0u};
         }
     }
-    mx = wmax_f32(mx);
-    z = wsum_f64(z);
+    z = wsum_f64(z);  // (mx was reduced over the wave above)
     NIS_STS(4);
     // the wave's record, its keys and (wave 0) the row's draw go out before
     // its histogram rounds, so that they overlap them
@@ -743,7 +771,7 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         const uint64_t zb = (uint64_t)__double_as_longlong(z);
         const uint32_t ra = lds_addr(&sh.rec[w]);
         lds_put_b128_m(1ull, ra, u4v{(uint32_t)zb, (uint32_t)(zb >> 32), __float_as_uint(mx),
-                                     __float_as_uint(Rw)});
+                                     __float_as_uint(Rz)});
         lds_put_b128_m(1ull, ra + 16, u4v{__float_as_uint(Kw > 0 ? thc : -INFINITY), nw, nsw, 0u});
     }
     // the row's one draw (sampler.rs:209), made by wave 0 off the critical
@@ -759,10 +787,10 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         rst = (l == 0) ? st[0] : (l == 1) ? st[1] : (l == 2) ? st[2] : st[3];
     }
     if (l == 0) {
-        const float thr = Kw > 0 ? thc : -INFINITY;
+        // (the lowest candidate of this wave is at or above its final thl)
+        const float thr = Kw > 0 ? thl : -INFINITY;
         atomicMax(&sh.kmax, key32(mx));
         if (nw > 0u || nsc > 0u) atomicMin(&sh.kthmin, key32(thr));
-        if (mx > -INFINITY) atomicMin(&sh.krwmin, key32(Rw));
         atomicMax(&sh.nmax, nw);
     }
     // every element of the wave's entries at or above thl (raised to the
@@ -823,6 +851,41 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     const int li = min(l, kSW - 1);
     const bool rv = l < kSW;
     lds_barrier();
+    // Ring overrun: a wave may have listed candidates more than 31 octaves
+    // below the row max (its threshold was clamped against a max that rose
+    // later); they alias in the 32-octave ring.  The row max and the lowest
+    // candidate bound are final now, so every wave takes the same decision:
+    // each subtracts its own such candidates (exact: integer counts and
+    // fixed-point masses), and one barrier orders that before the search.
+    // Nothing of the complete range is lost: it lies above x_lo >= M c -
+    // kSDeepK.  (PEN: the side lists' candidates are not in the rounds, so
+    // the search declines such a row instead.)
+    bool ringfix = false;
+    if constexpr (!PEN) {
+        const float Mr = unkey32(sh.kmax);
+        const float thr = unkey32(sh.kthmin);
+        if ((Mr > -INFINITY) & (Mr < INFINITY) & (fabsf(Mr * c) < 1e6f) & (thr > -INFINITY) &
+            (thr < INFINITY)) {
+            const int bMr = s_bucket(Mr * c);
+            if (!(bMr - (int)(thr * (float)kSRes) < kSHB - kSRes)) {
+                const uint32_t hist0 = lds_addr(&sh.hist[0]);
+                const uint32_t oct0 = lds_addr(&sh.oct[0]) + 8 * ((uint32_t)l & (kSOctC - 1));
+#pragma unroll
+                for (int r = 0; r < kSRounds; ++r) {
+                    if (r < nrd) {
+                        const int b = (int)cbk[r] >> 4;
+                        const uint64_t am = __ballot((cbk[r] != kSNone) & (b <= bMr - (kSHB - kSRes)));
+                        if (am)
+                            lds_add2_u64_m(am, hist0 + 8 * ((uint32_t)b & (uint32_t)(kSHB - 1)),
+                                           oct0 + 8 * kSOctC * ((uint32_t)(b >> kSLog) & 31u),
+                                           0ull - ((1ull << 48) | (uint64_t)cfm[r]));
+                    }
+                }
+                ringfix = true;
+                lds_barrier();
+            }
+        }
+    }
     if (w == 0) {
         NIS_STS(3);
         __builtin_amdgcn_s_setprio(3);
@@ -857,8 +920,6 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
             }
         }
         const double ZR = r16_sum(rv ? ldexp(rz, (int)(rrw - R)) : 0.0);  // exact rescales
-        // a wave whose reference sits far below the row max may have overflowed
-        const bool range_ok = fmaf(M, c, -unkey32(sh.krwmin)) <= 120.0f;
         // (TOPK: replaced below by p times the mass top-k keeps, or by its
         // upper bound when b_k's members straddle the k-th; off at p >= 1)
         double pz = (double)p * ZR * kS40;
@@ -878,10 +939,14 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
         cut.nabove = 0u;
         cut.M = M;
         cut.R = R;
-        if (!fin || !(ZR > 0.0) || !(ZR < INFINITY) || !range_ok) {
+        // (a wave's Z overflows only for an element 127 octaves above its
+        // first chunk's max: then ZR is infinite and the row is declined)
+        if (!fin || !(ZR > 0.0) || !(ZR < INFINITY)) {
             cut.reject = NIS_REJECT_NONFINITE;
-        } else if (!xfin || nmax > (uint32_t)kSE || (PEN && sh.pover != 0u) ||
-                   !(bM - (int)(thmin * (float)kSRes) < kSHB - kSRes) || oM - olo > 30) {
+        } else if (!xfin || nmax > (uint32_t)kSE || (PEN && sh.pover != 0u) || oM - olo > 30) {
+            cut.reject = NIS_REJECT_CAPACITY;
+        } else if (!ringfix && !(bM - (int)(thmin * (float)kSRes) < kSHB - kSRes)) {
+            // (PEN) candidates more than 31 octaves below the row max
             cut.reject = NIS_REJECT_CAPACITY;
         } else {
             // level 1.  Octave olo is the deepest lane, so the octaves' prefix

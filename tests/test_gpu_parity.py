@@ -261,6 +261,24 @@ def test_sparse_kernel_distribution_sweep(sampler, sigma):
                    label=f"sweep-s{sigma}-T{T}-p{p}")
 
 
+@pytest.mark.parametrize("sigma,T,p", [(3.0, 0.5, 0.9), (3.0, 0.3, 0.9), (3.0, 0.2, 0.94),
+                                       (3.0, 0.1, 0.9), (3.0, 0.3, 0.5), (25.0, 0.8, 0.9),
+                                       (25.0, 1.5, 0.5)])
+def test_sparse_kernel_low_temperatures(sampler, sigma, T, p):
+    # low temperatures (or wide logits) spread x c over 50-150 octaves: the
+    # listing thresholds are clamped 22 octaves below the largest max seen
+    # (nothing deeper is kept at top-p < 0.95), and candidates a wave listed
+    # against a max that later rose more than the ring allows are subtracted
+    # again before the search.  Every row must stay on the sparse kernel.
+    rnd = np.random.Generator(np.random.PCG64(int(sigma * 10 + T * 100)))
+    B, V = 64, 50257
+    x = (rnd.standard_normal((B, V)) * sigma).astype(np.float32)
+    x[::7, rnd.integers(0, V)] += np.float32(3.0 * sigma)  # rows whose max stands apart
+    rep = _check(sampler, x, V, _params(temperature=T, top_p=p), list(range(B)),
+                 label=f"low-T sigma={sigma} T={T} p={p}")
+    assert rep["sparse_rows"] == B, rep
+
+
 def test_sparse_kernel_bucket_edges_and_wide_ties(sampler):
     # headline-like logits rounded to a 1/32 lattice with T = log2(e)/2, so
     # x*c sits on (or a hair off) the sparse kernel's 1/64-octave bucket
