@@ -387,13 +387,32 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         const float u = fmaf(xr, cf, -Rf);
         return clo != 0.0f ? fmaf(xr, clo, u) : u;
     };
-    // 2^(x*c - R) in f64: exp2 of the octave-relative argument, then the
-    // exact power of two (0 for x = -inf; x is never NaN or +inf here)
-    auto massx = [&](float xr) -> double {
+    // 2^(x*c - R) as its octave mantissa fm = 2^(x*c - o) 2^24 rounded down
+    // (f32 exp2 of the octave-relative argument, in [2^24, 2^25]) and e =
+    // o - R: the mass is fm 2^(e - 24) exactly in f64, its 2^-40 fixed
+    // point fm 2^(e + 16) (a shift).  fm = 0 for x = -inf; x is never NaN or
+    // +inf here.
+    auto mparts = [&](float xr, uint32_t& fm, int& e) {
         const float of = fminf(fmaxf(floorf(xr * cf), Rf - 1100.0f), Rf + 2.0f);
         const float f = fmaf(xr, clo, fmaf(xr, cf, -of));
-        const double m = ldexp((double)__builtin_amdgcn_exp2f(f), (int)of - Ri);
-        return xr > -INFINITY ? m : 0.0;
+        fm = xr > -INFINITY ? (uint32_t)(__builtin_amdgcn_exp2f(f) * 16777216.0f) : 0u;
+        e = (int)of - Ri;
+    };
+    auto mfix = [](uint32_t fm, int e) -> unsigned long long {
+        const int sh = e + 16;  // <= 18 (o <= R + 2)
+        return sh >= 0 ? ((unsigned long long)fm << sh) : (sh > -32 ? (unsigned long long)(fm >> -sh) : 0ull);
+    };
+    auto massx = [&](float xr) -> double {
+        uint32_t fm;
+        int e;
+        mparts(xr, fm, e);
+        return ldexp((double)fm, e - 24);
+    };
+    auto fixx = [&](float xr) -> unsigned long long {  // floor(massx(x) 2^40)
+        uint32_t fm;
+        int e;
+        mparts(xr, fm, e);
+        return mfix(fm, e);
     };
     const double rho = mf32 ? 1.0 / massx((float)M) : 1.0;
     auto mass_w = [&](double wv) -> double {  // wv = value / T (penalised rows)
@@ -484,10 +503,6 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
 #pragma unroll
         for (int e = 0; e < 8; ++e) xs[e] = x[min(j0 + 64 * e, V - 1)];
     };
-    // m * 2^40 rounded down to an integer (m <= 2: an f32 mantissa times a
-    // power of two, so the product is exact in f64 and only the bits below
-    // 2^-40 are dropped)
-    auto fix40 = [](double m) -> unsigned long long { return (unsigned long long)(m * kGFix); };
     bool sums_done = false;   // kept mass of every chunk already in csum[]
     int64_t kept_pre = 0;     // and the kept count of this thread
 
@@ -511,11 +526,13 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             double zl = 0.0;
             NIS_G_EACH({
                 const float t = tpos(xr);
-                const double e = massx(xr);
-                zl += e;
+                uint32_t fm;
+                int me;
+                mparts(xr, fm, me);
+                zl += ldexp((double)fm, me - 24);
                 const uint32_t b = vbin(t);
                 atomicAdd(&sh.u.v.cnt[b], 1u);
-                atomicAdd(&sh.u.v.mass[b], fix40(e));
+                atomicAdd(&sh.u.v.mass[b], mfix(fm, me));
             })
             z_all = block_sum(zl, sh.dscr);
             const double pZ = (double)p * z_all;
@@ -631,7 +648,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                                 if (in_prefix(k, shift, prefix)) {
                                     const int d = (int)((k >> shift) & 255);
                                     atomicAdd(&sh.hcnt[d], 1u);
-                                    atomicAdd(&sh.hmass[d], fix40(massx(xl)));
+                                    atomicAdd(&sh.hmass[d], fixx(xl));
                                     atomicMax(&sh.hkey[d], (unsigned long long)k);
                                 }
                             }
@@ -674,7 +691,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                             const uint64_t k = (uint64_t)key32(xl) << 32;
                             if (k >= kstar) {
                                 const uint32_t jl = sh.u.v.li[i][tid];
-                                atomicAdd(&sh.csum[jl / kGChunk], fix40(massx(xl)));
+                                atomicAdd(&sh.csum[jl / kGChunk], fixx(xl));
                                 ++nkl;
                             }
                         }
