@@ -34,6 +34,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "sampled rows/s + HBM GB/s (% peak), B=256 x V=50257 fp32, T=0.8 top-p=0.9"
 GRAPH_MAX = 200          # launches per captured hipGraph in the timed region
 RESIDENT_MAX_V = 53245   # kRMaxV: the largest row one 1024-lane workgroup holds in registers
+LONG_SPARSE_MAX_V = 262141  # kLSMaxV: the longest row the single-read long kernel takes
 SPARSE_MAX_V = 53245     # kSMaxV
 
 
@@ -44,6 +45,9 @@ def routed_kernel(V, temperature, top_k, top_p, penalty, history=False):
     no_topk = top_k == 0 or top_k >= V
     if V > RESIDENT_MAX_V and temperature <= 0.0:
         return "sample_rows_long_kernel<greedy>"
+    if (RESIDENT_MAX_V < V <= LONG_SPARSE_MAX_V and 0.0 < top_p < 0.95 and (top_k == 0 or top_k >= V)
+            and (penalty == 1.0 or not history)):
+        return "sample_rows_long_sparse_kernel"
     if V > RESIDENT_MAX_V and (top_k == 0 or top_k >= V) and (penalty == 1.0 or not history):
         return "sample_rows_long_kernel<all>" if top_p >= 1.0 else "sample_rows_long_kernel<top-p>"
     pen = penalty != 1.0 and history

@@ -75,7 +75,9 @@ typedef struct nis_row_stats {
     uint32_t token;
     uint32_t kernel;/* 1 = a row kernel (sparse, dense, resident, long-row), 2 = general path */
     uint32_t reject;/* NIS_REJECT_*: kernel 2 -> why the row kernel handed the row on
-                       (SHAPE: no row kernel takes it); 0 if not */
+                       (SHAPE: no row kernel takes it); kernel 1 -> 0, or for a long
+                       top-p row, why the single-read path handed it to the
+                       long-row method that answered it */
 } nis_row_stats;
 
 /* nis_row_stats.reject: a row kernel declines a row it cannot prove exact

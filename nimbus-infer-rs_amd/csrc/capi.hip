@@ -164,10 +164,13 @@ nis::RowArgs row_args(const float* d_logits, int64_t ld, int64_t V, const nis_pa
 //   - 0 < top-k < V with any top-p > 0 and no penalty history: the sparse
 //     kernel's top-k form (the k-th largest found by count in the same
 //     histograms, top-p searched on the top-k mass);
-//   - V > 53245 (rows longer than the registers hold), no top-k: the
-//     512-lane long-row kernel (greedy, top-p off or top-p, the row read
-//     again from cache after its stream), then the general path on the rows
-//     it declined;
+//   - 53245 < V <= 262141, 0 < top-p < 0.95, no top-k, no penalty history:
+//     the 1024-lane long sparse kernel (the row read once, its candidates
+//     listed in LDS against a pooled sampled threshold; a declined row runs
+//     the long-row method, then the general path, inside the same kernel);
+//   - other rows with V > 53245, no top-k: the 512-lane long-row kernel
+//     (greedy, top-p off or top-p, the row read again from cache after its
+//     stream), then the general path on the rows it declined;
 //   - anything else (V < 256, top-p <= 0, top-k with a penalty history or
 //     past 53245, a penalty history on rows longer than the registers hold):
 //     the 512-lane general kernel.
@@ -211,6 +214,11 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
                (a.penalty == 1.0f || a.gen_ids == nullptr)) {
         // top-k (with top-p at any p > 0): found by count in the sparse path
         hipLaunchKernelGGL(nis::sample_rows_sparse_topk_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
+                           ctx->stream, a);
+    } else if (a.V > nis::kSMaxV && a.V <= nis::kLSMaxV && a.temperature > 0.0f && a.top_p > 0.0f &&
+               a.top_p < 0.95f && no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)) {
+        // long top-p rows, read once (declined rows finish inside the kernel)
+        hipLaunchKernelGGL(nis::sample_rows_long_sparse_kernel, dim3((unsigned)B), dim3(nis::kLSB), 0,
                            ctx->stream, a);
     } else if (a.V > nis::kDMaxV &&
                (a.temperature <= 0.0f || (no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)))) {

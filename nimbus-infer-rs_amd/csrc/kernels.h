@@ -4,6 +4,7 @@
 #include "resident_path.h"
 #include "dense_path.h"
 #include "long_path.h"
+#include "long_sparse_path.h"
 
 namespace nis {
 
@@ -51,6 +52,35 @@ __global__ __launch_bounds__(kSB) void sample_rows_sparse_pen_kernel(RowArgs a) 
 }
 __global__ __launch_bounds__(kSB) void sample_rows_sparse_topk_kernel(RowArgs a) {
     sparse_rows_body<false, true>(a);
+}
+
+// Top-p rows longer than the registers hold, read once: one 1024-lane
+// workgroup per row.  A row the single-read path declines runs the long-row
+// method (which reads it again) on the first 512 lanes, and the general path
+// when that declines too; the other waves leave first, as above.
+__global__ __launch_bounds__(kLSB) void sample_rows_long_sparse_kernel(RowArgs a) {
+    __shared__ union {
+        LSShared s;
+        LongShared lg;
+        GeneralShared g;
+    } sh;
+    const int row = (int)blockIdx.x;
+    if (a.done != nullptr && a.done[row]) return;  // a finished sequence (decode step)
+    asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
+                 "s"(a.penalty), "s"(a.top_k), "s"(a.gen_ids), "s"(a.gen_off));
+    uint32_t reject = NIS_REJECT_SHAPE;
+    if (lsparse_eligible(a, row)) {
+        reject = lsparse_row(a, row, sh.s);
+        if (reject == NIS_REJECT_NONE) return;
+    }
+    if (threadIdx.x >= kLB) return;
+    __syncthreads();
+    if (long_eligible<kLongTopP>(a, row)) {
+        reject = long_row<kLongTopP>(a, row, sh.lg, reject);
+        if (reject == NIS_REJECT_NONE) return;
+        __syncthreads();
+    }
+    general_row<1>(a, row, sh.g, reject);
 }
 
 // General path only (used by tests to cross-check the two paths).

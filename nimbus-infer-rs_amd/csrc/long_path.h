@@ -86,9 +86,11 @@ __device__ __forceinline__ bool long_eligible(const RowArgs a, int row) {
 
 // Returns NIS_REJECT_NONE when the row is done, else (uniformly across the
 // workgroup) why the general path must recompute it; nothing has been
-// written then.
+// written then.  `prior`: why the single-read path (long_sparse_path.h)
+// declined the row, when this runs after it (reported in the row's stats).
 template <int MODE>
-__device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, LongShared& sh) {
+__device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, LongShared& sh,
+                                             uint32_t prior = NIS_REJECT_NONE) {
     const int l = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const int tid = (int)threadIdx.x;
@@ -316,7 +318,7 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
             const double rho = exp2((double)R - (double)M * c64);  // 2^R units -> max-element units
             const double em = exp2((double)xq * c64 - (double)M * c64);
             write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)M / temp, Zk * rho, Zall * rho, u,
-                            (u == 0.0) ? 0.0 : em / (Zk * rho), kept, 1);
+                            (u == 0.0) ? 0.0 : em / (Zk * rho), kept, 1, prior);
         }
     };
 

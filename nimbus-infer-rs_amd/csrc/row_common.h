@@ -63,6 +63,21 @@ __device__ __forceinline__ void lds_put_x4_u16(uint64_t mask, uint32_t a, f4v v,
         : "memory");
 }
 
+// A 4-byte and a 1-byte LDS store by the lanes of `mask` only (as above).
+__device__ __forceinline__ void lds_put_f32_u8(uint64_t mask, uint32_t a, float v, uint32_t b,
+                                               uint32_t h) {
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %1\n\t"
+        "ds_write_b32 %2, %3\n\t"
+        "ds_write_b8 %4, %5\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "s"(mask), "v"(a), "v"(v), "v"(b), "v"(h)
+        : "memory");
+}
+
 // Value of a float4 slot that is not fully inside the row: the few head /
 // tail elements come from scalar loads, everything outside the row is -inf.
 __device__ __forceinline__ f4v fix_slot(f4v v, int f, int f_lo, int f_hi, int mis, int V, float h0,

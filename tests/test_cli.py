@@ -64,7 +64,8 @@ def test_bench_routing_constants_match_the_library():
     from conftest import PKG
     b = _bench()
     for fn, name, val in (("resident_path.h", "kRMaxV", b.RESIDENT_MAX_V),
-                          ("sparse_path.h", "kSMaxV", b.SPARSE_MAX_V)):
+                          ("sparse_path.h", "kSMaxV", b.SPARSE_MAX_V),
+                          ("long_sparse_path.h", "kLSMaxV", b.LONG_SPARSE_MAX_V)):
         with open(os.path.join(PKG, "csrc", fn)) as f:
             line = re.search(name + r"\s*=.*//\s*(\d+)", f.read()).group(1)
         assert int(line) == val, name
@@ -74,6 +75,13 @@ def test_bench_routing_constants_match_the_library():
     assert b.routed_kernel(50257, 0.7, 50, 1.0, 1.0) == "sample_rows_sparse_topk_kernel"
     assert b.routed_kernel(50257, 0.7, 50, 0.9, 1.3, history=True) == "sample_rows_kernel"
     assert b.routed_kernel(128256, 0.7, 50, 0.9, 1.0) == "sample_rows_kernel"
+    # long rows: top-p below 0.95 is read once; 0.95 and up, top-p off and
+    # greedy take the long-row kernel, and so do rows past 262141; a penalty
+    # history on a long row takes the general kernel
+    assert b.routed_kernel(128256, 0.8, 0, 0.9, 1.0) == "sample_rows_long_sparse_kernel"
+    assert b.routed_kernel(128256, 0.8, 0, 0.97, 1.0) == "sample_rows_long_kernel<top-p>"
+    assert b.routed_kernel(300000, 0.8, 0, 0.9, 1.0) == "sample_rows_long_kernel<top-p>"
+    assert b.routed_kernel(128256, 0.8, 0, 0.9, 1.2, history=True) == "sample_rows_kernel"
 
 
 def test_bench_refuses_more_than_one_gpu():

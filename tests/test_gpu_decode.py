@@ -119,6 +119,8 @@ def _run(sampler, B, V, steps, cap, params_kw, seed, kernels=None, sigma=2.0):
     # rows longer than the registers (the long-row kernel, whose penalised
     # rows are finished by the general path through the pending launch)
     (128256, dict(temperature=0.8, top_p=0.9, repetition_penalty=1.3), 8),
+    # no penalty: the single-read long kernel (top-p < 0.95)
+    (128256, dict(temperature=0.8, top_p=0.9), 5),
     (128256, dict(temperature=0.0, repetition_penalty=1.2), 3),
     (128256, dict(temperature=0.8, top_p=1.0, repetition_penalty=0.8), 8),
 ])

@@ -1,8 +1,11 @@
-"""GPU parity of the long-row kernel (nis_sample_batch with V > 53245, no
-top-k): greedy, top-p off and top-p of any nucleus size on rows streamed
-once and read again from cache, against the CPU oracle.  Where the rows fit
-the kernel's rules the test also checks that none was handed to the general
-path."""
+"""GPU parity of the long-row kernels (nis_sample_batch with V > 53245, no
+top-k) against the CPU oracle: the single-read kernel for 0 < top-p < 0.95
+(candidates listed in LDS against a pooled sampled threshold, the row read
+once), and the long-row kernel for greedy, top-p off, top-p >= 0.95 and
+penalty histories (the row read again from cache).  Where the rows fit a
+kernel's rules the test also checks which method answered them
+(nis_row_stats: kernel 1 with reject 0 for the single-read path, kernel 1
+with the single-read path's reason for the long-row method behind it)."""
 import numpy as np
 import pytest
 
@@ -31,7 +34,7 @@ def _check(sampler, x, V, T, p, seeds, ld=None, label=""):
 
 def test_c4_every_mode(sampler):
     # the Llama-3 vocabulary config (ties at the max on every tenth row):
-    # greedy, top-p 0.9 and top-p off, all on the long-row kernel
+    # greedy, top-p 0.9 (read once), top-p off and 0.99 (the long-row kernel)
     from nimbus_sampler import workloads
     w = workloads.WORKLOADS["c4"]
     x = w.make(64)
@@ -39,6 +42,99 @@ def test_c4_every_mode(sampler):
         rep = _check(sampler, x, w.V, T, p, list(range(64)), label=f"c4-T{T}-p{p}")
         if T > 0.0:
             assert rep["fast_rows"] == 64, rep
+        if p == 0.9:
+            assert rep["sparse_rows"] == 64, rep  # every row answered by the single read
+
+
+def test_c4_full_batch_single_read(sampler):
+    # all 512 rows of the config stay on the single-read path (a declined row
+    # would cost its CU two more reads of the row); parity on the first 64
+    import nimbus_sampler as ns
+    from nimbus_sampler import workloads
+    w = workloads.WORKLOADS["c4"]
+    x = w.make(512)
+    params = ns.SamplingParams(temperature=0.8, top_p=0.9)
+    gpu = run_gpu(sampler, x, w.V, params, list(range(512)))
+    st = gpu[1]
+    assert ((st["kernel"] == 1) & (st["reject"] == 0)).all(), (np.unique(st["kernel"]), np.unique(st["reject"]))
+    sub = (gpu[0][:64], st[:64], gpu[2][:64])
+    rep = compare(sub, run_oracle(x[:64], w.V, params, list(range(64))), greedy=False)
+    print(f"[long] c4 B=512 -> {rep}", flush=True)
+
+
+@pytest.mark.parametrize("V,ld_extra", [(53246, 0), (65537, 1), (100003, 3), (128256, 2), (151936, 0),
+                                        (200003, 1), (262141, 0)])
+def test_single_read_sizes_and_layouts(sampler, V, ld_extra):
+    # N(0, 2^2) rows at T 0.8 (nucleus ~11% of the row at p 0.9): on the
+    # single-read path while the lists hold that share (V up to ~160K),
+    # declined to the long-row method past it; p 0.5 everywhere
+    rnd = np.random.Generator(np.random.PCG64(V + 7))
+    B = 8
+    x = rnd.standard_normal((B, V), dtype=np.float32) * np.float32(2.0)
+    for p in (0.9, 0.5):
+        rep = _check(sampler, x, V, 0.8, p, list(range(B)), ld=V + ld_extra, label=f"single-read V{V} p{p}")
+        assert rep["fast_rows"] == B, rep
+        if V <= 151936 or p == 0.5:
+            assert rep["sparse_rows"] == B, rep
+
+
+def test_single_read_wide_nucleus_falls_back(sampler):
+    # near-flat rows at p 0.9 keep ~90% of the row: far below the listing
+    # threshold, so the single-read path declines (NIS_REJECT_WINDOW) and the
+    # long-row method answers inside the same kernel
+    import nimbus_sampler as ns
+    rnd = np.random.Generator(np.random.PCG64(31))
+    B, V = 8, 128256
+    x = rnd.uniform(-0.5, 0.5, size=(B, V)).astype(np.float32)
+    params = ns.SamplingParams(temperature=1.3, top_p=0.9)
+    gpu = run_gpu(sampler, x, V, params, list(range(B)))
+    st = gpu[1]
+    assert ((st["kernel"] == 1) & (st["reject"] == 3)).all(), (st["kernel"], st["reject"])
+    rep = compare(gpu, run_oracle(x, V, params, list(range(B))), greedy=False)
+    print(f"[long] flat p0.9 -> {rep}", flush=True)
+
+
+def test_single_read_peaks_low_temperature_and_ties(sampler):
+    # (a) a spike 30-60 logits above N(0,1) noise: the sample's threshold lies
+    # more than 31 octaves below the row max, so listed elements alias in the
+    # histogram ring and are subtracted again; (b) T 0.1-0.3 on N(0, 3^2)
+    # rows (the depth clamp); (c) values on a 1/64 lattice at T 1: each
+    # lattice value holds hundreds of tied elements, more than either long
+    # method ranks in its cutoff bucket, so these rows end on the general
+    # path (parity only)
+    rnd = np.random.Generator(np.random.PCG64(32))
+    B, V = 12, 128256
+    x = rnd.standard_normal((B, V), dtype=np.float32)
+    for r in range(B):
+        x[r, rnd.integers(0, V)] += np.float32(30.0 + 2.5 * r)
+    rep = _check(sampler, x, V, 0.8, 0.9, list(range(B)), label="spikes")
+    assert rep["sparse_rows"] == B, rep
+    y = rnd.standard_normal((B, V), dtype=np.float32) * np.float32(3.0)
+    for T in (0.1, 0.2, 0.3):
+        rep = _check(sampler, y, V, T, 0.9, list(range(B)), label=f"lowT{T}")
+        assert rep["sparse_rows"] == B, rep
+    z = (np.round(rnd.standard_normal((B, V)) * 2.0 * 64.0) / 64.0).astype(np.float32)
+    for p in (0.9, 0.6):
+        _check(sampler, z, V, 1.0, p, list(range(B)), label=f"lattice p{p}")
+
+
+def test_single_read_crowded_cutoff_bucket(sampler):
+    # a third of the row holds one value near the cutoff: its bucket has far
+    # more members than one wave ranks, on the single-read path and on the
+    # long-row method alike, so those rows end on the general path; the other
+    # rows (100-250 members per cutoff bucket) stay on the single read
+    import nimbus_sampler as ns
+    rnd = np.random.Generator(np.random.PCG64(33))
+    B, V = 6, 128256
+    x = rnd.standard_normal((B, V), dtype=np.float32) * np.float32(2.0)
+    x[:3, rnd.choice(V, size=V // 3, replace=False)] = np.float32(2.5)
+    params = ns.SamplingParams(temperature=0.8, top_p=0.9)
+    gpu = run_gpu(sampler, x, V, params, list(range(B)))
+    rep = compare(gpu, run_oracle(x, V, params, list(range(B))), greedy=False)
+    print(f"[long] crowded -> {rep} kernel={gpu[1]['kernel'].tolist()} reject={gpu[1]['reject'].tolist()}",
+          flush=True)
+    st = gpu[1]
+    assert ((st["kernel"][3:] == 1) & (st["reject"][3:] == 0)).all(), (st["kernel"], st["reject"])
 
 
 @pytest.mark.parametrize("V", [53246, 65537, 200003, 1 << 20])
