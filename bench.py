@@ -637,7 +637,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic: N(0,3^2) logits from PCG64 seed 7, 8 rotated batches resident in HBM",
+        "data": f"synthetic: {w.description}; 8 rotated batches resident in HBM",
         "config": {"workload": args.workload, "B": B, "V": V, "temperature": w.temperature,
                    "top_p": w.top_p, "top_k": args.top_k, "ld": V, "parallelism": "1 GPU",
                    "launch": f"hipGraph replays: {K // G} x {G} + {K % G} nis_sample_batch "

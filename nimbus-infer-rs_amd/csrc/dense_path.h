@@ -280,7 +280,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // issue, so each SIMD's share of chunks sets its length)
     const int nch = (nsl + 63) >> 6;
     const int cb = nch / kDW, cr = nch % kDW;
-    const int Kw = cb + (w < cr ? 1 : 0);  // <= kDN: V <= kDMaxV
+    int Kw = cb + (w < cr ? 1 : 0);  // <= kDN: V <= kDMaxV
     const int wbase = 64 * (cb * w + min(w, cr));
     const int slot0 = wbase + l;
     // row index of element 0 of chunk k of this lane
@@ -582,6 +582,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         if (l == 0) sh.u0 = u0;
         rst = (l == 0) ? st[0] : (l == 1) ? st[1] : (l == 2) ? st[2] : st[3];
     }
+    asm volatile("" : "+s"(Kw));  // (the chunk tests below recomputed, not kept live)
     // ---- B1: every wave's stream and histogram adds are done -----------------
     lds_barrier();
     NIS_DTS(2);
@@ -695,6 +696,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     const uint32_t nab0 = bcast_u32(cd.nab, Lb);
     NIS_DTS(3);
 
+    asm volatile("" : "+s"(Kw));  // (the chunk tests below recomputed, not kept live)
     // ---- listing: float4s that may hold members of b_p, and float4s of the
     // smaller side of the cutoff --------------------------------------------
     const bool kside = nab0 + nsel0 <= (uint32_t)V - nab0;  // few kept: list the kept side
@@ -735,6 +737,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     NIS_DTS(4);
     brute = brute || sh.over != 0u;
 
+    asm volatile("" : "+s"(Kw));  // (the chunk tests below recomputed, not kept live)
     // ---- the cutoff bucket's members: refined while more than kDMem ----------
     // Every float4 holding a member of b_p is on the listed side (or, when a
     // list overflowed, in this lane's registers); fn(x4, i0, valid) visits
@@ -949,6 +952,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         scL = sl;
     }
 
+    asm volatile("" : "+s"(Kw));  // (the chunk tests below recomputed, not kept live)
     // ---- kept masses: this wave's listed float4s, or all of its float4s -----
     // kept mass of float4 x4 (elements 0..3 at row index i0) and its stream
     // mass, from the same per-element masses the stream summed
@@ -1045,6 +1049,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         if (l == 0) sh.tw[w] = ldexp(Tw, (int)(Rz - R));  // 2^R units (exact)
     }
     if (w == 0 && l < 4) a.rng[4 * (int64_t)row + l] = rst;
+    asm volatile("" : "+s"(Kw));  // (the chunk tests below recomputed, not kept live)
     // ---- B6: per-wave kept masses -----------------------------------------------
     lds_barrier();
     NIS_DTS(7);
