@@ -262,35 +262,43 @@ void launch_lm_head_f(const nis::LmHeadArgs& a, bool vec, bool grouped, int nb, 
 }
 
 // The one-hidden-row GEMV (lm_head_row_kernel) when its shape holds: whole
-// 16-byte runs per row (H % R == 0), one scale per run, aligned operands and
-// at most KMAX runs per lane with 16 or 64 lanes per row.  Returns false to
-// leave the call to the matrix-core kernel.
+// runs per row (H % R == 0), one scale per run, aligned operands and at most
+// 4 runs per lane with 16 or 64 lanes per row (3 when they suffice, which
+// keeps fewer hidden values in registers).  Returns false to leave the call
+// to the matrix-core kernel.
 // nis_lm_head_greedy: workgroup keys kept per context (a fused launch of more
 // workgroups takes the two-launch form instead)
 constexpr int64_t kGreedyMaxBlocks = 1 << 16;
+
+template <int FMT, bool GREEDY, int KM>
+void launch_lm_head_row_km(const nis::LmHeadArgs& a, bool grouped, dim3 grid, hipStream_t st, int log2L,
+                           int runs) {
+    if (grouped)
+        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, true, GREEDY, KM>), grid, dim3(256), 0, st, a, log2L,
+                           runs);
+    else
+        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, false, GREEDY, KM>), grid, dim3(256), 0, st, a, log2L,
+                           runs);
+}
 
 template <int FMT, bool GREEDY = false>
 bool launch_lm_head_row(const nis::LmHeadArgs& a, bool grouped, uintptr_t wp, hipStream_t st,
                         int64_t* blocks = nullptr) {
     constexpr int R = nis::LhRowCfg<FMT>::R;
-    constexpr int KMAX = nis::LhRowCfg<FMT>::KMAX;
     if (a.H % R != 0 || (wp & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
     if (grouped && a.group % R != 0) return false;
     const int runs = a.H / R;
-    int log2L;
-    if ((runs + 15) / 16 <= KMAX) log2L = 4;
-    else if ((runs + 63) / 64 <= KMAX) log2L = 6;
+    int log2L, km;
+    if ((runs + 15) / 16 <= 4) log2L = 4, km = (runs + 15) / 16 <= 3 ? 3 : 4;
+    else if ((runs + 63) / 64 <= 4) log2L = 6, km = (runs + 63) / 64 <= 3 ? 3 : 4;
     else return false;
     const int64_t rows_per_wave = (int64_t)(64 >> log2L) * nis::LhRowCfg<FMT>::ITER;
     const int64_t waves = (a.V + rows_per_wave - 1) / rows_per_wave;
-    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    const dim3 grid((unsigned)((waves + 3) / 4));
     if (blocks) *blocks = (int64_t)grid.x;
     if (GREEDY && (int64_t)grid.x > kGreedyMaxBlocks) return false;
-    if (grouped)
-        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, true, GREEDY>), grid, block, 0, st, a, log2L, runs);
-    else
-        hipLaunchKernelGGL((nis::lm_head_row_kernel<FMT, false, GREEDY>), grid, block, 0, st, a, log2L,
-                           runs);
+    if (km == 3) launch_lm_head_row_km<FMT, GREEDY, 3>(a, grouped, grid, st, log2L, runs);
+    else launch_lm_head_row_km<FMT, GREEDY, 4>(a, grouped, grid, st, log2L, runs);
     return true;
 }
 

@@ -309,42 +309,63 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
 
 // One hidden row (B = 1, the reference's own decode shape): matrix-core tiles
 // would pad it to 16 rows, so this is a VALU GEMV streaming the head once.
-// Each lane takes 16-byte weight runs (4 f32, 16 int8 or 32 int4 codes) at
-// fixed h positions j*R, j = li + k*L, of one weight row; L (16 or 64) lanes
-// share a row, 64/L rows per wave step, kLhIter steps per wave.  The lane's
-// hidden values for those positions stay in registers across the steps; the
-// runs of D steps are in flight while a step is summed; the L partial sums
-// of a row meet in an XOR butterfly (fixed order, deterministic).
+// Each lane takes runs of R codes (16 bytes: 4 f32 or 16 int8; 8 bytes: 16
+// int4) at fixed h positions j*R, j = li + k*L (k < KM), of one weight row;
+// L (16 or 64) lanes share a row, 64/L rows per wave step, ITER steps per
+// wave.  The lane's hidden values for those positions stay in registers
+// across the steps, with their sum per run; the runs of D steps are in
+// flight while a step is summed; the L partial sums of a row meet in an XOR
+// butterfly (fixed order, deterministic).
+//
+// A quantized code is converted as the unsigned byte it is stored in (one
+// v_cvt_f32_ubyte per code: int8 bytes as they are, int4 nibbles spread one
+// per byte first), and the zero point (128, 8) comes off once per run:
+// sum (q - z) x = sum q x - z sum x.  The issue slots per code (one convert,
+// one fma) bound these kernels, not their bytes.
 
 template <int FMT>
 struct LhRowCfg {
-    static constexpr int R = FMT == kLhF32 ? 4 : (FMT == kLhInt8 ? 16 : 32);  // h per run
-    static constexpr int KMAX = FMT == kLhInt4 ? 2 : 4;                        // runs per lane
-    // measured at H = 768, V = 50257: more steps per wave (fewer waves) or
-    // more steps in flight per wave were slower for every format
-    static constexpr int ITER = FMT == kLhInt4 ? 8 : 4;                        // wave steps
-    static constexpr int D = FMT == kLhInt8 ? 2 : ITER;                        // steps in flight
+    static constexpr int R = FMT == kLhF32 ? 4 : 16;                         // h per run
+    static constexpr int RB = FMT == kLhInt4 ? 8 : 16;                      // bytes per run
+    // measured at H = 768, V = 50257 (wave steps, steps in flight): int8
+    // (4, 2) against (2, 2) (4, 4) (8, 4) (8, 8); int4 (4, 4) against (8, 8)
+    // (8, 4) (16, 8); f32 (4, 4)
+    static constexpr int ITER = 4;                                          // wave steps
+    static constexpr int D = FMT == kLhInt8 ? 2 : ITER;                     // steps in flight
 };
+template <int FMT> struct LhRunT { typedef uint4 T; };
+template <> struct LhRunT<kLhInt4> { typedef uint2 T; };
 
-template <int FMT, bool GROUPED>
-__device__ __forceinline__ float lh_run_dot(const uint4& raw, const float* xr) {
+// sum over the run of code * x, the zero point taken off with the run's sum of x
+template <int FMT>
+__device__ __forceinline__ float lh_run_dot(const typename LhRunT<FMT>::T& raw, const float* xr, float sx) {
     constexpr int R = LhRowCfg<FMT>::R;
     float part = 0.f;
-    const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+    if constexpr (FMT == kLhF32) {
+        const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-    for (int e = 0; e < R; ++e) {
-        float wv;
-        if (FMT == kLhF32) wv = __uint_as_float(wd[e]);
-        else if (FMT == kLhInt8) wv = (float)((int)((wd[e >> 2] >> (8 * (e & 3))) & 255u) - 128);
-        else {
-            // nibble e of word e/8, taken from the even or odd nibbles spread
-            // one per byte, so the convert is a single byte-lane conversion
-            const uint32_t spread = (e & 1) ? ((wd[e >> 3] >> 4) & 0x0F0F0F0Fu) : (wd[e >> 3] & 0x0F0F0F0Fu);
-            wv = (float)((spread >> (8 * ((e & 7) >> 1))) & 255u) - 8.0f;
+        for (int e = 0; e < R; ++e) part = fmaf(__uint_as_float(wd[e]), xr[e], part);
+        return part;
+    } else if constexpr (FMT == kLhInt8) {
+        const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < R; ++e) part = fmaf((float)((wd[e >> 2] >> (8 * (e & 3))) & 255u), xr[e], part);
+        return fmaf(-128.0f, sx, part);
+    } else {
+        // code e: word e/8, byte (e%8)/2, the low nibble for even e
+        const uint32_t wd[2] = {raw.x, raw.y};
+#pragma unroll
+        for (int wi = 0; wi < 2; ++wi) {
+            uint32_t lo = wd[wi] & 0x0F0F0F0Fu, hi = (wd[wi] >> 4) & 0x0F0F0F0Fu;
+            asm("" : "+v"(lo), "+v"(hi));  // (the masks hidden: byte conversions, not bit extracts)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                part = fmaf((float)((lo >> (8 * b)) & 255u), xr[8 * wi + 2 * b], part);
+                part = fmaf((float)((hi >> (8 * b)) & 255u), xr[8 * wi + 2 * b + 1], part);
+            }
         }
-        part = fmaf(wv, xr[e], part);
+        return fmaf(-8.0f, sx, part);
     }
-    return part;
 }
 
 // GREEDY: greedy decoding fused into the epilogue.  Each lane holding a
@@ -352,10 +373,11 @@ __device__ __forceinline__ float lh_run_dot(const uint4& raw, const float* xr) {
 // goes to a.part[blockIdx.x], and lm_head_greedy_final_kernel reduces those.
 // (The last workgroup to finish reducing them instead needs a release fence
 // per workgroup, which writes the L2 back each time: far slower.)
-template <int FMT, bool GROUPED, bool GREEDY = false>
+template <int FMT, bool GROUPED, bool GREEDY, int KM>
 __global__ __launch_bounds__(256) void lm_head_row_kernel(LmHeadArgs a, int log2L, int runs) {
     constexpr int R = LhRowCfg<FMT>::R;
-    constexpr int KMAX = LhRowCfg<FMT>::KMAX;
+    constexpr int RB = LhRowCfg<FMT>::RB;
+    typedef typename LhRunT<FMT>::T RunT;
     const int lane = threadIdx.x & 63;
     const int L = 1 << log2L;
     const int li = lane & (L - 1);
@@ -376,45 +398,53 @@ __global__ __launch_bounds__(256) void lm_head_row_kernel(LmHeadArgs a, int log2
     const int64_t row_bytes = FMT == kLhF32 ? (int64_t)a.H * 4 : (FMT == kLhInt8 ? (int64_t)a.H : (int64_t)a.H / 2);
 
     constexpr int D = LhRowCfg<FMT>::D;
-    uint4 ring[D][KMAX];
-    auto load_step = [&](int it, uint4* dst) {
+    RunT ring[D][KM];
+    auto load_step = [&](int it, RunT* dst) {
         const int64_t vl = min(wave_row0 + it * P + gl, a.V - 1);
         const uint8_t* wrow = (const uint8_t*)a.w + vl * row_bytes;
 #pragma unroll
-        for (int k = 0; k < KMAX; ++k) {
+        for (int k = 0; k < KM; ++k) {
+            // (every load made, from an address clamped into the row, and
+            // zeroed after: no branch around a load)
             const int j = li + k * L;
-            dst[k] = j < runs ? *(const uint4*)(wrow + (int64_t)j * 16) : make_uint4(0u, 0u, 0u, 0u);
+            const RunT v = *(const RunT*)(wrow + (int64_t)min(j, runs - 1) * RB);
+            RunT z{};
+            dst[k] = j < runs ? v : z;
         }
     };
 #pragma unroll
     for (int it = 0; it < D; ++it) load_step(it, ring[it]);
-    float xr[KMAX][R];
+    float xr[KM][R];
+    float sx[KM];
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
+    for (int k = 0; k < KM; ++k) {
         const int j = li + k * L;
+        sx[k] = 0.f;
 #pragma unroll
         for (int q = 0; q < R / 4; ++q) {
-            lh_f4 xv = j < runs ? *(const lh_f4*)(a.x + (int64_t)j * R + 4 * q) : lh_f4{0.f, 0.f, 0.f, 0.f};
+            const lh_f4 xl = *(const lh_f4*)(a.x + (int64_t)min(j, runs - 1) * R + 4 * q);
+            const lh_f4 xv = j < runs ? xl : lh_f4{0.f, 0.f, 0.f, 0.f};
             xr[k][4 * q] = xv[0];
             xr[k][4 * q + 1] = xv[1];
             xr[k][4 * q + 2] = xv[2];
             xr[k][4 * q + 3] = xv[3];
+            sx[k] += (xv[0] + xv[1]) + (xv[2] + xv[3]);
         }
     }
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t v = wave_row0 + it * P + gl;
         const int64_t vl = min(v, a.V - 1);
-        uint4 cur[KMAX];
+        RunT cur[KM];
 #pragma unroll
-        for (int k = 0; k < KMAX; ++k) cur[k] = ring[it % D][k];
+        for (int k = 0; k < KM; ++k) cur[k] = ring[it % D][k];
         if (it + D < ITER) load_step(it + D, ring[it % D]);
         float acc = 0.f;
 #pragma unroll
-        for (int k = 0; k < KMAX; ++k) {
+        for (int k = 0; k < KM; ++k) {
             const int j = li + k * L;
             if (j < runs) {
-                const float part = lh_run_dot<FMT, GROUPED>(cur[k], xr[k]);
+                const float part = lh_run_dot<FMT>(cur[k], xr[k], sx[k]);
                 if (GROUPED) acc = fmaf(part, a.scales[vl * a.groups + lh_group_of(a, j * R)], acc);
                 else acc += part;
             }
