@@ -77,14 +77,17 @@ def _run(sampler, fmt, B, H, V, group=None, pad_h=0, pad_v=0, seed=0):
     (0, 1, 768, 50257, None, 0, 0),      # 64 lanes per row, 3 runs per lane
     (8, 1, 768, 50257, None, 0, 0),      # 16 lanes per row
     (8, 1, 768, 3001, 48, 0, 0),         # groups of 48 = 3 runs of 16
-    (4, 1, 768, 50257, 64, 0, 0),        # int4 groups of 64, 24 runs per row
-    (4, 1, 4096, 999, None, 0, 0),       # 64 lanes, 2 runs per lane
+    (4, 1, 768, 50257, 64, 0, 0),        # int4 groups of 64, 48 runs of 16 codes per row
+    (4, 1, 4096, 999, None, 0, 0),       # 64 lanes, 4 runs per lane
+    (4, 1, 784, 1000, None, 0, 0),       # int4, 49 runs: 16 lanes, 4 runs per lane, some idle
+    (8, 1, 1024, 999, None, 0, 0),       # int8, 64 runs: 16 lanes, 4 runs per lane
+    (8, 1, 768, 500, 16, 0, 0),          # int8, groups of one run
     (0, 1, 1024, 777, None, 0, 0),       # 64 lanes, 4 runs per lane (the cap)
     (0, 1, 4096, 300, None, 0, 0),       # over the cap: matrix-core kernel
     (8, 1, 96, 130, 8, 0, 0),            # group 8 < run of 16: matrix-core kernel
     (8, 3, 40, 77, 1, 0, 0),             # int8, one scale per weight (group 1)
     (8, 1, 40, 77, 1, 0, 0),             # the same through the one-row dispatch
-    (4, 1, 40, 65, None, 0, 0),          # H % 32 != 0: matrix-core kernel
+    (4, 1, 40, 65, None, 0, 0),          # int4 H % 16 != 0: matrix-core kernel
 ])
 def test_lm_head_matches_exact_sum_within_f32_bound(sampler, fmt, B, H, V, group, pad_h, pad_v):
     worst = _run(sampler, fmt, B, H, V, group, pad_h, pad_v, seed=B + H + V)
@@ -207,10 +210,10 @@ def _greedy_case(sampler, fmt, H, V, group=None, seed=0, tweak=None, with_logits
     (8, 768, 50257, None),    # int8, 16 lanes per row
     (8, 768, 50257, 64),      # int8 grouped
     (4, 768, 50257, 64),      # int4 grouped
-    (4, 4096, 999, None),     # 64 lanes, 2 runs per lane
+    (4, 4096, 999, None),     # 64 lanes, 4 runs per lane
     (0, 1024, 777, None),     # a grid of few workgroups, the last one partly past V
     (0, 4096, 300, None),     # over the one-row kernel's cap: the two-launch form
-    (4, 40, 65, None),        # int4 H % 32 != 0: the two-launch form
+    (4, 40, 65, None),        # int4 H % 16 != 0: the two-launch form
 ])
 def test_greedy_matches_argmax_of_the_logits(sampler, fmt, H, V, group):
     for seed in range(3):
