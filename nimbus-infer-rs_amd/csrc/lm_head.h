@@ -34,6 +34,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "device_common.h"
 
 namespace nis {
 
@@ -314,8 +315,8 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmHeadArgs a) {
 // L (16 or 64) lanes share a row, 64/L rows per wave step, ITER steps per
 // wave.  The lane's hidden values for those positions stay in registers
 // across the steps, with their sum per run; the runs of D steps are in
-// flight while a step is summed; the L partial sums of a row meet in an XOR
-// butterfly (fixed order, deterministic).
+// flight while a step is summed; the L partial sums of a row meet in a DPP
+// scan (fixed order, deterministic).
 //
 // A quantized code is converted as the unsigned byte it is stored in (one
 // v_cvt_f32_ubyte per code: int8 bytes as they are, int4 nibbles spread one
@@ -449,8 +450,18 @@ __global__ __launch_bounds__(256) void lm_head_row_kernel(LmHeadArgs a, int log2
                 else acc += part;
             }
         }
-        for (int off = L >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-        if (li == 0 && v < a.V) {
+        // the L partial sums of the row, in the VALU: an inclusive DPP scan
+        // inside each 16-lane row (L = 16) or over the wave (L = 64), the
+        // row's sum landing in its last lane (fixed order, deterministic)
+        if (log2L == 4) {
+            acc += __uint_as_float(dpp0<0x111>(__float_as_uint(acc)));
+            acc += __uint_as_float(dpp0<0x112>(__float_as_uint(acc)));
+            acc += __uint_as_float(dpp0<0x114>(__float_as_uint(acc)));
+            acc += __uint_as_float(dpp0<0x118>(__float_as_uint(acc)));
+        } else {
+            acc = wscan_f32(acc);
+        }
+        if (li == L - 1 && v < a.V) {
             if (FMT != kLhF32 && !GROUPED) acc *= a.scales[v];  // dot * scale (quant.rs:128)
             if (!GREEDY || a.out != nullptr) a.out[v] = acc;
             if (GREEDY) {
