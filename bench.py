@@ -213,9 +213,14 @@ def bench_floor(args, w, sampler, bufs):
     B, V = w.B, w.V
     out = torch.empty((B, 2), dtype=torch.float32, device=bufs[0].device)
     nb = len(bufs)
+    S = args.split
+    part = torch.empty((max(S, 1) * B * 4, 4), dtype=torch.float32, device=bufs[0].device)
 
     def launch(i):
-        sampler.stream_floor(bufs[i % nb], w.temperature, out=out)
+        if S:
+            sampler.stream_floor_split(bufs[i % nb], w.temperature, S, out=out, part=part)
+        else:
+            sampler.stream_floor(bufs[i % nb], w.temperature, out=out)
 
     for i in range(args.warmup):
         launch(i)
@@ -235,18 +240,22 @@ def bench_floor(args, w, sampler, bufs):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / K
     alg_bytes = B * 4 * V
+    what = (f"each row split over {S} workgroups of 256 lanes, partials merged by a second launch"
+            if S else "the sparse kernel's layout")
     print(json.dumps({
-        "metric": f"stream floor: rows/s + HBM GB/s (% peak), B={B} x V={V} fp32 read with the "
-                  f"sparse kernel's layout (max and exp-sum only, nothing sampled)",
+        "metric": f"stream floor: rows/s + HBM GB/s (% peak), B={B} x V={V} fp32 read with "
+                  f"{what} (max and exp-sum only, nothing sampled)",
         "value": B / (us * 1e-6), "unit": "rows/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "us_per_step": us, "higher_is_better": True,
         "data": "synthetic logits of the workload, 8 rotated batches resident in HBM",
         "config": {"workload": args.workload, "B": B, "V": V,
-                   "launch": f"hipGraph replays of up to {G} nis_stream_floor launches"},
+                   "launch": f"hipGraph replays of up to {G} "
+                             f"{'nis_stream_floor_split calls (2 launches each)' if S else 'nis_stream_floor launches'}"},
         "roofline": {"bound": "hbm", "achieved": alg_bytes / (us * 1e-6) / 1e9,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                     "kernel": "stream_floor_kernel", "launch_interval_us": us,
+                     "kernel": "split_floor_part_kernel + split_floor_merge_kernel" if S
+                     else "stream_floor_kernel", "launch_interval_us": us,
                      "alg_bytes_per_launch": alg_bytes},
     }))
 
@@ -467,6 +476,10 @@ def main():
                     help="time nis_stream_floor instead: the sparse kernel's layout and load "
                          "pipeline computing only each row's max and exp-sum (the bandwidth "
                          "ceiling the sampler's roofline fraction is measured against)")
+    ap.add_argument("--split", type=int, default=0, metavar="S",
+                    help="with --floor: time nis_stream_floor_split, each row read by S "
+                         "workgroups and merged by a second launch (the least a sampler that "
+                         "splits rows pays per merge)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 4 plain device copies of MIB MiB (reads MIB, writes MIB) "
                          "to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")

@@ -238,6 +238,17 @@ int nis_lm_head_greedy(nis_ctx* ctx, const float* d_hidden, int32_t H, const nis
 int nis_stream_floor(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
                      float temperature, float* d_out);
 
+/* Measurement only: the floor of splitting rows over workgroups.  Row b is
+ * read by S workgroups of 256 lanes (a slice of the row's float4 slots
+ * each, 1 <= S <= 64, at most 4096 slots per slice); each of their waves
+ * writes its slice's max and sum of 2^(x c - R_w) to d_part (B * S * 4
+ * records of 16 bytes, 16-byte aligned), and a second launch merges a row's
+ * records into d_out as nis_stream_floor does.  No counterpart in the
+ * reference: bench.py --floor --split S times it, the least any sampler
+ * that splits rows pays per merge.  Asynchronous on the context stream. */
+int nis_stream_floor_split(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                           float temperature, int32_t S, void* d_part, float* d_out);
+
 /* Wait for all work queued on the context stream. */
 int nis_sync(nis_ctx* ctx);
 

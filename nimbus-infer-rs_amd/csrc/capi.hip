@@ -626,6 +626,30 @@ int nis_stream_floor(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B,
     return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "stream floor launch");
 }
 
+int nis_stream_floor_split(nis_ctx* ctx, const float* d_logits, int64_t ld, int32_t B, int64_t V,
+                           float temperature, int32_t S, void* d_part, float* d_out) {
+    if (!ctx) return NIS_EINVAL;
+    if (!d_logits || !d_out || !d_part) return fail(ctx, NIS_EINVAL, "null pointer argument");
+    if (B <= 0 || V < 256 || V > nis::kSMaxV || ld < V)
+        return fail(ctx, NIS_EINVAL, "B must be positive, 256 <= V <= 53245 and ld >= V");
+    if (B > NIS_MAX_B) return fail(ctx, NIS_ERANGE, "B too large");
+    const int64_t nsl = (V + 3 + 3) / 4;  // slots touching a row (at most)
+    if (S < 1 || S > 64 || (nsl + S - 1) / S > (int64_t)nis::kFPB * nis::kFPN)
+        return fail(ctx, NIS_EINVAL, "S must be 1..64 with at most 4096 float4 slots per slice");
+    if (((uintptr_t)d_logits & 3u) || ((uintptr_t)d_out & 3u) || ((uintptr_t)d_part & 15u))
+        return fail(ctx, NIS_EALIGN, "logits and out must be 4-byte, part 16-byte aligned");
+    if (!(temperature > 0.0f)) return fail(ctx, NIS_EINVAL, "temperature must be positive");
+    DeviceGuard g(ctx->device);
+    if (g.status != hipSuccess) return hip_fail(ctx, g.status, "hipSetDevice");
+    const float c = (float)(1.4426950408889634 / fmax((double)temperature, 1e-6));
+    hipLaunchKernelGGL(nis::split_floor_part_kernel, dim3((unsigned)S, (unsigned)B), dim3(nis::kFPB), 0,
+                       ctx->stream, d_logits, ld, (int)V, c, (int)S, (float4*)d_part);
+    hipLaunchKernelGGL(nis::split_floor_merge_kernel, dim3((unsigned)B), dim3(64), 0, ctx->stream,
+                       (const float4*)d_part, (int)S, c, d_out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NIS_OK : hip_fail(ctx, e, "split stream floor launch");
+}
+
 int nis_sync(nis_ctx* ctx) {
     if (!ctx) return NIS_EINVAL;
     DeviceGuard g(ctx->device);

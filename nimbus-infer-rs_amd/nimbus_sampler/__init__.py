@@ -36,7 +36,7 @@ EXPORTED_SYMBOLS = (
     "nis_rng_next_f64", "nis_rng_seed_batch", "nis_sample_batch", "nis_argmax_batch",
     "nis_apply_repetition_penalty", "nis_sample_one", "nis_sample_one_noalloc", "nis_sync",
     "nis_decode_step",
-    "nis_lm_head_logits", "nis_lm_head_greedy", "nis_stream_floor",
+    "nis_lm_head_logits", "nis_lm_head_greedy", "nis_stream_floor", "nis_stream_floor_split",
 )
 
 
@@ -115,9 +115,12 @@ def load_library(path: str = LIB_PATH):
     L.nis_sync.argtypes = [vp]
     L.nis_stream_floor.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_float, vp]
+    L.nis_stream_floor_split.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                                         ctypes.c_float, ctypes.c_int32, vp, vp]
     for name in ("nis_ctx_create", "nis_ctx_destroy", "nis_ctx_set_stream", "nis_rng_seed_batch",
                  "nis_sample_batch", "nis_argmax_batch", "nis_apply_repetition_penalty",
-                 "nis_sample_one", "nis_sample_one_noalloc", "nis_sync", "nis_stream_floor"):
+                 "nis_sample_one", "nis_sample_one_noalloc", "nis_sync", "nis_stream_floor",
+                 "nis_stream_floor_split"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -379,6 +382,26 @@ class Sampler:
         rc = self._L.nis_stream_floor(self._ctx, ctypes.c_void_p(logits.data_ptr()),
                                       logits.stride(0), B, V, ctypes.c_float(temperature),
                                       ctypes.c_void_p(out.data_ptr()))
+        _check(self._L, self._ctx, rc)
+        return out
+
+    def stream_floor_split(self, logits, temperature: float, S: int, V: Optional[int] = None,
+                           out=None, part=None):
+        """Measurement only (nis_stream_floor_split): stream_floor's result
+        with each row read by S workgroups and their per-wave partials merged
+        by a second launch; part is a [B * S * 4, 4] float32 workspace."""
+        import torch
+        B = logits.shape[0]
+        V = logits.shape[1] if V is None else V
+        if out is None:
+            out = torch.empty((B, 2), dtype=torch.float32, device=logits.device)
+        if part is None:
+            part = torch.empty((B * S * 4, 4), dtype=torch.float32, device=logits.device)
+        self._bind_stream()
+        rc = self._L.nis_stream_floor_split(self._ctx, ctypes.c_void_p(logits.data_ptr()),
+                                            logits.stride(0), B, V, ctypes.c_float(temperature), S,
+                                            ctypes.c_void_p(part.data_ptr()),
+                                            ctypes.c_void_p(out.data_ptr()))
         _check(self._L, self._ctx, rc)
         return out
 
