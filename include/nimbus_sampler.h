@@ -70,7 +70,8 @@ typedef struct nis_row_stats {
     double z_all;   /* same sum before top-p (top-p `sum`, sampler.rs:143); 0 if top-p inactive */
     double u;       /* next_f64() drawn (sampler.rs:209); -1 when the RNG was not advanced */
     double prob;    /* exp(w_token - max_w) / z_kept for a drawn token, else 0 */
-    uint64_t kept;  /* tokens surviving top-k / top-p */
+    uint64_t kept;  /* tokens surviving top-k / top-p; counted on the DRAW and
+                       FALLTHROUGH paths, 0 on the others */
     uint32_t path;  /* NIS_PATH_* */
     uint32_t token;
     uint32_t kernel;/* 1 = a row kernel (sparse, dense, resident, long-row), 2 = general path */

@@ -417,6 +417,9 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     const double rho = mf32 ? 1.0 / massx((float)M) : 1.0;
     auto mass_w = [&](double wv) -> double {  // wv = value / T (penalised rows)
         const double t = (wv - M_w) * 1.4426950408889634;
+        // far below f32's exp2 range (wv = -inf included, where t - th would
+        // be NaN): mass 0
+        if (!(t > -256.0)) return 0.0;
         const float th = (float)t;
         return (double)__builtin_amdgcn_exp2f(th) * (1.0 + (t - (double)th) * 0.6931471805599453);
     };
@@ -829,7 +832,10 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                 kp = tie ? ((int64_t)tr < n_keep) : kp;
                 rowbase += (uint32_t)__popcll(mt);
             }
-            kp = kp && in;
+            // (a -inf survivor of top-k or of top-p off has mass 0: it can
+            // never end the walk, and the kept count, like the reference's
+            // finite survivors, leaves it out)
+            kp = kp && in && (v > -INFINITY);
             km |= kp ? (1u << e) : 0u;
             e8[e] = kp ? massv(v, xs[e]) : 0.0;
         }

@@ -243,12 +243,13 @@ uint32_t oracle_sample(const float* logits, size_t n, const oracle_params* param
         double max = -INFINITY;                                            /* 191 */
         for (size_t i = 0; i < n; ++i) max = fmax(max, work[i]);
         st.max_w = max;
-        for (size_t i = 0; i < n; ++i) st.kept += isfinite(work[i]) ? 1 : 0;
         if (!isfinite(max)) {                                              /* 192-200 */
             token = (uint32_t)first_argmax(work, n);
             st.path = ORACLE_PATH_NONFINITE_MAX;
             goto done;
         }
+        uint64_t kept = 0;  /* entries still finite after the filters */
+        for (size_t i = 0; i < n; ++i) kept += isfinite(work[i]) ? 1 : 0;
         double total = 0.0;                                                /* 201-205 */
         for (size_t i = 0; i < n; ++i) {
             work[i] = exp(work[i] - max);
@@ -260,6 +261,7 @@ uint32_t oracle_sample(const float* logits, size_t n, const oracle_params* param
             st.path = ORACLE_PATH_BAD_TOTAL;
             goto done;
         }
+        st.kept = kept;  /* reported on the draw paths only (0 on the ones above) */
         const double u = oracle_rng_next_f64(state);                      /* 209 */
         double r = u * total;
         st.u = u;

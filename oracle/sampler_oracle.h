@@ -66,7 +66,8 @@ typedef struct oracle_stats {
     double prob;         /* work[token] / total for a drawn token, else 0 */
     double topp_margin;  /* min_pos |cum - probs[pos] - p| over finite entries (sampler.rs:150), +inf if inactive */
     double cdf_margin;   /* distance of r to the nearest CDF boundary / total (sampler.rs:209-215), +inf if no draw */
-    uint64_t kept;       /* entries still finite after top-k / top-p */
+    uint64_t kept;       /* entries still finite after top-k / top-p, on the
+                            draw and walk-overshoot paths; 0 on the others */
     uint32_t path;       /* ORACLE_PATH_* */
     uint32_t token;
 } oracle_stats;

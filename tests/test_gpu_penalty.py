@@ -417,3 +417,26 @@ def test_dense_strong_penalties(sampler, pen, T, p, on):
         assert ((st["kernel"] == 1) | (st["reject"] == 2)).all(), (st["kernel"].tolist(), st["reject"].tolist())
     drew = sum(int(gpu[0][r]) in set(gen[r].tolist()) for r in range(B))
     print(f"[penalty] dense strong pen={pen}: rows that drew a penalised token {drew}/{B}", flush=True)
+
+
+@pytest.mark.parametrize("V,k,p", [(100000, 0, 0.65), (100000, 0, 1.0), (151936, 0, 0.9),
+                                   (50257, 40, 0.9), (100000, 5000, 1.0)])
+def test_penalised_masked_rows_on_the_general_path(sampler, V, k, p):
+    # penalised rows with -inf entries that the general path answers (long
+    # rows with a history, top-k with a history): a -inf element's mass is 0
+    # (it was NaN in the f64 correction of the penalised mass, which turned
+    # the total into NaN and the row into the bad-total path), and the kept
+    # count holds only finite survivors, as the reference's filtered row
+    # does (a -inf survivor of top-k or of top-p off is not counted)
+    B = 6
+    rnd = np.random.Generator(np.random.PCG64(V + k))
+    x = (rnd.standard_normal((B, V)) * 0.3).astype(np.float32)
+    for r in range(B):
+        x[r, rnd.random(V) < rnd.uniform(0.1, 0.9)] = -np.inf
+    x[5, :] = -np.inf
+    x[5, 123] = 0.5  # one finite element
+    gen = [rnd.integers(0, V + 16, size=int(rnd.integers(1, 600))) for _ in range(B)]
+    gpu, ref = _check(sampler, x, V, _params(temperature=1.9, top_p=p, top_k=k, repetition_penalty=1.119),
+                      gen, f"masked general V={V} k={k} p={p}", on_kernel=False)
+    assert (ref[1]["path"] == 4).all()
+    assert np.array_equal(gpu[1]["kept"], ref[1]["kept"])
