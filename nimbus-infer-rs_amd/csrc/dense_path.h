@@ -169,6 +169,8 @@ struct NucleusShared {
                                       //   kept masses (listed rows, after the cutoff)
     uint32_t kmax;                    // the waves' maxima, reduced as they arrive (key32)
     uint32_t krw0;                    //   their first references (min, key32)
+    uint32_t krw0hi;                  //   the highest of those of the waves holding
+                                      //   data (max, key32)
     uint32_t fnan;                    //   a NaN seen
     uint32_t kpl;                     // PEN: the plain elements' max (key32; kmax also
                                       //   holds the penalised values rounded up)
@@ -323,6 +325,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         sh.over = 0u;
         sh.kmax = 0u;
         sh.krw0 = 0xFFFFFFFFu;
+        sh.krw0hi = 0u;
         sh.fnan = 0u;
         if (PEN) {
             sh.kpl = 0u;
@@ -391,7 +394,31 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     // ---- stream: chunk masses, max, and every element into the ring --------
     NIS_DFIX(0);
     // (PEN: of the plain elements; the stream leaves the penalised ones out)
-    const float m0 = wmax_f32(r_max4((PEN && (pany & 1u)) ? d_mask4(xv[0], (uint32_t)pnl & 15u) : xv[0]));
+    float m0 = wmax_f32(r_max4((PEN && (pany & 1u)) ? d_mask4(xv[0], (uint32_t)pnl & 15u) : xv[0]));
+    if (m0 == -INFINITY && Kw > 1) {
+        // chunk 0 holds nothing above -inf (a masked stretch): the first
+        // reference comes from the wave's whole run instead, every chunk's
+        // load issued now (the stream issues them again as usual), so that
+        // no element of the wave lies above it or folds below a floor set
+        // too high
+#pragma unroll
+        for (int k = kDD; k < kDN; ++k) NIS_DLOAD(k);
+        float mw = -INFINITY;
+#pragma unroll
+        for (int k = 1; k < kDN; ++k) {
+            if (k < Kw) {
+                f4v t = xv[k];
+                if (edge_wave) {
+                    const int fb0 = wbase + k * 64;
+                    if (fb0 < f_lo || fb0 + 63 > f_hi)
+                        t = fix_slot(t, slot0 + k * 64, f_lo, f_hi, mis, V, h0, h1, h2, t0, t1, t2);
+                }
+                if (PEN && ((pany >> k) & 1u)) t = d_mask4(t, (uint32_t)(pnl >> (4 * k)) & 15u);
+                mw = fmaxf(mw, r_max4(t));
+            }
+        }
+        m0 = wmax_f32(mw);
+    }
     const float Rw0 = (m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f;
     // elements more than 64 octaves below the first reference share one bucket
     const float tflo = (Rw0 - (float)kDSpan) * 64.0f;
@@ -561,6 +588,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
             if (Kw > 0) {
                 atomicMax(&sh.kmax, key32(mx == mx ? mx : -INFINITY));
                 atomicMin(&sh.krw0, key32(Rw0));
+                if (mx > -INFINITY || (PEN && pany != 0u)) atomicMax(&sh.krw0hi, key32(Rw0));
             }
             if (nan_seen) atomicOr(&sh.fnan, 1u);
             if (PEN && Kw > 0) atomicMax(&sh.kpl, key32(mx == mx ? mx : -INFINITY));
@@ -593,9 +621,13 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     {
         const bool anynan = sh.fnan != 0u;
         const float rw0min = unkey32(sh.krw0);
-        // |M c| < 4096 keeps the finest bucket index floor(64^3 x c) in range
+        const float rw0hi = sh.krw0hi ? unkey32(sh.krw0hi) : -INFINITY;
+        // |M c| < 4096 keeps the finest bucket index floor(64^3 x c) in range;
+        // no wave may fold what lies within the searched octaves (R above
+        // every first reference of a wave holding data, less than 64 octaves
+        // above the lowest)
         const bool ok = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
-                        (R - rw0min < (float)kDSpan);
+                        (R - rw0min < (float)kDSpan) & (rw0hi <= R);
         if (!ok) {
             NIS_DTFLUSH();
             return NIS_REJECT_NONFINITE;

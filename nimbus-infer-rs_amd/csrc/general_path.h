@@ -333,6 +333,62 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     const bool topp_zero = (p <= 0.0f);
     const bool topp_on = (p > 0.0f) && (p < 1.0f);  // NaN p: neither branch
 
+    // ---- a NaN row at top-p <= 0 without top-k (sampler.rs:122-134) -----
+    // max_by hands the running maximum on at every comparison that is not
+    // Greater, NaN on either side included, so the entry it keeps is the
+    // last index of the maximum of w past the last NaN (at L), or L itself
+    // when the NaN is the last entry.  Every other entry becomes -inf: a
+    // finite kept value is drawn with mass 1 (index 0 when u = 0, as the
+    // walk stops there), +inf is the non-finite-max argmax, and a kept NaN
+    // or -inf returns 0.  (With top-k active the k-th value comes from a
+    // sort whose comparator NaN makes inconsistent: not handled here.)
+    if (any_nan && p <= 0.0f && !(a.top_k > 0 && a.top_k < (uint64_t)V)) {
+        int64_t lnan = -1;
+        NIS_G_EACH({ lnan = (pval(j, xr) != pval(j, xr)) ? max(lnan, j) : lnan; })
+        lnan = block_max(lnan, sh.iscr);
+        double smax = -INFINITY;
+        int64_t slast = -1;
+        NIS_G_EACH({
+            if (j > lnan) {
+                const double wv = pval(j, xr) / temp;  // sampler.rs:184-186
+                const bool take = slast < 0 || wv > smax || (wv == smax && j > slast);
+                smax = take ? wv : smax;
+                slast = take ? j : slast;
+            }
+        })
+        const double S = block_max(slast >= 0 ? smax : -INFINITY, sh.dscr);
+        slast = block_max((slast >= 0 && smax == S) ? slast : (int64_t)-1, sh.iscr);
+        const bool kept_nan = lnan == V - 1;
+        const int64_t best = kept_nan ? lnan : slast;
+        const double keep = kept_nan ? (double)NAN : S;
+        if (w == 0) {
+            if (keep > -INFINITY && keep < INFINITY) {
+                uint64_t st[4];  // sampler.rs:209
+                const uint64_t* sp = a.rng + 4 * (int64_t)row;
+                st[0] = sp[0];
+                st[1] = sp[1];
+                st[2] = sp[2];
+                st[3] = sp[3];
+                const double u = rng_next_f64(st);
+                if (l == 0) {
+                    uint64_t* so = a.rng + 4 * (int64_t)row;
+                    so[0] = st[0];
+                    so[1] = st[1];
+                    so[2] = st[2];
+                    so[3] = st[3];
+                    const uint32_t tok = (u == 0.0) ? 0u : (uint32_t)best;
+                    write_row_result(a, row, tok, NIS_PATH_DRAW, keep, 1.0, 0.0, u,
+                                     (tok == (uint32_t)best) ? 1.0 : 0.0, 1, 2, reject);
+                }
+            } else if (l == 0) {
+                const uint32_t tok = (keep == INFINITY) ? (uint32_t)best : 0u;
+                write_row_result(a, row, tok, NIS_PATH_NONFINITE_MAX, keep == INFINITY ? keep : -INFINITY, 0.0, 0.0, -1.0, 0.0,
+                                 0, 2, reject);
+            }
+        }
+        return true;
+    }
+
     // ---- non-finite rows ------------------------------------------------
     // NaN survives every filter (all comparisons with NaN are false), so
     // `total` is NaN (sampler.rs:206) unless +inf makes the max non-finite

@@ -85,7 +85,8 @@ struct alignas(16) RRec {
     uint32_t nc;   // top-p off with stats: the wave's elements above -inf (greedy
                    // with a penalty: the first index of that penalised value)
     uint32_t bad;  // the wave saw input this path does not take
-    uint32_t pad;
+    uint32_t high; // top-p off: the wave's reference ended more than 64 octaves
+                   // above its own max (its masses may have underflowed)
 };
 
 struct ResShared {
@@ -381,7 +382,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             r.thc = __int_as_float(wi);
             r.nc = wpi;
             r.bad = bad;
-            r.pad = 0u;
+            r.high = 0u;
             sh.rec[w] = r;
         }
         lds_barrier();
@@ -520,7 +521,11 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             r.thc = 0.0f;
             r.nc = nfin;
             r.bad = (uint32_t)!(z < INFINITY);
-            r.pad = 0u;
+            // the reference only rises during the stream; one set from chunk
+            // 0 far above the wave's values (a penalised logit's raw value,
+            // or 0 for a chunk of -inf) leaves their masses underflowed
+            const float wtop = PEN ? fmaxf(mx, mxp) : mx;
+            r.high = (uint32_t)((wtop > -INFINITY) && (Rz - ceilf(wtop * chi) > 64.0f));
             sh.rec[w] = r;
         }
         uint64_t rst = 0;
@@ -558,7 +563,8 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const double Tincl = rscan16_f64(T);
         const double Z = bcast_f64(Tincl, 15);
         const bool ok = (M > -INFINITY) & (M < INFINITY) & (Z > 0.0) & (Z < INFINITY) &
-                        (__ballot(rv & (rr.bad != 0u)) == 0ull) & (fmaf(M, chi, -rwmin) <= 100.0f);
+                        (__ballot(rv & ((rr.bad | rr.high) != 0u)) == 0ull) &
+                        (fmaf(M, chi, -rwmin) <= 100.0f);
         if (!ok) return NIS_REJECT_NONFINITE;
         if (w == 0 && l < 4) a.rng[4 * (int64_t)row + l] = rst;
         const double u = sh.u0;
@@ -659,7 +665,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             if (a.stats) {
                 // the drawn token's mass against the row max, exactly reduced
                 const double em = exp2(xq * c64 - Mx * c64);
-                const double zM = ldexp(Z, (int)R) * exp2(-Mx * c64);
+                const double zM = Z * exp2((double)R - Mx * c64);  // (R - Mx c within about [0, 1])
                 write_row_stats(a, row, tok, NIS_PATH_DRAW, Mx / temp, zM, 0.0, u,
                                 (u == 0.0) ? 0.0 : em / zM, (uint64_t)nkept, 1);
             }

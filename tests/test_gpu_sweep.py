@@ -1,4 +1,5 @@
-"""Seeded sweep over the whole parameter space of sample() against the oracle.
+"""Seeded sweep over the whole parameter space of sample() against the oracle,
+and the edge cases its runs found.
 
 The other GPU tests pin each kernel route with hand-picked rows.  This one
 draws 48 cases from a fixed seed and crosses what they keep apart: V across
@@ -130,3 +131,87 @@ def test_sweep_case(sampler, i):
     routes = {f"kernel{k}/reject{r}": int(((st["kernel"] == k) & (st["reject"] == r)).sum())
               for k, r in sorted(set(zip(st["kernel"].tolist(), st["reject"].tolist())))}
     print(f"[sweep {i}] routes {routes} -> {rep}", flush=True)
+
+
+@pytest.mark.parametrize("V", [50257, 128256])
+@pytest.mark.parametrize("shift", [-60.0, -200.0])
+def test_rows_far_below_zero_with_masked_runs(sampler, V, shift):
+    # rows whose values all lie far below 0 (a constant shift leaves the
+    # reference's softmax unchanged) with a run of -inf entries: a wave
+    # whose first chunk is all -inf used to keep reference 0, so its masses
+    # underflowed and its fold floor lay above the searched octaves (the
+    # dense and long-row kernels gave wrong kept sets and tokens).  The
+    # dense kernel now takes such a wave's first reference from all of its
+    # chunks; the long-row kernel declines the row to the general path.
+    import nimbus_sampler as ns
+    for blk in ((0, 20000), (20000, 40000), (3000, 3600)):
+        g = np.random.Generator(np.random.PCG64(int(-shift) + blk[0] + V))
+        B = 8
+        x = (g.standard_normal((B, V)) + shift).astype(np.float32)
+        x[:, blk[0]:blk[1]] = -np.inf
+        for T, p, k in ((0.8, 0.9, 0), (0.8, 0.97, 0), (0.8, 1.0, 0), (0.0, 1.0, 0), (0.8, 0.9, 50),
+                        (0.3, 0.5, 0)):
+            params = ns.SamplingParams(temperature=T, top_p=p, top_k=k)
+            print(f"[shifted] V={V} shift={shift} blk={blk} T={T} p={p} k={k}", flush=True)
+            gpu = run_gpu(sampler, x, V, params, list(range(B)))
+            ref = run_oracle(x, V, params, list(range(B)))
+            compare(gpu, ref, greedy=params.greedy())
+
+
+@pytest.mark.parametrize("pen", [1.0, 0.8, 1.5])
+def test_nan_rows_at_top_p_zero(sampler, pen):
+    # top-p <= 0 keeps only max_by's entry (sampler.rs:122-134): a NaN hands
+    # the running maximum to the entry after it, so the kept entry is the
+    # last maximum past the last NaN (or that NaN when it is the last entry),
+    # and a finite one is drawn; NaN then survives nothing else
+    import nimbus_sampler as ns
+    rnd = np.random.Generator(np.random.PCG64(31 + int(pen * 10)))
+    for V in (1000, 50257, 100000):
+        B = 8
+        x = rnd.standard_normal((B, V)).astype(np.float32) * np.float32(2.0)
+        x[0, 5] = np.nan                                   # early NaN, the max before it
+        x[0, 3] = np.float32(50.0)
+        x[1, V - 1] = np.nan                               # NaN last: kept, token 0
+        x[2, [10, V // 2]] = np.nan                        # two NaNs
+        x[3, 0] = np.nan                                   # NaN at index 0
+        x[4, 7] = np.nan
+        x[4, V - 3] = np.inf                               # +inf past the NaN
+        x[5, V // 3] = np.inf
+        x[5, V // 2] = np.nan                              # +inf before the NaN
+        x[6, 100] = np.nan
+        x[6, 101:] = -np.inf                               # only -inf past the NaN
+        x[7, 9] = np.nan
+        x[7, [20, 30, 40]] = np.float32(40.0)              # tied maxima past the NaN
+        gen = [rnd.integers(0, V, size=50) for _ in range(B)] if pen != 1.0 else None
+        ids = off = None
+        if gen is not None:
+            ids, off = _csr([h.astype(np.int64) for h in gen])
+        for T in (0.7, 1.3):
+            params = ns.SamplingParams(temperature=T, top_p=0.0, repetition_penalty=pen)
+            print(f"[nan p=0] V={V} T={T} pen={pen}", flush=True)
+            seeds = list(range(B))
+            gpu = run_gpu(sampler, x, V, params, seeds, ids, off)
+            ref = run_oracle(x, V, params, seeds, ids, off)
+            compare(gpu, ref, greedy=False)
+
+
+def test_penalised_top_p_off_at_low_temperature(sampler):
+    # top-p off with a penalty history at T = 0.06 on a coarse value lattice
+    # (sigma 15): a penalised logit's raw value in a wave's first chunk sat
+    # ~700 octaves above its penalised value, the wave's reference (which
+    # only rises) stayed there and its masses underflowed; such a row is now
+    # declined, and the kept mass statistic no longer overflows at large R
+    import nimbus_sampler as ns
+    rnd = np.random.Generator(np.random.PCG64(74))
+    B, V = 16, 50257
+    x = (np.round(rnd.standard_normal((B, V)) * 15.0 * 4.0) / 4.0).astype(np.float32)
+    order = np.argsort(-x, axis=1, kind="stable")
+    gen = [np.concatenate([order[r, : int(rnd.integers(1, 60))], rnd.integers(0, V, size=600)])
+           .astype(np.int64) for r in range(B)]
+    ids, off = _csr(gen)
+    for T, pen in ((0.062, 1.958), (0.1, 1.5), (0.5, 1.3)):
+        params = ns.SamplingParams(temperature=T, top_p=1.0, repetition_penalty=pen)
+        print(f"[pen low T] T={T} pen={pen}", flush=True)
+        gpu = run_gpu(sampler, x, V, params, list(range(B)), ids, off)
+        ref = run_oracle(x, V, params, list(range(B)), ids, off)
+        compare(gpu, ref, greedy=False)
