@@ -287,16 +287,20 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         const bool anynan = __ballot(rv && (rr.flags & 1u)) != 0ull;
         const float rw0min = -wmax_f32(has ? -rr.rw0 : -INFINITY);
         const float rzmin = -wmax_f32(has ? -rr.rz : -INFINITY);
-        // a wave whose first chunk held nothing above -inf keeps reference 0:
-        // for a row far below 0 its masses may underflow and its fold floor
-        // lie above the searched octaves, so every wave holding data must
-        // have its references at or below R (its fold floor) and within 64
-        // octaves above R (its masses)
+        // a wave whose first chunk held nothing above -inf keeps reference 0,
+        // which may lie far above the wave's values: its fold floor must not
+        // lie above R's searched octaves (every wave holding data has its
+        // first reference at or below R), and a final reference more than 2
+        // octaves above the wave's max costs its masses precision (their f32
+        // arguments' rounding grows with depth) or, past 64 octaves, the
+        // masses themselves: harmless only for a wave whose max lies 20 or
+        // more octaves below R
         const bool hasd = has && rr.mx > -INFINITY;
         const float rw0hi = wmax_f32(hasd ? rr.rw0 : -INFINITY);
-        const float rzhi = wmax_f32(hasd ? rr.rz : -INFINITY);
+        const float cw = ceilf(rr.mx * chi);
+        const bool gapbad = hasd & (rr.rz - cw > 2.0f) & ((R - cw < 20.0f) | (rr.rz - cw > 64.0f));
         const bool ok = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
-                        (rzhi <= R + 64.0f) &
+                        (__ballot(gapbad) == 0ull) &
                         (MODE == kLongTopP ? (R - rw0min < (float)kLSpan) & (rw0hi <= R)
                                            : (R - rzmin <= 100.0f));
         if (!ok) return NIS_REJECT_NONFINITE;

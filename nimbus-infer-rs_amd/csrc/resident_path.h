@@ -85,8 +85,7 @@ struct alignas(16) RRec {
     uint32_t nc;   // top-p off with stats: the wave's elements above -inf (greedy
                    // with a penalty: the first index of that penalised value)
     uint32_t bad;  // the wave saw input this path does not take
-    uint32_t high; // top-p off: the wave's reference ended more than 64 octaves
-                   // above its own max (its masses may have underflowed)
+    uint32_t pad;
 };
 
 struct ResShared {
@@ -382,7 +381,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             r.thc = __int_as_float(wi);
             r.nc = wpi;
             r.bad = bad;
-            r.high = 0u;
+            r.pad = 0u;
             sh.rec[w] = r;
         }
         lds_barrier();
@@ -416,7 +415,21 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
     NIS_RTDECL
     NIS_RTS(0);
     NIS_RFIX(0);
-    const float m0 = wmax_f32(r_max4(xv[0]));
+    float c0m = r_max4(xv[0]);
+    if constexpr (PEN) {
+        // the penalised elements of chunk 0 by their penalised values (rounded
+        // up), so that the reference starts at the wave's values and not
+        // above them (the masses' f32 arguments lose precision with depth)
+        if (pany & 1u) {
+            const uint32_t nb0 = (uint32_t)pnl & 15u;
+            f4v t = xv[0];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if ((nb0 >> q) & 1u) t[q] = pen_f32_up(pen_value(xv[0][q], (double)a.penalty));
+            c0m = r_max4(t);
+        }
+    }
+    const float m0 = wmax_f32(c0m);
     NIS_RTS(1);
     const float Rw = (m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f;
 
@@ -521,11 +534,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             r.thc = 0.0f;
             r.nc = nfin;
             r.bad = (uint32_t)!(z < INFINITY);
-            // the reference only rises during the stream; one set from chunk
-            // 0 far above the wave's values (a penalised logit's raw value,
-            // or 0 for a chunk of -inf) leaves their masses underflowed
-            const float wtop = PEN ? fmaxf(mx, mxp) : mx;
-            r.high = (uint32_t)((wtop > -INFINITY) && (Rz - ceilf(wtop * chi) > 64.0f));
+            r.pad = 0u;
             sh.rec[w] = r;
         }
         uint64_t rst = 0;
@@ -547,8 +556,8 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         float M = wmax_f32(rv ? rr.mx : -INFINITY);
         double Mx = (double)M;
         bool wdata = rv && rr.mx > -INFINITY;  // the wave holds an element above -inf
+        const float pm = (PEN && rv) ? sh.pmx[l] : -INFINITY;
         if constexpr (PEN) {
-            const float pm = rv ? sh.pmx[l] : -INFINITY;
             double py = rv ? sh.pymx[l] : -INFINITY;
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) py = fmax(py, __shfl_xor(py, o));
@@ -562,8 +571,17 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const double T = rv ? ldexp(rr.z, (int)(rr.rw - R)) : 0.0;
         const double Tincl = rscan16_f64(T);
         const double Z = bcast_f64(Tincl, 15);
+        // a wave's reference only rises during the stream: one that ended
+        // more than 2 octaves above the wave's max (set from a chunk 0 of -inf)
+        // costs its masses precision (their f32 arguments' rounding grows with
+        // depth) or, past 64 octaves, the masses themselves; that is
+        // harmless only for a wave whose max lies 20 or more octaves below R
+        const float wtop = rv ? fmaxf(rr.mx, pm) : -INFINITY;
+        const float cw = ceilf(wtop * chi);
+        const bool gapbad = rv & (wtop > -INFINITY) & (rr.rw - cw > 2.0f) &
+                            ((R - cw < 20.0f) | (rr.rw - cw > 64.0f));
         const bool ok = (M > -INFINITY) & (M < INFINITY) & (Z > 0.0) & (Z < INFINITY) &
-                        (__ballot(rv & ((rr.bad | rr.high) != 0u)) == 0ull) &
+                        (__ballot(rv & (rr.bad != 0u)) == 0ull) & (__ballot(gapbad) == 0ull) &
                         (fmaf(M, chi, -rwmin) <= 100.0f);
         if (!ok) return NIS_REJECT_NONFINITE;
         if (w == 0 && l < 4) a.rng[4 * (int64_t)row + l] = rst;

@@ -215,3 +215,20 @@ def test_penalised_top_p_off_at_low_temperature(sampler):
         gpu = run_gpu(sampler, x, V, params, list(range(B)), ids, off)
         ref = run_oracle(x, V, params, list(range(B)), ids, off)
         compare(gpu, ref, greedy=False)
+    # normal rows whose penalised head leads them (sigma 5.4, T 0.126): the
+    # wave reference taken from chunk 0's raw logits sat ~55 octaves above the
+    # penalised values, and the masses' f32 arguments lost ~1e-6 of precision
+    # (the kept mass 2e-6 off); it now starts from the penalised values
+    x2 = (rnd.standard_normal((B, V)) * 5.4).astype(np.float32)
+    order2 = np.argsort(-x2, axis=1, kind="stable")
+    gen2 = [np.concatenate([order2[r, : int(rnd.integers(1, 40))], rnd.integers(0, V, size=400)])
+            .astype(np.int64) for r in range(B)]
+    ids2, off2 = _csr(gen2)
+    for T, pen in ((0.126, 1.3), (0.33, 1.46)):
+        params = ns.SamplingParams(temperature=T, top_p=1.0, repetition_penalty=pen)
+        print(f"[pen head] T={T} pen={pen}", flush=True)
+        gpu = run_gpu(sampler, x2, V, params, list(range(B)), ids2, off2)
+        ref = run_oracle(x2, V, params, list(range(B)), ids2, off2)
+        rep = compare(gpu, ref, greedy=False)
+        assert (gpu[1]["kernel"] == 1).sum() >= B // 2, gpu[1]["kernel"].tolist()  # on the kernel
+        print(f"[pen head] -> {rep}", flush=True)
