@@ -18,10 +18,12 @@
 // octave-relative fixed-point masses fm = floor(2^(x c - floor(j / 64)) 2^24)
 // (derived from e by an exact power-of-two scaling).  Sums of fm are exact
 // integers, so the histogram is the same in any order of the adds.  A wave
-// folds elements more than 64 octaves below its first reference into one
-// floor bucket; the rows where that could alias inside the searched range
-// (the row max more than 64 octaves above a wave's first reference) are
-// declined.
+// folds elements more than 64 octaves below its first reference into that
+// floor octave (one bucket per lane, so -inf entries do not all add to one
+// address); the rows where that could alias inside the searched range (the
+// row max more than 64 octaves above a wave's first reference, or a wave's
+// first reference above the row's) are declined.  A wave whose first chunk
+// holds nothing above -inf takes its first reference from all its chunks.
 //
 // Cutoff without a sort.  The reference keeps sorted position pos iff
 // D(pos) = cum_excl(pos) - q(pos) <= p Z (sampler.rs:147-154); D is
@@ -421,7 +423,12 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
     }
     const float Rw0 = (m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f;
     // elements more than 64 octaves below the first reference share one bucket
-    const float tflo = (Rw0 - (float)kDSpan) * 64.0f;
+    // (each lane's floor is its own bucket of the floor octave, so the adds
+    // of a row's -inf entries are spread over 64 LDS addresses instead of
+    // serialised on one; that octave lies 64 octaves below the wave's first
+    // reference, at or below the bottom of the searched ones, and never
+    // holds the cutoff at top-p < 1)
+    const float tflo = (Rw0 - (float)kDSpan) * 64.0f + (float)l;
     float mx = -INFINITY;   // (PEN: of the plain elements)
     float mxu = -INFINITY;  // PEN: of the penalised values rounded up
     double ymx = -INFINITY; // PEN: of the penalised values

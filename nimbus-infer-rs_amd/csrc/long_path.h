@@ -290,15 +290,15 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         // a wave whose first chunk held nothing above -inf keeps reference 0,
         // which may lie far above the wave's values: its fold floor must not
         // lie above R's searched octaves (every wave holding data has its
-        // first reference at or below R), and a final reference more than 2
+        // first reference at or below R), and a final reference more than 8
         // octaves above the wave's max costs its masses precision (their f32
-        // arguments' rounding grows with depth) or, past 64 octaves, the
-        // masses themselves: harmless only for a wave whose max lies 20 or
-        // more octaves below R
+        // arguments' rounding grows with depth: 8 octaves, 3e-7) or, past 64
+        // octaves, the masses themselves: harmless only for a wave whose max
+        // lies 20 or more octaves below R
         const bool hasd = has && rr.mx > -INFINITY;
         const float rw0hi = wmax_f32(hasd ? rr.rw0 : -INFINITY);
         const float cw = ceilf(rr.mx * chi);
-        const bool gapbad = hasd & (rr.rz - cw > 2.0f) & ((R - cw < 20.0f) | (rr.rz - cw > 64.0f));
+        const bool gapbad = hasd & (rr.rz - cw > 8.0f) & ((R - cw < 20.0f) | (rr.rz - cw > 64.0f));
         const bool ok = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
                         (__ballot(gapbad) == 0ull) &
                         (MODE == kLongTopP ? (R - rw0min < (float)kLSpan) & (rw0hi <= R)

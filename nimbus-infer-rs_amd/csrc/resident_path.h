@@ -429,7 +429,43 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             c0m = r_max4(t);
         }
     }
-    const float m0 = wmax_f32(c0m);
+    float m0 = wmax_f32(c0m);
+    if (m0 == -INFINITY && Kw > 1) {
+        // chunk 0 holds nothing above -inf (a masked stretch): the first
+        // reference comes from the wave's other chunks (without a penalty,
+        // all of them, their loads issued now and again by the stream as
+        // usual; with one, the chunks already in flight, which keeps the
+        // penalised form within its registers).  A wave still empty there
+        // keeps 0, and the reference guard at the first barrier declines the
+        // row if that leaves it far above the wave's values.
+        constexpr int KREF = PEN ? (kRD < kRN ? kRD : kRN) : kRN;
+        if constexpr (!PEN) {
+#pragma unroll
+            for (int k = kRD; k < kRN; ++k) NIS_RLOAD(k);
+        }
+        float mw = -INFINITY;
+#pragma unroll
+        for (int k = 1; k < KREF; ++k) {
+            if (k < Kw) {
+                f4v t = xv[k];
+                if (edge_wave) {
+                    const int fb0 = wbase + k * 64;
+                    if (fb0 < f_lo || fb0 + 63 > f_hi)
+                        t = fix_slot(t, slot0 + k * 64, f_lo, f_hi, mis, V, h0, h1, h2, t0, t1, t2);
+                }
+                // (penalised elements left out: if one of them is the wave's
+                // max, the stream raises the reference when it meets it)
+                if (PEN && ((pany >> k) & 1u)) {
+                    const uint32_t nbk = (uint32_t)(pnl >> (4 * k)) & 15u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if ((nbk >> q) & 1u) t[q] = -INFINITY;
+                }
+                mw = fmaxf(mw, r_max4(t));
+            }
+        }
+        m0 = wmax_f32(mw);
+    }
     NIS_RTS(1);
     const float Rw = (m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f;
 
@@ -572,13 +608,14 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const double Tincl = rscan16_f64(T);
         const double Z = bcast_f64(Tincl, 15);
         // a wave's reference only rises during the stream: one that ended
-        // more than 2 octaves above the wave's max (set from a chunk 0 of -inf)
-        // costs its masses precision (their f32 arguments' rounding grows with
-        // depth) or, past 64 octaves, the masses themselves; that is
+        // more than 8 octaves above the wave's max would cost its masses
+        // precision (their f32 arguments' rounding grows with depth: 8
+        // octaves, 3e-7) or, past 64 octaves, the masses themselves; that is
         // harmless only for a wave whose max lies 20 or more octaves below R
+        // (the first reference is the wave's own max, so this is a guard)
         const float wtop = rv ? fmaxf(rr.mx, pm) : -INFINITY;
         const float cw = ceilf(wtop * chi);
-        const bool gapbad = rv & (wtop > -INFINITY) & (rr.rw - cw > 2.0f) &
+        const bool gapbad = rv & (wtop > -INFINITY) & (rr.rw - cw > 8.0f) &
                             ((R - cw < 20.0f) | (rr.rw - cw > 64.0f));
         const bool ok = (M > -INFINITY) & (M < INFINITY) & (Z > 0.0) & (Z < INFINITY) &
                         (__ballot(rv & (rr.bad != 0u)) == 0ull) & (__ballot(gapbad) == 0ull) &
