@@ -685,6 +685,22 @@ __device__ __forceinline__ uint32_t sparse_row(const RowArgs a, const int row, W
     } else {
         NIS_SSTREAM(false)
     }
+    // A wave whose sample missed the bulk of its data (a masked stretch over
+    // its first chunks) sets its threshold too deep and overflows its list.
+    // If a higher threshold has been published meanwhile, it lists again
+    // from its registers at that one: still every element at or above the
+    // final x_lo, which is at least the threshold published now.
+    if (nw > (uint32_t)kSE) {  // (wave-uniform)
+        const float tpub = unkey32(sh.kxlo);
+        if (tpub > thl && tpub < INFINITY) {
+            thl = tpub;
+            thx = thl / c - fabsf(thl / c) * 1.0e-6f - 1.0e-30f;
+            nw = 0u;
+#pragma unroll
+            for (int k = 0; k < kSN; ++k)
+                if (k < Kw) NIS_SLIST(k, max4(xv[k]) >= thx)
+        }
+    }
 #undef NIS_SSTREAM
 #undef NIS_SLIST
 #undef NIS_SLOAD
