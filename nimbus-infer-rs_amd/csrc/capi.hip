@@ -207,8 +207,11 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
                            ctx->stream, a);
     } else if (a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f && a.top_p > 0.0f &&
                a.top_p < 0.95f && no_topk) {
-        // a repetition-penalty history: applied inside the sparse path
+        // a repetition-penalty history: applied inside the sparse path; the
+        // rows it declines (long histories) finish on the dense path
         hipLaunchKernelGGL(nis::sample_rows_sparse_pen_kernel, dim3((unsigned)B), dim3(nis::kSB), 0,
+                           ctx->stream, a);
+        hipLaunchKernelGGL(nis::sample_rows_dense_pending_kernel, dim3((unsigned)B), dim3(nis::kDB), 0,
                            ctx->stream, a);
     } else if (a.V >= 256 && a.V <= nis::kSMaxV && a.temperature > 0.0f && a.top_p > 0.0f && !no_topk &&
                (a.penalty == 1.0f || a.gen_ids == nullptr)) {

@@ -47,8 +47,46 @@ __device__ __forceinline__ void sparse_rows_body(const RowArgs& a) {
 __global__ __launch_bounds__(kSB) void sample_rows_sparse_kernel(RowArgs a) {
     sparse_rows_body<false>(a);
 }
+// Sparse top-p rows with a repetition-penalty history.  A row the sparse
+// path declines (most often a long history: more penalised elements in a
+// wave's range than its side lists hold) gets the token kLPending | reason,
+// and sample_rows_dense_pending_kernel, launched after it, finishes exactly
+// those rows (the sparse path has written nothing when it declines).
 __global__ __launch_bounds__(kSB) void sample_rows_sparse_pen_kernel(RowArgs a) {
-    sparse_rows_body<true>(a);
+    __shared__ WideShared sh;
+    const int row = (int)blockIdx.x;
+    if (a.done != nullptr && a.done[row]) return;  // a finished sequence (decode step)
+    asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
+                 "s"(a.penalty), "s"(a.top_k), "s"(a.gen_ids), "s"(a.gen_off));
+    uint32_t reject = NIS_REJECT_SHAPE;
+    if (sparse_eligible<true, false>(a, row)) {
+        reject = sparse_row<true, false>(a, row, sh);
+        if (reject == NIS_REJECT_NONE) return;
+    }
+    if (threadIdx.x == 0) a.tokens[row] = kLPending | reject;
+}
+
+// The rows a penalised sparse launch declined (token kLPending | reason): the
+// dense path, which takes any nucleus and up to 16 penalised elements per
+// lane, then the general path (first 512 lanes) if that declines too.  One
+// 1024-lane workgroup per row; a row not pending costs one token read.
+__global__ __launch_bounds__(kDB) void sample_rows_dense_pending_kernel(RowArgs a) {
+    __shared__ DenseKernelShared sh;
+    const int row = (int)blockIdx.x;
+    if (a.done != nullptr && a.done[row]) return;
+    const uint32_t t = a.tokens[row];
+    if ((t & kLPending) != kLPending) return;
+    asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.temperature), "s"(a.top_p),
+                 "s"(a.penalty), "s"(a.gen_ids), "s"(a.gen_off));
+    __syncthreads();  // (every lane has read the marker before any result overwrites it)
+    uint32_t reject = t & ~kLPending;
+    if (dense_eligible<true>(a, row)) {
+        reject = dense_row<true>(a, row, sh.d);
+        if (reject == NIS_REJECT_NONE) return;
+    }
+    if (threadIdx.x >= kBlock) return;
+    __syncthreads();
+    general_row<1>(a, row, sh.g, reject);
 }
 __global__ __launch_bounds__(kSB) void sample_rows_sparse_topk_kernel(RowArgs a) {
     sparse_rows_body<false, true>(a);

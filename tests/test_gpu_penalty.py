@@ -140,19 +140,28 @@ def test_padded_rows_and_short_vocabularies(sampler):
             assert (gpu[1]["kernel"] == 1).all() and (gpu[1]["reject"] == 0).all(), (V, ld)
 
 
-def test_crowded_histories_fall_back_to_the_general_path(sampler):
-    # more penalised elements in one wave's range than its side list holds:
-    # those rows are declined before anything is written and recomputed by
-    # the general path, with the same result
+def test_crowded_histories_finish_on_the_dense_path(sampler):
+    # more penalised elements in one wave's range than the sparse path's side
+    # lists hold: the sparse launch marks those rows pending before anything
+    # is written, and the pending launch finishes them on the dense path (up
+    # to 16 penalised elements per lane); past that, on the general path
     from nimbus_sampler import workloads
-    B, V = 8, 50257
+    B, V = 9, 50257
     x = workloads.headline(B)
-    gen = [np.arange(0, 3000, 7) if r % 2 else np.arange(40000, 40010) for r in range(B)]
+    gen = []
+    for r in range(B):
+        if r % 3 == 0:
+            gen.append(np.arange(40000, 40010))        # short: the sparse path
+        elif r % 3 == 1:
+            gen.append(np.arange(0, 3000, 7))          # crowded: the dense path
+        else:
+            gen.append(np.arange(0, 4000))             # every element of a lane: general
     gpu, _ = _check(sampler, x, V, _params(temperature=0.8, top_p=0.9, repetition_penalty=1.3),
                     gen, "crowded", on_kernel=False)
     st = gpu[1]
-    assert (st["kernel"][0::2] == 1).all() and (st["reject"][0::2] == 0).all()
-    assert (st["kernel"][1::2] == 2).all()
+    assert (st["kernel"][0::3] == 1).all() and (st["reject"][0::3] == 0).all()
+    assert (st["kernel"][1::3] == 1).all() and (st["reject"][1::3] == 0).all()
+    assert (st["kernel"][2::3] == 2).all()
 
 
 # ---------------------------------------------------------------------------
