@@ -492,6 +492,28 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         }
     };
 
+    // Bounds that skip an element before its key is computed (an f64
+    // division on penalised rows) where it cannot matter: a lower bound on
+    // the value of every element whose key is >= k (unpenalised rows key the
+    // f32 logit, penalised ones the f64 value v / T), and an upper bound on
+    // the value the penalty can give the logit x.
+    auto vlb_of_key = [&](uint64_t k) -> double {
+        if (!SIMPLE && pen) {
+            const double wv = unkey64(k);  // every key >= k has v / T >= wv
+            if (!(wv > -INFINITY) || !(wv < INFINITY)) return -INFINITY;
+            const double b = wv * temp;
+            return b - fabs(b) * 1.0e-12 - 1.0e-300;  // (v / T rounds: a margin)
+        }
+        const float f = unkey32((uint32_t)(k >> 32));
+        return f == f ? (double)f : -INFINITY;
+    };
+    auto vub_of_x = [&](float xr) -> double {
+        const double x = (double)xr;
+        if (SIMPLE || !pen) return x;
+        return x > 0.0 ? x * fmax(1.0, 1.0 / penf) * (1.0 + 1.0e-12)
+                       : x * fmin(1.0, penf) * (1.0 - 1.0e-12);
+    };
+
     // ---- top-k (sampler.rs:103-116): keep keys >= key of the k-th largest
     uint64_t kth = 0;
     const bool topk_on = a.top_k > 0 && a.top_k < (uint64_t)V;
@@ -506,9 +528,14 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                 __syncthreads();
                 if (tid < 256) sh.hcnt[tid] = 0;
                 __syncthreads();
+                // (an element whose value lies below every key of the prefix
+                // cannot be in it)
+                const double vlp = (shift + 8 >= 64) ? -INFINITY : vlb_of_key(prefix << (shift + 8));
                 NIS_G_EACH({
-                    const uint64_t k = keyof(pval(j, xr));
-                    if (in_prefix(k, shift, prefix)) atomicAdd(&sh.hcnt[(k >> shift) & 255], 1u);
+                    if (vub_of_x(xr) >= vlp) {
+                        const uint64_t k = keyof(pval(j, xr));
+                        if (in_prefix(k, shift, prefix)) atomicAdd(&sh.hcnt[(k >> shift) & 255], 1u);
+                    }
                 })
                 __syncthreads();
                 if (w == 0) {
@@ -552,6 +579,9 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             kth = kmax;
         }
     }
+
+    // every element of value below vlb_kth has a key below the k-th's
+    const double vlb_kth = topk_on ? vlb_of_key(kth) : -INFINITY;
 
     // ---- walk chunks: chunk c = elements [c*kGChunk, (c+1)*kGChunk), wave
     // c % kWaves; row e of it is elements c*kGChunk + 64e + (0..63), one per
@@ -766,11 +796,13 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         double zl = 0.0;
         uint64_t diff = 0;
         NIS_G_EACH({
-            const double v = pval(j, xr);
-            const uint64_t k = keyof(v);
-            const bool live = k >= kth;
-            zl += live ? massv(v, xr) : 0.0;
-            diff |= live ? (k ^ kmax) : 0ull;
+            if (vub_of_x(xr) >= vlb_kth) {
+                const double v = pval(j, xr);
+                const uint64_t k = keyof(v);
+                const bool live = k >= kth;
+                zl += live ? massv(v, xr) : 0.0;
+                diff |= live ? (k ^ kmax) : 0ull;
+            }
         })
         z_all = block_sum(zl, sh.dscr);
         const DigitRange dr = digit_range(block_or(diff, sh.uscr));
@@ -787,13 +819,15 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                 }
                 __syncthreads();
                 NIS_G_EACH({
-                    const double v = pval(j, xr);
-                    const uint64_t k = keyof(v);
-                    if (k >= kth && in_prefix(k, shift, prefix)) {
-                        const int d = (int)((k >> shift) & 255);
-                        atomicAdd(&sh.hcnt[d], 1u);
-                        atomicAdd(&sh.hmass[d], (unsigned long long)(massv(v, xr) * kGFix));
-                        atomicMax(&sh.hkey[d], (unsigned long long)k);
+                    if (vub_of_x(xr) >= vlb_kth) {  // (below the k-th: not live)
+                        const double v = pval(j, xr);
+                        const uint64_t k = keyof(v);
+                        if (k >= kth && in_prefix(k, shift, prefix)) {
+                            const int d = (int)((k >> shift) & 255);
+                            atomicAdd(&sh.hcnt[d], 1u);
+                            atomicAdd(&sh.hmass[d], (unsigned long long)(massv(v, xr) * kGFix));
+                            atomicMax(&sh.hkey[d], (unsigned long long)k);
+                        }
                     }
                 })
                 __syncthreads();
@@ -872,8 +906,13 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         for (int e = 0; e < 8; ++e) {
             const int64_t j = cc * kGChunk + 64 * e + l;
             const bool in = j < V;
-            const double v = pval(j, xs[e]);
-            const uint64_t k = keyof(v);
+            // (an element below the k-th's value gets key 0: below kth, not kept)
+            double v = -INFINITY;
+            uint64_t k = 0ull;
+            if (vub_of_x(xs[e]) >= vlb_kth) {
+                v = pval(j, xs[e]);
+                k = keyof(v);
+            }
             bool kp;
             if (mode == 2) kp = (j == ilast);
             else if (k < kth) kp = false;
