@@ -518,10 +518,29 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
     uint64_t kth = 0;
     const bool topk_on = a.top_k > 0 && a.top_k < (uint64_t)V;
     if (topk_on) {
+        // On a penalised row the radix runs on keys of v itself (no division
+        // per element) and its result converts once: w = v / T rounds
+        // monotonically, so the k-th largest w is fl(v_k / T) for the k-th
+        // largest v, ties the division creates included (they compare equal
+        // as w-keys downstream).
+        auto tkey = [&](double v) -> uint64_t {
+            if constexpr (SIMPLE) return keyof(v);
+            else return pen ? key64(v) : keyof(v);
+        };
+        auto vlb_of_tkey = [&](uint64_t k) -> double {
+            if constexpr (!SIMPLE) {
+                if (pen) {
+                    const double v = unkey64(k);  // every key >= k has value >= v
+                    return (v > -INFINITY && v < INFINITY) ? v : -INFINITY;
+                }
+            }
+            return vlb_of_key(k);
+        };
+        const uint64_t tkmax = tkey(M);
         uint64_t diff = 0;
-        NIS_G_EACH({ diff |= keyof(pval(j, xr)) ^ kmax; })
+        NIS_G_EACH({ diff |= tkey(pval(j, xr)) ^ tkmax; })
         const DigitRange dr = digit_range(block_or(diff, sh.uscr));
-        uint64_t prefix = (dr.hi_shift + 8 >= 64) ? 0 : (kmax >> (dr.hi_shift + 8));
+        uint64_t prefix = (dr.hi_shift + 8 >= 64) ? 0 : (tkmax >> (dr.hi_shift + 8));
         uint64_t remaining = a.top_k;
         if (!dr.all_equal) {
             for (int shift = dr.hi_shift; shift >= dr.lo_shift; shift -= 8) {
@@ -530,10 +549,10 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                 __syncthreads();
                 // (an element whose value lies below every key of the prefix
                 // cannot be in it)
-                const double vlp = (shift + 8 >= 64) ? -INFINITY : vlb_of_key(prefix << (shift + 8));
+                const double vlp = (shift + 8 >= 64) ? -INFINITY : vlb_of_tkey(prefix << (shift + 8));
                 NIS_G_EACH({
                     if (vub_of_x(xr) >= vlp) {
-                        const uint64_t k = keyof(pval(j, xr));
+                        const uint64_t k = tkey(pval(j, xr));
                         if (in_prefix(k, shift, prefix)) atomicAdd(&sh.hcnt[(k >> shift) & 255], 1u);
                     }
                 })
@@ -574,9 +593,12 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                 remaining = (uint64_t)sh.bi[1];
             }
             const uint64_t lowmask = (dr.lo_shift == 0) ? 0 : ((1ull << dr.lo_shift) - 1);
-            kth = (prefix << dr.lo_shift) | (kmax & lowmask);
+            kth = (prefix << dr.lo_shift) | (tkmax & lowmask);
         } else {
-            kth = kmax;
+            kth = tkmax;
+        }
+        if constexpr (!SIMPLE) {
+            if (pen) kth = keyof(unkey64(kth));  // the k-th largest w = fl(v_k / T)
         }
     }
 
