@@ -20,10 +20,13 @@
 // integers, so the histogram is the same in any order of the adds.  A wave
 // folds elements more than 64 octaves below its first reference into that
 // floor octave (one bucket per lane, so -inf entries do not all add to one
-// address); the rows where that could alias inside the searched range (the
-// row max more than 64 octaves above a wave's first reference, or a wave's
-// first reference above the row's) are declined.  A wave whose first chunk
-// holds nothing above -inf takes its first reference from all its chunks.
+// address).  A row whose max lies 64 or more octaves above a wave's first
+// reference (that wave's unfolded range would alias into the searched
+// octaves) has its ring built again from the registers after the stream,
+// every floor raised to at least 127 octaves below the row max; a wave's
+// first reference above the row's declines the row.  A wave whose first
+// chunk holds nothing above -inf takes its first reference from all its
+// chunks.
 //
 // Cutoff without a sort.  The reference keeps sorted position pos iff
 // D(pos) = cum_excl(pos) - q(pos) <= p Z (sampler.rs:147-154); D is
@@ -634,7 +637,7 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         // every first reference of a wave holding data, less than 64 octaves
         // above the lowest)
         const bool ok = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
-                        (R - rw0min < (float)kDSpan) & (rw0hi <= R);
+                        (rw0hi <= R);
         if (!ok) {
             NIS_DTFLUSH();
             return NIS_REJECT_NONFINITE;
@@ -642,6 +645,75 @@ __device__ __forceinline__ uint32_t dense_row(const RowArgs a, const int row, Nu
         if (PEN && sh.pover != 0u) {
             NIS_DTFLUSH();
             return NIS_REJECT_CAPACITY;  // a history past the bitmaps, or a crowded lane
+        }
+        if (!(R - rw0min < (float)kDSpan)) {
+            // The row max lies 64 or more octaves above some wave's first
+            // reference (a spike or a head far above that wave's first chunk,
+            // a wave masked whole, a penalty below 1 lifting the head): that
+            // wave's unfolded range reaches below the 128 octaves the ring
+            // holds, and would alias into the searched ones.  The ring is
+            // built again from the registers with every wave's floor at least
+            // 127 octaves below R (its first reference raised to R - 63),
+            // each mass at the wave's final reference; nothing above the
+            // floors changes, and what lies below them is 2^-127 of the max.
+            // (All waves take this branch: R and rw0min are shared.)
+            lds_barrier();  // (every wave has read the values above)
+            {
+                u4v* const rp = reinterpret_cast<u4v*>(&sh.ring[(kDRing / kDB) * tid]);
+#pragma unroll
+                for (int i = 0; i < kDRing / kDB / 2; ++i) rp[i] = u4v{0u, 0u, 0u, 0u};
+            }
+            lds_barrier();
+            const float tfl = (fmaxf(Rw0, R - (float)(kDSpan - 1)) - (float)kDSpan) * 64.0f + (float)l;
+            const int Rs = (int)Rz + 24;
+            auto hadd = [&](float xq) {
+                const float e = r_mass(xq, czh, czl, Rz);
+                const int j = d_flr(d_vmax(xq * chi64, tfl));
+                const uint32_t fm = (uint32_t)__builtin_amdgcn_ldexpf(e, Rs - (j >> 6));
+                __hip_atomic_fetch_add(&sh.ring[j & (kDRing - 1)], (1ull << 48) | fm, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+            };
+#pragma unroll 1
+            for (int k = 0; k < kDN; ++k) {
+                if (k < Kw) {
+                    // (PEN: the penalised elements as -inf here, moved below)
+                    f4v x;
+                    switch (k) {  // (a switch keeps the registers out of scratch)
+                        case 0: x = xv[0]; break;
+                        case 1: x = xv[1]; break;
+                        case 2: x = xv[2]; break;
+                        case 3: x = xv[3]; break;
+                        case 4: x = xv[4]; break;
+                        case 5: x = xv[5]; break;
+                        case 6: x = xv[6]; break;
+                        case 7: x = xv[7]; break;
+                        case 8: x = xv[8]; break;
+                        case 9: x = xv[9]; break;
+                        case 10: x = xv[10]; break;
+                        case 11: x = xv[11]; break;
+                        default: x = xv[12]; break;
+                    }
+                    if (PEN && ((pany >> k) & 1u)) x = d_mask4(x, (uint32_t)(pnl >> (4 * k)) & 15u);
+                    hadd(x.x);
+                    hadd(x.y);
+                    hadd(x.z);
+                    hadd(x.w);
+                }
+            }
+            if constexpr (PEN) {
+                const int jfl = d_flr(tfl);
+                each_pen_x([&](float x, int) {
+                    const double y = pen_value(x, pen);
+                    const float ey = (float)pen_mass(y * c64, Rz);
+                    const int j = d_flr(d_vmax(d_pt(y, chid) * 64.0f, tfl));
+                    const uint32_t fm = (uint32_t)__builtin_amdgcn_ldexpf(ey, Rs - (j >> 6));
+                    __hip_atomic_fetch_add(&sh.ring[j & (kDRing - 1)], (1ull << 48) | fm, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+                    __hip_atomic_fetch_add(&sh.ring[jfl & (kDRing - 1)], 0ull - (1ull << 48),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                });
+            }
+            lds_barrier();
         }
     }
 

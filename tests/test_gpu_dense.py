@@ -74,8 +74,9 @@ def test_lattice_ties_across_refinement_levels(sampler):
 
 def test_masked_vocabulary_and_far_spikes(sampler):
     # -inf (masked) entries, a masked first chunk, and one spike far above the
-    # rest (more than 64 octaves above some waves' first reference: such a
-    # row is declined and the general path produces it)
+    # rest (more than 64 octaves above some waves' first reference: the row
+    # runs again with every first reference raised to 63 octaves below the
+    # row max, and stays on the kernel)
     rnd = np.random.Generator(np.random.PCG64(13))
     B, V = 32, 40000
     x = rnd.standard_normal((B, V), dtype=np.float32) * np.float32(2.0)
@@ -83,8 +84,34 @@ def test_masked_vocabulary_and_far_spikes(sampler):
     x[8:16, :3000] = -np.inf
     x[16:20, rnd.integers(0, V, size=4)] = np.float32(60.0)
     x[20:24, 5] = np.float32(150.0)
-    _check(sampler, x, V, 1.0, 0.96, list(range(B)), label="masked")
-    _check(sampler, x, V, 0.5, 0.999, list(range(B)), label="masked-deep")
+    rep = _check(sampler, x, V, 1.0, 0.96, list(range(B)), label="masked")
+    assert rep["fast_rows"] == B, rep
+    rep = _check(sampler, x, V, 0.5, 0.999, list(range(B)), label="masked-deep")
+    assert rep["fast_rows"] == B, rep
+
+
+@pytest.mark.parametrize("p", [0.95, 0.99])
+def test_far_heads_stay_on_the_kernel(sampler, p):
+    # a head of 2-300 logits 70-80 octaves above the rest (their spread puts
+    # the cutoff inside the head), and rows whose masked waves hold nothing
+    # while the rest lies ~100 octaves above 0: both run again with raised
+    # first references; the lowest waves then fold wholly into their floors
+    rnd = np.random.Generator(np.random.PCG64(int(p * 100) + 17))
+    B, V = 32, 50257
+    x = rnd.standard_normal((B, V), dtype=np.float32) * np.float32(1.5)
+    for r in range(16):
+        n = int(rnd.integers(2, 301))
+        pos = rnd.choice(V, size=n, replace=False)
+        x[r, pos] = (50.0 + rnd.uniform(-3.0, 3.0, size=n)).astype(np.float32)
+    for r in range(16, B):
+        n = int(rnd.integers(V // 4, 3 * V // 4))
+        st = int(rnd.integers(0, V - n))
+        x[r] += np.float32(40.0)
+        x[r, st:st + n] = -np.inf
+    rep = _check(sampler, x, V, 1.0, p, list(range(B)), label=f"far-heads-p{p}")
+    assert rep["fast_rows"] == B, rep
+    rep = _check(sampler, x, V, 0.6, p, list(range(100, 100 + B)), label=f"far-heads-p{p}-T0.6")
+    assert rep["fast_rows"] == B, rep
 
 
 @pytest.mark.parametrize("ld_extra", [0, 1, 2, 3])

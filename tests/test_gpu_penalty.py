@@ -401,8 +401,8 @@ def test_dense_crowded_lane_falls_back_to_the_general_path(sampler):
     assert (st["kernel"][1::2] == 2).all()
 
 
-@pytest.mark.parametrize("pen,T,p,on", [(0.5, 0.3, 0.99, False), (5.0, 1.7, 0.95, True),
-                                        (0.25, 1.0, 0.97, False), (0.8, 0.5, 0.99, True)])
+@pytest.mark.parametrize("pen,T,p,on", [(0.5, 0.3, 0.99, True), (5.0, 1.7, 0.95, True),
+                                        (0.25, 1.0, 0.97, True), (0.8, 0.5, 0.99, True)])
 def test_dense_strong_penalties(sampler, pen, T, p, on):
     # penalties far from 1 at low and high temperature: with penalty < 1 the
     # penalised head rises octaves above the unpenalised max (the wave's
@@ -411,8 +411,9 @@ def test_dense_strong_penalties(sampler, pen, T, p, on):
     # penalty 0.5 and T = 0.3 (and in some rows at 0.25 and T = 1) the head
     # rises more than 64 octaves above a wave's first reference (at T = 0.3
     # a logit of 12 is 58 octaves, its penalised value 115): the histogram
-    # ring cannot span that, so such a row is declined (NIS_REJECT_NONFINITE)
-    # and the general path gives the same answer.
+    # ring cannot span that, so such a row runs a second time with every
+    # first reference raised to 63 octaves below the row max, and stays on
+    # the kernel.
     B, V = 64, 50257
     rnd = np.random.Generator(np.random.PCG64(int(pen * 100) + int(T * 10)))
     x = _rows("normal", B)
