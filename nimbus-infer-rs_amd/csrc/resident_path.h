@@ -591,7 +591,6 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         // rounded up); Mx is the exact row max, for the statistics
         float M = wmax_f32(rv ? rr.mx : -INFINITY);
         double Mx = (double)M;
-        bool wdata = rv && rr.mx > -INFINITY;  // the wave holds an element above -inf
         const float pm = (PEN && rv) ? sh.pmx[l] : -INFINITY;
         if constexpr (PEN) {
             double py = rv ? sh.pymx[l] : -INFINITY;
@@ -599,12 +598,12 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
             for (int o = 32; o >= 1; o >>= 1) py = fmax(py, __shfl_xor(py, o));
             Mx = fmax(Mx, py);
             M = fmaxf(M, wmax_f32(pm));
-            wdata |= rv && pm > -INFINITY;
         }
         const float R = (M > -INFINITY && fabsf(M * chi) < 1e30f) ? ceilf(M * chi) : 0.0f;
-        const float rwmin = -wmax_f32(wdata ? -rr.rw : -INFINITY);
-        // each wave's total in 2^R units (exact power-of-two rescales)
-        const double T = rv ? ldexp(rr.z, (int)(rr.rw - R)) : 0.0;
+        // each wave's total in 2^R units (exact power-of-two rescales; a wave
+        // more than ~1075 octaves below R holds 0 in f64, as its exp(w - max)
+        // does in the reference's, and is never drawn)
+        const double T = rv ? ldexp(rr.z, (int)fmaxf(rr.rw - R, -2048.0f)) : 0.0;
         const double Tincl = rscan16_f64(T);
         const double Z = bcast_f64(Tincl, 15);
         // a wave's reference only rises during the stream: one that ended
@@ -618,8 +617,7 @@ __device__ __forceinline__ uint32_t resident_row(const RowArgs a, const int row,
         const bool gapbad = rv & (wtop > -INFINITY) & (rr.rw - cw > 8.0f) &
                             ((R - cw < 20.0f) | (rr.rw - cw > 64.0f));
         const bool ok = (M > -INFINITY) & (M < INFINITY) & (Z > 0.0) & (Z < INFINITY) &
-                        (__ballot(rv & (rr.bad != 0u)) == 0ull) & (__ballot(gapbad) == 0ull) &
-                        (fmaf(M, chi, -rwmin) <= 100.0f);
+                        (__ballot(rv & (rr.bad != 0u)) == 0ull) & (__ballot(gapbad) == 0ull);
         if (!ok) return NIS_REJECT_NONFINITE;
         if (w == 0 && l < 4) a.rng[4 * (int64_t)row + l] = rst;
         const double u = sh.u0;

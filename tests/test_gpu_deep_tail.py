@@ -95,3 +95,29 @@ def test_deep_tail_probabilities_general_path(sampler, V, T, top_p, lo, hi, B):
     rep["deepest_draw_octaves"] = float(depth.max())
     print(f"[deep-tail general] -> {rep}", flush=True)
     assert drawn_deep >= 4, rep
+
+
+@pytest.mark.parametrize("T", [0.8, 0.6])
+def test_far_heads_top_p_off_on_the_resident_kernel(sampler, T):
+    # top-p off: a forced token (a logit of 100 among N(0, 3) logits, ~170
+    # octaves above the rest) or a head of 2-300 logits near 50; every wave's
+    # total is rescaled to the row max exactly in f64, so such rows stay on
+    # the resident kernel however far below the max the other waves lie
+    import nimbus_sampler as ns
+    rnd = np.random.Generator(np.random.PCG64(int(T * 10) + 41))
+    B, V = 32, 50257
+    x = (rnd.standard_normal((B, V)) * 3.0).astype(np.float32)
+    for r in range(B):
+        if r % 2:
+            x[r, int(rnd.integers(0, V))] = np.float32(100.0)
+        else:
+            n = int(rnd.integers(2, 301))
+            x[r, rnd.choice(V, size=n, replace=False)] = (50.0 + rnd.uniform(-3.0, 3.0, size=n)).astype(np.float32)
+    params = ns.SamplingParams(temperature=T, top_p=1.0)
+    seeds = list(range(500, 500 + B))
+    print(f"[far-heads] resident B={B} V={V} T={T}", flush=True)
+    gpu = run_gpu(sampler, x, V, params, seeds)
+    rep = compare(gpu, run_oracle(x, V, params, seeds), greedy=False)
+    print(f"[far-heads] -> {rep}", flush=True)
+    st = gpu[1]
+    assert ((st["kernel"] == 1) & (st["reject"] == 0)).all(), (st["kernel"].tolist(), st["reject"].tolist())
