@@ -286,7 +286,6 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
     {
         const bool anynan = __ballot(rv && (rr.flags & 1u)) != 0ull;
         const float rw0min = -wmax_f32(has ? -rr.rw0 : -INFINITY);
-        const float rzmin = -wmax_f32(has ? -rr.rz : -INFINITY);
         // a wave whose first chunk held nothing above -inf keeps reference 0,
         // which may lie far above the wave's values: its fold floor must not
         // lie above R's searched octaves (every wave holding data has its
@@ -301,8 +300,7 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         const bool gapbad = hasd & (rr.rz - cw > 8.0f) & ((R - cw < 20.0f) | (rr.rz - cw > 64.0f));
         const bool ok = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
                         (__ballot(gapbad) == 0ull) &
-                        (MODE == kLongTopP ? (R - rw0min < (float)kLSpan) & (rw0hi <= R)
-                                           : (R - rzmin <= 100.0f));
+                        (MODE != kLongTopP || ((R - rw0min < (float)kLSpan) & (rw0hi <= R)));
         if (!ok) return NIS_REJECT_NONFINITE;
     }
 
@@ -339,6 +337,9 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
     // =====================================================================
     if constexpr (MODE == kLongAll) {
         // ---- top-p off: every element kept ----------------------------------
+        // (each wave's total rescaled exactly in f64, however far below R the
+        // wave lies: one ~1075 octaves down holds 0, as exp(w - max) does in
+        // the reference's f64)
         const double T = rv ? ldexp(sh.tw[l], (int)(rr.rz - R)) : 0.0;  // 2^R units
         const double Tincl = rscan16_f64(T);
         const double Z = bcast_f64(Tincl, 15);

@@ -186,3 +186,22 @@ def test_long_masked_and_non_finite(sampler):
         ref = run_oracle(x[6:8], V, params, [6, 7])
         assert np.array_equal(gpu[0], ref[0]), (T, p, gpu[0], ref[0])
         assert np.array_equal(gpu[2], ref[2])
+
+
+def test_long_far_heads_top_p_off(sampler):
+    # top-p off at V = 128256: a forced token (a logit of 100 among N(0, 3)
+    # logits) and rows with a masked half under logits near +40 at T = 0.6;
+    # each wave's total is rescaled exactly in f64, so however far below the
+    # max a wave lies the rows stay on the long-row kernel
+    rnd = np.random.Generator(np.random.PCG64(61))
+    B, V = 16, 128256
+    x = (rnd.standard_normal((B, V)) * 3.0).astype(np.float32)
+    for r in range(B):
+        if r % 2:
+            x[r, int(rnd.integers(0, V))] = np.float32(100.0)
+        else:
+            x[r] += np.float32(40.0)
+            x[r, V // 4: 3 * V // 4] = -np.inf
+    for T in (0.8, 0.6):
+        rep = _check(sampler, x, V, T, 1.0, list(range(900, 900 + B)), label=f"far-heads-T{T}")
+        assert rep["fast_rows"] == B, rep
