@@ -814,6 +814,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             __syncthreads();
         }
     }
+    double vlb_p = -INFINITY;  // (top-p on the general form) no element below it is kept
     if (topp_on && !topp_done) {
         double zl = 0.0;
         uint64_t diff = 0;
@@ -829,6 +830,21 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
         z_all = block_sum(zl, sh.dscr);
         const DigitRange dr = digit_range(block_or(diff, sh.uscr));
         const double pZ = (double)p * z_all;
+        // sampler.rs:150 removes an element of mass m, whatever the others,
+        // once (V + 1) m < (1 - p) Z: the mass at or below it and its own are
+        // then less than (1 - p) Z, so the mass before it exceeds p Z plus its
+        // own.  Every element whose value lies below vlb_p (a 16-fold margin
+        // on that mass) is removed, and the passes below skip it before its
+        // key is computed (on a penalised row of N(0, 3) logits at T 0.8 and
+        // p 0.9, ~90 % of the row).
+        {
+            const double mrel = (1.0 - (double)p) * z_all * rho / (16.0 * (double)V);
+            if (mrel > 0.0 && mrel < 1.0 && M_w > -INFINITY && M_w < INFINITY) {
+                const double b = temp * (M_w + log(mrel));
+                vlb_p = b - fabs(b) * 1.0e-12 - 1.0e-300;
+            }
+        }
+        const double vlb = fmax(vlb_kth, vlb_p);
         uint64_t prefix = (dr.hi_shift + 8 >= 64) ? 0 : (kmax >> (dr.hi_shift + 8));
         double G = 0.0;
         if (!dr.all_equal) {
@@ -841,7 +857,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
                 }
                 __syncthreads();
                 NIS_G_EACH({
-                    if (vub_of_x(xr) >= vlb_kth) {  // (below the k-th: not live)
+                    if (vub_of_x(xr) >= vlb) {  // (below the k-th: not live; below vlb_p: removed)
                         const double v = pval(j, xr);
                         const uint64_t k = keyof(v);
                         if (k >= kth && in_prefix(k, shift, prefix)) {
@@ -901,7 +917,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int64_t j = cc * kGChunk + 64 * e + l;
-                tl += (j < V && keyof(pval(j, xs[e])) == kstar) ? 1u : 0u;
+                tl += (j < V && vub_of_x(xs[e]) >= vlb_p && keyof(pval(j, xs[e])) == kstar) ? 1u : 0u;
             }
             const uint32_t tc = wsum_u32(tl);
             if (l == 0) sh.tcnt[cc] = tc;
@@ -931,7 +947,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             // (an element below the k-th's value gets key 0: below kth, not kept)
             double v = -INFINITY;
             uint64_t k = 0ull;
-            if (vub_of_x(xs[e]) >= vlb_kth) {
+            if (vub_of_x(xs[e]) >= vlb_kth && (mode != 1 || vub_of_x(xs[e]) >= vlb_p)) {
                 v = pval(j, xs[e]);
                 k = keyof(v);
             }
