@@ -88,9 +88,18 @@ __device__ __forceinline__ bool long_eligible(const RowArgs a, int row) {
 // workgroup) why the general path must recompute it; nothing has been
 // written then.  `prior`: why the single-read path (long_sparse_path.h)
 // declined the row, when this runs after it (reported in the row's stats).
+//
+// Top-p: a row whose max lies kLSpan or more octaves above a wave's first
+// reference (a forced token, a masked wave under high logits) would alias in
+// the ring.  With `rnext` given, such a row returns kLSpanRetry and *rnext =
+// R - (kLSpan - 1); run again with rfloor = *rnext (every first reference
+// raised to at least that), it fits.
+constexpr uint32_t kLSpanRetry = 0x200u;  // (internal: never reported)
+constexpr uint32_t kLSpanFlag = 0x40000u; // pending token: retry with rfloor in the low 14 bits (+8192)
 template <int MODE>
 __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, LongShared& sh,
-                                             uint32_t prior = NIS_REJECT_NONE) {
+                                             uint32_t prior = NIS_REJECT_NONE, const float rfloor = -INFINITY,
+                                             float* const rnext = nullptr) {
     const int l = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const int tid = (int)threadIdx.x;
@@ -206,7 +215,7 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
 
     // ---- stream -----------------------------------------------------------
     const float m0 = wmax_f32(r_max4(fixc(buf[0], 0)));
-    const float Rw0 = (m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f;
+    const float Rw0 = fmaxf((m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f, rfloor);
     const float tflo = (Rw0 - (float)kLSpan) * 64.0f;  // deeper elements share one bucket
     float Rz = Rw0;
     float mx = -INFINITY;
@@ -297,11 +306,20 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         const bool hasd = has && rr.mx > -INFINITY;
         const float rw0hi = wmax_f32(hasd ? rr.rw0 : -INFINITY);
         const float cw = ceilf(rr.mx * chi);
-        const bool gapbad = hasd & (rr.rz - cw > 8.0f) & ((R - cw < 20.0f) | (rr.rz - cw > 64.0f));
-        const bool ok = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
-                        (__ballot(gapbad) == 0ull) &
-                        (MODE != kLongTopP || ((R - rw0min < (float)kLSpan) & (rw0hi <= R)));
-        if (!ok) return NIS_REJECT_NONFINITE;
+        // (with raised first references a wave lying 64 or more octaves below
+        // its reference lies as far below R: its masses are 2^-64 of the max)
+        const bool gapbad = hasd & (rr.rz - cw > 8.0f) &
+                            ((R - cw < 20.0f) | ((rfloor == -INFINITY) & (rr.rz - cw > 64.0f)));
+        const bool fin = (M > -INFINITY) & (M < INFINITY) & !anynan & (fabsf(M * chi) < 4096.0f) &
+                         (__ballot(gapbad) == 0ull) & (MODE != kLongTopP || (rw0hi <= R));
+        if (!fin) return NIS_REJECT_NONFINITE;
+        if (MODE == kLongTopP && !(R - rw0min < (float)kLSpan)) {
+            if (rnext != nullptr && rfloor == -INFINITY) {
+                *rnext = R - (float)(kLSpan - 1);
+                return kLSpanRetry;
+            }
+            return NIS_REJECT_NONFINITE;
+        }
     }
 
     // the walk's last step: the drawn element of float4 x4 (row index i0 of
@@ -754,8 +772,11 @@ __global__ __launch_bounds__(kLB, 2) void sample_rows_long_kernel(RowArgs a) {
                  "s"(a.penalty), "s"(a.gen_ids), "s"(a.gen_off));
     uint32_t reject = NIS_REJECT_SHAPE;
     if (long_eligible<MODE>(a, row)) {
-        reject = long_row<MODE>(a, row, sh);
+        float rn = 0.0f;
+        reject = long_row<MODE>(a, row, sh, NIS_REJECT_NONE, -INFINITY, MODE == kLongTopP ? &rn : nullptr);
         if (reject == NIS_REJECT_NONE) return;
+        // (|R| < 4096: the retry's floor fits the token's low 14 bits)
+        if (reject == kLSpanRetry) reject = kLSpanFlag | ((uint32_t)((int)rn + 8192) & 0x3FFFu);
     }
     if (threadIdx.x == 0) a.tokens[row] = kLPending | reject;
 }
@@ -764,13 +785,29 @@ __global__ __launch_bounds__(kLB, 2) void sample_rows_long_kernel(RowArgs a) {
 // kLPending | reason).  At most one workgroup per CU, each stepping over the
 // rows with the grid's stride, so a launch with nothing pending costs one
 // token read per row.
+// A top-p row declined for its span alone (kLSpanFlag) runs the long-row
+// method once more first, with every first reference raised to the floor
+// the token carries.
+union PendingShared {
+    GeneralShared g;
+    LongShared l;
+};
 __global__ __launch_bounds__(kBlock) void sample_rows_pending_kernel(RowArgs a, int32_t B) {
-    __shared__ GeneralShared sh;
+    __shared__ PendingShared sh;
     for (int row = (int)blockIdx.x; row < B; row += (int)gridDim.x) {
         if (a.done != nullptr && a.done[row]) continue;
         const uint32_t t = a.tokens[row];
         if ((t & kLPending) != kLPending) continue;
-        general_row<1>(a, row, sh, t & ~kLPending);
+        uint32_t reason = t & ~kLPending;
+        __syncthreads();  // (every lane has read the marker before a result overwrites it)
+        if (reason & kLSpanFlag) {
+            const float rfl = (float)((int)(reason & 0x3FFFu) - 8192);
+            const uint32_t rj = long_row<kLongTopP>(a, row, sh.l, NIS_REJECT_NONE, rfl, nullptr);
+            __syncthreads();  // (every wave has left it before the shared state is used again)
+            if (rj == NIS_REJECT_NONE) continue;
+            reason = rj;
+        }
+        general_row<1>(a, row, sh.g, reason);
         __syncthreads();  // (the next row reuses the shared state)
     }
 }

@@ -205,3 +205,24 @@ def test_long_far_heads_top_p_off(sampler):
     for T in (0.8, 0.6):
         rep = _check(sampler, x, V, T, 1.0, list(range(900, 900 + B)), label=f"far-heads-T{T}")
         assert rep["fast_rows"] == B, rep
+
+
+@pytest.mark.parametrize("p", [0.95, 0.99])
+def test_long_far_heads_top_p(sampler, p):
+    # top-p >= 0.95 at V = 128256: a forced token (a logit of 100) or a
+    # masked half under logits near +40 at T = 0.6 puts the row max 32 or
+    # more octaves above some wave's first reference; the long-row launch
+    # declines the row for that alone, and the pending launch runs the
+    # long-row method again with every first reference raised to R - 31
+    rnd = np.random.Generator(np.random.PCG64(int(p * 100) + 63))
+    B, V = 16, 128256
+    x = (rnd.standard_normal((B, V)) * 3.0).astype(np.float32)
+    for r in range(B):
+        if r % 2:
+            x[r, int(rnd.integers(0, V))] = np.float32(100.0)
+        else:
+            x[r] += np.float32(40.0)
+            x[r, V // 4: 3 * V // 4] = -np.inf
+    for T in (0.8, 0.6):
+        rep = _check(sampler, x, V, T, p, list(range(700, 700 + B)), label=f"far-heads-T{T}-p{p}")
+        assert rep["fast_rows"] == B, rep
