@@ -636,6 +636,7 @@ __device__ __noinline__ bool general_row_t(const RowArgs a, const int row, Gener
             };
             double zl = 0.0;
             NIS_G_EACH({
+                (void)j;  // (the bin needs the value only)
                 const float t = tpos(xr);
                 uint32_t fm;
                 int me;

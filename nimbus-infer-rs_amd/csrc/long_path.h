@@ -42,6 +42,7 @@ constexpr uint32_t kLPending = 0xFFF00000u;  // token of a declined row (| rejec
 constexpr int kLMem = 2048;           // members of the cutoff bucket listed by the second read
 
 enum { kLongTopP = 0, kLongAll = 1, kLongGreedy = 2 };
+constexpr int kLPenMaxV = kLRing * 64 - 64;  // greedy with a penalty history: the bitmap's reach
 
 // A member of the cutoff bucket, listed by the second read.
 struct LMem {
@@ -62,7 +63,7 @@ struct LongShared {
     double tw[kLW];                   // per-wave kept mass (2^R units)
     double tmem[kLW];                 // per-wave kept mass of listed members (2^R_z units)
     uint32_t nfin[kLW];               // top-p off: each wave's elements above -inf (stats)
-    float gx[kLW];                    // greedy: each wave's max
+    double gx[kLW];                   // greedy: each wave's max (penalised values in f64)
     int32_t gi[kLW];                  //   and the first index holding it
     DCut cut;
     double u0;                        // the draw
@@ -80,7 +81,10 @@ __device__ __forceinline__ bool long_eligible(const RowArgs a, int row) {
         if (MODE == kLongAll ? !(a.top_p >= 1.0f) : !(a.top_p > 0.0f && a.top_p < 1.0f)) return false;
     }
     int64_t g0 = 0, g1 = 0;
-    if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) return false;
+    if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) {
+        // greedy takes the history as a bitmap over the ring's words
+        if (MODE != kLongGreedy || a.V > kLPenMaxV) return false;
+    }
     return true;
 }
 
@@ -165,17 +169,66 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
     // =====================================================================
     if constexpr (MODE == kLongGreedy) {
         // ---- greedy: first index of the maximum (sampler.rs:172-181) ----
+        // A repetition-penalty history (sampler.rs:83-101) becomes a bitmap
+        // of the row's indices over the ring's words (V <= kLPenMaxV); a
+        // float4 holding a penalised element takes its f64 values aside (the
+        // lane's own max and first index) and -inf in their places.
+        int64_t g0 = 0, g1 = 0;
+        const bool pen = a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0;  // (uniform)
+        uint32_t* const pbm = reinterpret_cast<uint32_t*>(&sh.ring[0]);
+        if (pen) {
+            const int nwd = ((int)a.V + 31) / 32 + 1;  // (+1: the window's second word)
+            for (int i = tid; i < nwd; i += kLB) pbm[i] = 0u;
+            lds_barrier();
+            for (int64_t i = g0 + tid; i < g1; i += kLB) {
+                const uint32_t id = a.gen_ids[i];
+                if (id < (uint32_t)a.V) atomicOr(&pbm[id >> 5], 1u << (id & 31));
+            }
+            lds_barrier();
+        }
+        const double penf = (double)a.penalty;
         float bx = -INFINITY;
         int bi = 0x7FFFFFFF;
-        float fs = 0.0f;  // NaN probe
+        double by = -INFINITY;  // the lane's penalised max (above -inf) and its first index
+        int byi = 0x7FFFFFFF;
+        float fs = 0.0f;  // NaN probe (of the logits, penalised ones included)
+        // (two copies of the stream: the plain one keeps the loop of a row
+        // without a history as lean as it was)
+        auto stream = [&](auto PEN_) {
+        constexpr bool PENS = decltype(PEN_)::value;
         for (int k0 = 0; k0 < Kw; k0 += kLD) {
 #pragma unroll
             for (int i = 0; i < kLD; ++i) {
                 const int k = k0 + i;
-                const f4v x = fixc(buf[i], k);
+                f4v x = fixc(buf[i], k);
                 buf[i] = ld(k + kLD);
                 if (k < Kw) {
                     fs += (x.x + x.y) + (x.z + x.w);
+                    if constexpr (PENS) {
+                        // bits of indices i0 .. i0 + 3 (i0 >= -3; indices
+                        // outside the row are -inf here and set no bit)
+                        const int i0 = NIS_LIDX(k);
+                        const int ib = max(i0, 0);
+                        const uint32_t wd = (uint32_t)ib >> 5;
+                        const unsigned long long win =
+                            (unsigned long long)pbm[wd] | ((unsigned long long)pbm[wd + 1] << 32);
+                        uint32_t nb = (uint32_t)(win >> (ib & 31)) & 15u;
+                        if (i0 < 0) nb = (nb << (-i0)) & 15u;
+                        if (nb) {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                if ((nb >> q) & 1u) {
+                                    const double y = pen_value(elem(x, q), penf);
+                                    if (y > -INFINITY && (y > by || (y == by && i0 + q < byi))) {
+                                        by = y;
+                                        byi = i0 + q;
+                                    }
+                                }
+                            }
+                            x = f4v{(nb & 1u) ? -INFINITY : x.x, (nb & 2u) ? -INFINITY : x.y,
+                                    (nb & 4u) ? -INFINITY : x.z, (nb & 8u) ? -INFINITY : x.w};
+                        }
+                    }
                     const float m4 = r_max4(x);
                     const int q = (x.x == m4) ? 0 : ((x.y == m4) ? 1 : ((x.z == m4) ? 2 : 3));
                     const bool up = m4 > bx;
@@ -184,8 +237,17 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
                 }
             }
         }
-        const float wm = wmax_f32(bx);
-        const int wi = (int)wmin_u32((uint32_t)((bx == wm) ? bi : 0x7FFFFFFF));
+        };
+        if (pen) stream(std::true_type{});
+        else stream(std::false_type{});
+        // the lane's best in f64 (plain and penalised), the first index at it
+        const double vb = fmax((double)bx, by);
+        const uint32_t ib2 = min((uint32_t)(((double)bx == vb) ? bi : 0x7FFFFFFF),
+                                 (uint32_t)((by == vb) ? byi : 0x7FFFFFFF));
+        double wm = vb;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) wm = fmax(wm, __shfl_xor(wm, o));
+        const int wi = (int)wmin_u32((vb == wm) ? ib2 : 0x7FFFFFFFu);
         const uint32_t bad = (uint32_t)(__ballot(fs != fs) != 0ull);
         if (l == 0) {
             sh.gx[w] = wm;
@@ -193,14 +255,16 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         }
         lds_barrier();
         const bool rv = l < kLW;
-        const float gx = rv ? sh.gx[l] : -INFINITY;
+        const double gx = rv ? sh.gx[l] : -INFINITY;
         const int gi = rv ? sh.gi[l] : 0x7FFFFFFF;
         if (__ballot(rv & (gi < 0))) return NIS_REJECT_NONFINITE;
-        const float M = wmax_f32(gx);
+        double M = gx;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) M = fmax(M, __shfl_xor(M, o));
         int tok = (int)wmin_u32((uint32_t)((rv && gx == M) ? gi : 0x7FFFFFFF));
         if (tok == 0x7FFFFFFF) tok = 0;  // every element -inf: nothing exceeds work[0]
         if (w == 0 && l == 0)
-            write_row_result(a, row, (uint32_t)tok, NIS_PATH_GREEDY, (double)M, 0.0, 0.0, -1.0, 0.0, 0, 1);
+            write_row_result(a, row, (uint32_t)tok, NIS_PATH_GREEDY, M, 0.0, 0.0, -1.0, 0.0, 0, 1);
         return NIS_REJECT_NONE;
     }
 

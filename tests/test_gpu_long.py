@@ -226,3 +226,36 @@ def test_long_far_heads_top_p(sampler, p):
     for T in (0.8, 0.6):
         rep = _check(sampler, x, V, T, p, list(range(700, 700 + B)), label=f"far-heads-T{T}-p{p}")
         assert rep["fast_rows"] == B, rep
+
+
+@pytest.mark.parametrize("V", [60000, 128256, 262080])
+def test_long_greedy_with_penalty_histories(sampler, V):
+    # greedy with a repetition-penalty history past 53245 (the long-row
+    # kernel's greedy mode: the history as a bitmap in LDS, penalised values
+    # compared in f64 beside the f32 max): histories holding each row's top
+    # tokens at penalties above and below 1, ties between a penalised value
+    # and a plain logit, rows of -inf with a history, misaligned rows
+    import nimbus_sampler as ns
+    from parity_util import compare, run_gpu, run_oracle
+    rnd = np.random.Generator(np.random.PCG64(V + 5))
+    B = 16
+    x = (rnd.standard_normal((B, V)) * 3.0).astype(np.float32)
+    order = np.argsort(-x, axis=1, kind="stable")
+    gen = [np.concatenate([order[r, : int(rnd.integers(1, 50))], rnd.integers(0, V + 10, size=60)])
+           for r in range(B)]
+    x[3, :] = -np.inf  # nothing exceeds work[0]: index 0
+    x[4, 10] = np.float32(6.0)
+    x[4, 20] = np.float32(3.0)  # penalised 6.0 / 2 == 3.0: the lower index wins
+    gen[4] = np.array([10, 99], dtype=np.int64)
+    off = np.zeros(B + 1, np.int64)
+    off[1:] = np.cumsum([len(h) for h in gen])
+    ids = np.concatenate(gen).astype(np.uint32)
+    for pen in (2.0, 1.3, 0.5):
+        params = ns.SamplingParams(temperature=0.0, repetition_penalty=pen)
+        for ld in (V, V + 1):
+            print(f"[long] greedy pen={pen} V={V} ld={ld}", flush=True)
+            gpu = run_gpu(sampler, x, V, params, list(range(B)), ids, off, ld=ld)
+            ref = run_oracle(x, V, params, list(range(B)), ids, off)
+            compare(gpu, ref, greedy=True)
+            st = gpu[1]
+            assert ((st["kernel"] == 1) & (st["reject"] == 0)).all(), (st["kernel"].tolist(), st["reject"].tolist())
