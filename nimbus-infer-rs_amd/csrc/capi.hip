@@ -224,7 +224,9 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
         hipLaunchKernelGGL(nis::sample_rows_long_sparse_kernel, dim3((unsigned)B), dim3(nis::kLSB), 0,
                            ctx->stream, a);
     } else if (a.V > nis::kDMaxV &&
-               (a.temperature <= 0.0f || (no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr)))) {
+               (a.temperature <= 0.0f ||
+                (no_topk && (a.penalty == 1.0f || a.gen_ids == nullptr || a.top_p >= 1.0f)))) {
+        // (greedy and top-p off take a penalty history on the long-row kernel)
         if (a.temperature <= 0.0f)
             hipLaunchKernelGGL(nis::sample_rows_long_kernel<nis::kLongGreedy>, dim3((unsigned)B),
                                dim3(nis::kLB), 0, ctx->stream, a);
@@ -234,7 +236,8 @@ int launch_rows(nis_ctx* ctx, const nis::RowArgs& a, int32_t B) {
         else
             hipLaunchKernelGGL(nis::sample_rows_long_kernel<nis::kLongTopP>, dim3((unsigned)B),
                                dim3(nis::kLB), 0, ctx->stream, a);
-        // the rows it declined (penalty history, non-finite, exact-tie overflow)
+        // the rows it declined (penalty history past its reach, non-finite,
+        // exact-tie overflow, a top-p row's span)
         hipLaunchKernelGGL(nis::sample_rows_pending_kernel, dim3((unsigned)std::min(B, 256)),
                            dim3(nis::kBlock), 0, ctx->stream, a, B);
     } else {

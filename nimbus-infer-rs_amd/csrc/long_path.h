@@ -82,8 +82,8 @@ __device__ __forceinline__ bool long_eligible(const RowArgs a, int row) {
     }
     int64_t g0 = 0, g1 = 0;
     if (a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0) {
-        // greedy takes the history as a bitmap over the ring's words
-        if (MODE != kLongGreedy || a.V > kLPenMaxV) return false;
+        // greedy and top-p off take the history as a bitmap over the ring's words
+        if (MODE == kLongTopP || a.V > kLPenMaxV) return false;
     }
     return true;
 }
@@ -166,27 +166,40 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
     uint64_t rsv = 0;
     if (MODE != kLongGreedy && w == 0) rsv = ((gu64p)(a.rng + 4 * (int64_t)row))[l & 3];
 
+    // ---- greedy and top-p off: a repetition-penalty history (sampler.rs:
+    // 83-101) becomes a bitmap of the row's indices over the ring's words
+    // (V <= kLPenMaxV); pnib(i0) is the 4-bit mask of indices i0 .. i0 + 3
+    // (i0 >= -3; indices outside the row are -inf in the stream and set no
+    // bit)
+    int64_t pg0 = 0, pg1 = 0;
+    const bool pen = MODE != kLongTopP && a.penalty != 1.0f && gen_range(a, row, pg0, pg1) &&
+                     pg1 > pg0;  // (uniform)
+    uint32_t* const pbm = reinterpret_cast<uint32_t*>(&sh.ring[0]);
+    if (pen) {
+        const int nwd = ((int)a.V + 31) / 32 + 1;  // (+1: the window's second word)
+        for (int i = tid; i < nwd; i += kLB) pbm[i] = 0u;
+        lds_barrier();
+        for (int64_t i = pg0 + tid; i < pg1; i += kLB) {
+            const uint32_t id = a.gen_ids[i];
+            if (id < (uint32_t)a.V) atomicOr(&pbm[id >> 5], 1u << (id & 31));
+        }
+        lds_barrier();
+    }
+    const double penf = (double)a.penalty;
+    auto pnib = [&](int i0) -> uint32_t {
+        const int ib = max(i0, 0);
+        const uint32_t wd = (uint32_t)ib >> 5;
+        const unsigned long long win = (unsigned long long)pbm[wd] | ((unsigned long long)pbm[wd + 1] << 32);
+        uint32_t nb = (uint32_t)(win >> (ib & 31)) & 15u;
+        if (i0 < 0) nb = (nb << (-i0)) & 15u;
+        return nb;
+    };
+
     // =====================================================================
     if constexpr (MODE == kLongGreedy) {
         // ---- greedy: first index of the maximum (sampler.rs:172-181) ----
-        // A repetition-penalty history (sampler.rs:83-101) becomes a bitmap
-        // of the row's indices over the ring's words (V <= kLPenMaxV); a
-        // float4 holding a penalised element takes its f64 values aside (the
-        // lane's own max and first index) and -inf in their places.
-        int64_t g0 = 0, g1 = 0;
-        const bool pen = a.penalty != 1.0f && gen_range(a, row, g0, g1) && g1 > g0;  // (uniform)
-        uint32_t* const pbm = reinterpret_cast<uint32_t*>(&sh.ring[0]);
-        if (pen) {
-            const int nwd = ((int)a.V + 31) / 32 + 1;  // (+1: the window's second word)
-            for (int i = tid; i < nwd; i += kLB) pbm[i] = 0u;
-            lds_barrier();
-            for (int64_t i = g0 + tid; i < g1; i += kLB) {
-                const uint32_t id = a.gen_ids[i];
-                if (id < (uint32_t)a.V) atomicOr(&pbm[id >> 5], 1u << (id & 31));
-            }
-            lds_barrier();
-        }
-        const double penf = (double)a.penalty;
+        // A float4 holding a penalised element takes its f64 values aside
+        // (the lane's own max and first index) and -inf in their places.
         float bx = -INFINITY;
         int bi = 0x7FFFFFFF;
         double by = -INFINITY;  // the lane's penalised max (above -inf) and its first index
@@ -205,15 +218,8 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
                 if (k < Kw) {
                     fs += (x.x + x.y) + (x.z + x.w);
                     if constexpr (PENS) {
-                        // bits of indices i0 .. i0 + 3 (i0 >= -3; indices
-                        // outside the row are -inf here and set no bit)
                         const int i0 = NIS_LIDX(k);
-                        const int ib = max(i0, 0);
-                        const uint32_t wd = (uint32_t)ib >> 5;
-                        const unsigned long long win =
-                            (unsigned long long)pbm[wd] | ((unsigned long long)pbm[wd + 1] << 32);
-                        uint32_t nb = (uint32_t)(win >> (ib & 31)) & 15u;
-                        if (i0 < 0) nb = (nb << (-i0)) & 15u;
+                        const uint32_t nb = pnib(i0);
                         if (nb) {
 #pragma unroll
                             for (int q = 0; q < 4; ++q) {
@@ -282,9 +288,16 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
     const float Rw0 = fmaxf((m0 > -INFINITY && fabsf(m0 * chi) < 1e30f) ? ceilf(m0 * chi) : 0.0f, rfloor);
     const float tflo = (Rw0 - (float)kLSpan) * 64.0f;  // deeper elements share one bucket
     float Rz = Rw0;
-    float mx = -INFINITY;
+    float mx = -INFINITY;  // (top-p off with a penalty: penalised values rounded up)
+    double mex = -INFINITY; // top-p off with a penalty: the exact max (statistics)
     double z = 0.0;     // the lane's mass total (2^R_z units)
     uint32_t nfin = 0;  // top-p off with stats: elements above -inf (the kept count)
+    // Top-p off with a penalty: the f64 values y of a float4's penalised
+    // elements give the max operand pen_f32_up(y) and the masses
+    // 2^(y c - R_z) in place of their logits'.  (Two copies of the stream:
+    // a row without a history keeps the plain one.)
+    auto sstream = [&](auto PEN_) {
+    constexpr bool PENS = decltype(PEN_)::value && MODE == kLongAll;
     for (int k0 = 0; k0 < Kw; k0 += kLD) {
 #pragma unroll
         for (int i = 0; i < kLD; ++i) {
@@ -292,7 +305,30 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
             const f4v x = fixc(buf[i], k);
             buf[i] = ld(k + kLD);
             if (k < Kw) {
-                const float m4 = r_max4(x);
+                f4v xm = x;
+                uint32_t nb = 0u;
+                double yv[4] = {0.0, 0.0, 0.0, 0.0};
+                if constexpr (PENS) {
+                    nb = pnib(NIS_LIDX(k));
+                    if (nb) {
+                        f4v xp = x;  // the plain elements
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            if ((nb >> q) & 1u) {
+                                yv[q] = pen_value(elem(x, q), penf);
+                                mex = fmax(mex, yv[q]);
+                            }
+                        }
+                        xm = f4v{(nb & 1u) ? pen_f32_up(yv[0]) : x.x, (nb & 2u) ? pen_f32_up(yv[1]) : x.y,
+                                 (nb & 4u) ? pen_f32_up(yv[2]) : x.z, (nb & 8u) ? pen_f32_up(yv[3]) : x.w};
+                        xp = f4v{(nb & 1u) ? -INFINITY : x.x, (nb & 2u) ? -INFINITY : x.y,
+                                 (nb & 4u) ? -INFINITY : x.z, (nb & 8u) ? -INFINITY : x.w};
+                        mex = fmax(mex, (double)r_max4(xp));
+                    } else {
+                        mex = fmax(mex, (double)r_max4(x));
+                    }
+                }
+                const float m4 = r_max4(xm);
                 mx = fmaxf(mx, m4);
                 if (__ballot(m4 * chi > Rz + 1.0f)) {
                     const float Rn = ceilf(wmax_f32(mx) * chi);
@@ -301,8 +337,16 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
                         Rz = Rn;
                     }
                 }
-                const float e0 = r_mass(x.x, czh, czl, Rz), e1 = r_mass(x.y, czh, czl, Rz);
-                const float e2 = r_mass(x.z, czh, czl, Rz), e3 = r_mass(x.w, czh, czl, Rz);
+                float e0 = r_mass(x.x, czh, czl, Rz), e1 = r_mass(x.y, czh, czl, Rz);
+                float e2 = r_mass(x.z, czh, czl, Rz), e3 = r_mass(x.w, czh, czl, Rz);
+                if constexpr (PENS) {
+                    if (nb) {
+                        if (nb & 1u) e0 = (float)pen_mass(yv[0] * c64, Rz);
+                        if (nb & 2u) e1 = (float)pen_mass(yv[1] * c64, Rz);
+                        if (nb & 4u) e2 = (float)pen_mass(yv[2] * c64, Rz);
+                        if (nb & 8u) e3 = (float)pen_mass(yv[3] * c64, Rz);
+                    }
+                }
                 z += (double)((e0 + e1) + (e2 + e3));
                 if (MODE == kLongAll && a.stats)
                     nfin += (uint32_t)(x.x > -INFINITY) + (uint32_t)(x.y > -INFINITY) +
@@ -325,8 +369,23 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
             }
         }
     }
+    };
+    if constexpr (MODE == kLongAll) {
+        if (pen) sstream(std::true_type{});
+        else sstream(std::false_type{});
+    } else {
+        sstream(std::false_type{});
+    }
     NIS_DTS(1);
     mx = wmax_f32(mx);
+    if constexpr (MODE == kLongAll) {
+        // the wave's exact max (statistics): with a penalty, of the plain
+        // logits and the penalised f64 values
+        double me = pen ? mex : (double)mx;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) me = fmax(me, __shfl_xor(me, o));
+        if (l == 0) sh.gx[w] = me;
+    }
     {
         const uint32_t nan_seen = (uint32_t)(__ballot(z != z) != 0ull);
         const double zw = wsum_f64(z);
@@ -389,6 +448,8 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
     // the walk's last step: the drawn element of float4 x4 (row index i0 of
     // element 0, per-element masses ev in the units of r_run), and the row's
     // result
+    double Mst = (double)M;  // the row max for the statistics (top-p off: exact, f64)
+    double vfin[4] = {0.0, 0.0, 0.0, 0.0};  // top-p off: the final float4's values (penalised in f64)
     auto finish = [&](const f4v& x4, uint32_t i0, const float ev[4], double r_run, double Zk,
                       double Zall, uint64_t kept) {
         int q = -1, qlast = 0;
@@ -404,14 +465,14 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         }
         if (q < 0) q = qlast;
         const double u = sh.u0;
-        const float xq = elem(x4, q);
+        const double xq = (MODE == kLongAll) ? vfin[q] : (double)elem(x4, q);
         uint32_t tok = i0 + (uint32_t)q;
         if (u == 0.0) tok = 0u;  // r == 0 stops the reference's walk at index 0
         emit_token(a, row, tok);
         if (a.stats) {
-            const double rho = exp2((double)R - (double)M * c64);  // 2^R units -> max-element units
-            const double em = exp2((double)xq * c64 - (double)M * c64);
-            write_row_stats(a, row, tok, NIS_PATH_DRAW, (double)M / temp, Zk * rho, Zall * rho, u,
+            const double rho = exp2((double)R - Mst * c64);  // 2^R units -> max-element units
+            const double em = exp2(xq * c64 - Mst * c64);
+            write_row_stats(a, row, tok, NIS_PATH_DRAW, Mst / temp, Zk * rho, Zall * rho, u,
                             (u == 0.0) ? 0.0 : em / (Zk * rho), kept, 1, prior);
         }
     };
@@ -432,14 +493,41 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         const uint64_t nzw = __ballot(rv & (T > 0.0));
         const int ws = hw ? (__ffsll((long long)hw) - 1) : (63 - __clzll((long long)(nzw | 1ull)));
         if (w != ws) return NIS_REJECT_NONE;
+        {
+            double me = rv ? sh.gx[l] : -INFINITY;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) me = fmax(me, __shfl_xor(me, o));
+            Mst = me;
+        }
+        // a float4's masses (2^R_z units) and values as the stream took them
+        auto wmass4 = [&](const f4v& x, int k, float ev[4], double vv[4]) {
+            ev[0] = r_mass(x.x, czh, czl, Rz);
+            ev[1] = r_mass(x.y, czh, czl, Rz);
+            ev[2] = r_mass(x.z, czh, czl, Rz);
+            ev[3] = r_mass(x.w, czh, czl, Rz);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) vv[q] = (double)elem(x, q);
+            if (pen) {
+                const uint32_t nb = pnib(NIS_LIDX(k));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if ((nb >> q) & 1u) {
+                        vv[q] = pen_value(elem(x, q), penf);
+                        ev[q] = (float)pen_mass(vv[q] * c64, Rz);
+                    }
+                }
+            }
+        };
         double rk = ldexp(r - bcast_f64(Tincl - T, ws), (int)(R - Rz));  // 2^R_z units
         // this wave's chunks in order until the one holding the crossing (the
         // last with mass if rounding leaves r above every prefix)
         int kc = -1, klast = 0;
         for (int k = 0; k < Kw && kc < 0; ++k) {
             const f4v x = fixc(ld(k), k);
-            const float s4 = (r_mass(x.x, czh, czl, Rz) + r_mass(x.y, czh, czl, Rz)) +
-                             (r_mass(x.z, czh, czl, Rz) + r_mass(x.w, czh, czl, Rz));
+            float e4[4];
+            double v4[4];
+            wmass4(x, k, e4, v4);
+            const float s4 = (e4[0] + e4[1]) + (e4[2] + e4[3]);
             const double ct = wsum_f64((double)s4);
             if (ct > 0.0) {
                 klast = k;
@@ -449,8 +537,8 @@ __device__ __forceinline__ uint32_t long_row(const RowArgs a, const int row, Lon
         }
         if (kc < 0) kc = klast;
         const f4v xc = fixc(ld(kc), kc);
-        float ev[4] = {r_mass(xc.x, czh, czl, Rz), r_mass(xc.y, czh, czl, Rz), r_mass(xc.z, czh, czl, Rz),
-                       r_mass(xc.w, czh, czl, Rz)};
+        float ev[4];
+        wmass4(xc, kc, ev, vfin);
         const double sl = (double)((ev[0] + ev[1]) + (ev[2] + ev[3]));
         const double lincl = wscan_f64(sl);
         const uint64_t hl = __ballot((sl > 0.0) & (lincl >= rk));

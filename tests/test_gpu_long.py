@@ -259,3 +259,33 @@ def test_long_greedy_with_penalty_histories(sampler, V):
             compare(gpu, ref, greedy=True)
             st = gpu[1]
             assert ((st["kernel"] == 1) & (st["reject"] == 0)).all(), (st["kernel"].tolist(), st["reject"].tolist())
+
+
+@pytest.mark.parametrize("V", [60000, 128256])
+def test_long_top_p_off_with_penalty_histories(sampler, V):
+    # top-p off with a repetition-penalty history past 53245 (the long-row
+    # kernel's top-p-off mode: penalised values' masses 2^(y c - R_z) from
+    # their f64 values, the max bound from them rounded up): histories of
+    # each row's top tokens at penalties above and below 1, a row whose
+    # penalised head rises far above the rest, misaligned rows
+    import nimbus_sampler as ns
+    from parity_util import compare, run_gpu, run_oracle
+    rnd = np.random.Generator(np.random.PCG64(V + 9))
+    B = 16
+    x = (rnd.standard_normal((B, V)) * 3.0).astype(np.float32)
+    order = np.argsort(-x, axis=1, kind="stable")
+    gen = [np.concatenate([order[r, : int(rnd.integers(1, 50))], rnd.integers(0, V + 10, size=60)])
+           for r in range(B)]
+    off = np.zeros(B + 1, np.int64)
+    off[1:] = np.cumsum([len(h) for h in gen])
+    ids = np.concatenate(gen).astype(np.uint32)
+    for pen, T in ((1.3, 0.8), (2.0, 1.2), (0.5, 0.6)):
+        params = ns.SamplingParams(temperature=T, top_p=1.0, repetition_penalty=pen)
+        for ld in (V, V + 3):
+            print(f"[long] top-p off pen={pen} T={T} V={V} ld={ld}", flush=True)
+            seeds = list(range(40, 40 + B))
+            gpu = run_gpu(sampler, x, V, params, seeds, ids, off, ld=ld)
+            ref = run_oracle(x, V, params, seeds, ids, off)
+            compare(gpu, ref, greedy=False)
+            st = gpu[1]
+            assert ((st["kernel"] == 1) & (st["reject"] == 0)).all(), (st["kernel"].tolist(), st["reject"].tolist())
