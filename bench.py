@@ -500,7 +500,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this sampler build runs on one GPU only (rows are independent; "
-              "row sharding across GPUs is described in DESIGN.md). Use --gpus 1.",
+              "row sharding across GPUs is not built). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 

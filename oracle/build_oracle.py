@@ -5,7 +5,8 @@ with gcc, IEEE f64 semantics: no fast-math and no FMA contraction, so the
 arithmetic follows the reference's operation order.
 
 The reference itself is Rust and this image has no rustc/cargo, so there is
-no oracle/_ref build of it.
+no oracle/_ref build of it; the restatement is pinned by the reference's
+own test vectors and independent checks instead.
 """
 import os
 import subprocess

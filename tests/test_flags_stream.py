@@ -59,7 +59,7 @@ def test_generate_defaults_and_seed_rules():
 
 def test_f32_parse_is_correctly_rounded():
     from nimbus_sampler.flags import FlagError, parse_f32
-    # values the survey records for the configs' f32 fields
+    # the f32 values of the configs' temperature and top-p fields
     for text, val in [("0.7", 0.699999988079071), ("0.8", 0.800000011920929),
                       ("0.9", 0.8999999761581421), ("0.95", 0.949999988079071),
                       ("0.99", 0.9900000095367432), ("1.3", 1.2999999523162842)]:

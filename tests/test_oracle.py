@@ -60,9 +60,9 @@ def test_rng_matches_python_bigint_kats(oracle_mod):
         assert oracle_mod.Rng(int(k["seed"])).next_f64() == float(k["first_f64"])
 
 
-def test_rng_matches_survey_appendix_values(oracle_mod):
-    # Values computed independently (a separate big-int restatement made
-    # while surveying the reference).
+def test_rng_matches_independent_values(oracle_mod):
+    # Values computed independently (a separate big-int restatement of
+    # SplitMix64 seeding and xoshiro256++, not this oracle's code).
     table = {
         0: (0x6E789E6AA1B965F4, 0x58F24F57E97E3F07, 0.34744735618868894),
         1: (0xBEEB8DA1658EEC67, 0xFC06D5F275A73FD8, 0.9844793049757329),
